@@ -1,0 +1,231 @@
+"""CPU oracle for the JPEG AI synthesis hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import this package, and only as the checker. The product library (``zenjpegai_amd``) never
+imports, links or calls anything here.
+
+Layer primitives are the C++ loops in ``oracle.cpp`` (restating the reference's
+``src/nn/reference.rs`` and ``src/nn/fast/math.rs``); graph-level functions live in
+``oracle.graphs`` and the integer tiling geometry in ``oracle.geometry``. Tensors are numpy
+float32 arrays, planar ``[c, h, w]`` like the reference's ``Tensor<f32>``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+
+
+def build() -> None:
+    """Compile ``liboracle.so`` from ``oracle.cpp`` (gcc)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.or_conv2d.restype = ctypes.c_int
+        L.or_conv2d.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p,
+                                ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32p, _f32p]
+        L.or_conv_transpose2d.restype = ctypes.c_int
+        L.or_conv_transpose2d.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p,
+                                          _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int, _f32p]
+        L.or_pixel_shuffle.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int, _f32p]
+        for name in ("or_relu", "or_relu6", "or_leaky_relu", "or_denormalize", "or_exp_slice",
+                     "or_sigmoid"):
+            getattr(L, name).argtypes = [_f32p, ctypes.c_long]
+        for name in ("or_add", "or_gate", "or_mul", "or_elu_gate"):
+            getattr(L, name).argtypes = [_f32p, _f32p, ctypes.c_long]
+        L.or_exp.restype = ctypes.c_float
+        L.or_exp.argtypes = [ctypes.c_float]
+        L.or_layer_norm_channels.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             _f32p, _f32p]
+        L.or_dot8.restype = ctypes.c_double
+        L.or_dot8.argtypes = [_f32p, _f32p, ctypes.c_long]
+        L.or_channel_attention.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_int, _f32p, _f32p, _f32p]
+        L.or_quantize_plane.argtypes = [_f32p, ctypes.c_long, ctypes.c_int, _u16p]
+        L.or_f32_to_f16.restype = ctypes.c_uint16
+        L.or_f32_to_f16.argtypes = [ctypes.c_float]
+        L.or_f16_to_f32.restype = ctypes.c_float
+        L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.or_f16_round_trip.argtypes = [_f32p, ctypes.c_long, _f32p]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_f32p)
+
+
+def _c(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class OracleError(ValueError):
+    pass
+
+
+def conv2d(x, weight, bias, stride=1, pad=(0, 0), groups=1, extra_pad=(0, 0, 0, 0)):
+    """``reference::conv2d`` (src/nn/reference.rs:103-133) with the optional
+    ``ConvLayer::with_extra_pad`` border (src/nn/fast/layers.rs:36)."""
+    x, weight = _c(x), _c(weight)
+    c, h, w = x.shape
+    out_ch, _icg, kh, kw = weight.shape
+    ih, iw = h + extra_pad[0] + extra_pad[2], w + extra_pad[1] + extra_pad[3]
+    oh = (ih + 2 * pad[0] - kh) // stride + 1
+    ow = (iw + 2 * pad[1] - kw) // stride + 1
+    y = np.empty((out_ch, oh, ow), np.float32)
+    b = _c(bias) if bias is not None else None
+    ext = (ctypes.c_int * 4)(*extra_pad)
+    rc = lib().or_conv2d(_p(x), c, h, w, _p(weight), _p(b) if b is not None else None, out_ch,
+                         kh, kw, stride, pad[0], pad[1], groups, ext, _p(y))
+    if rc:
+        raise OracleError("conv2d: inconsistent geometry")
+    return y
+
+
+def conv_transpose2d(x, weight, bias, stride, pad, out_pad):
+    """``reference::conv_transpose2d`` (src/nn/reference.rs:206-236); weight [in][out][k][k]."""
+    x, weight = _c(x), _c(weight)
+    c, h, w = x.shape
+    _, out_ch, k, _ = weight.shape
+    oh = (h - 1) * stride + k + out_pad - 2 * pad
+    ow = (w - 1) * stride + k + out_pad - 2 * pad
+    y = np.empty((out_ch, oh, ow), np.float32)
+    b = _c(bias) if bias is not None else None
+    rc = lib().or_conv_transpose2d(_p(x), c, h, w, _p(weight), _p(b) if b is not None else None,
+                                   out_ch, k, stride, pad, out_pad, _p(y))
+    if rc:
+        raise OracleError("conv_transpose2d: unsupported geometry")
+    return y
+
+
+def pixel_shuffle(x, r):
+    x = _c(x)
+    c, h, w = x.shape
+    if c % (r * r):
+        raise OracleError("pixel_shuffle: channels not divisible by r^2")
+    y = np.empty((c // (r * r), h * r, w * r), np.float32)
+    lib().or_pixel_shuffle(_p(x), c, h, w, r, _p(y))
+    return y
+
+
+def _unary(name, x):
+    y = _c(x).copy()
+    getattr(lib(), name)(_p(y), y.size)
+    return y
+
+
+def _binary(name, a, b):
+    y = _c(a).copy()
+    b = _c(b)
+    assert b.shape == y.shape
+    getattr(lib(), name)(_p(y), _p(b), y.size)
+    return y
+
+
+def relu(x):
+    return _unary("or_relu", x)
+
+
+def relu6(x):
+    return _unary("or_relu6", x)
+
+
+def leaky_relu(x):
+    return _unary("or_leaky_relu", x)
+
+
+def denormalize(x):
+    return _unary("or_denormalize", x)
+
+
+def exp(x):
+    return _unary("or_exp_slice", x)
+
+
+def sigmoid(x):
+    return _unary("or_sigmoid", x)
+
+
+def add(a, b):
+    return _binary("or_add", a, b)
+
+
+def gate(x, mask):
+    """``x * (1 + mask)`` (src/nn/fast/layers.rs:195-201)."""
+    return _binary("or_gate", x, mask)
+
+
+def mul(a, b):
+    return _binary("or_mul", a, b)
+
+
+def elu_gate(a, b):
+    return _binary("or_elu_gate", a, b)
+
+
+def layer_norm_channels(x, weight, bias):
+    y = _c(x).copy()
+    c, h, w = y.shape
+    lib().or_layer_norm_channels(_p(y), c, h, w, _p(_c(weight)), _p(_c(bias)))
+    return y
+
+
+def dot8(a, b):
+    a, b = _c(a).ravel(), _c(b).ravel()
+    return lib().or_dot8(_p(a), _p(b), a.size)
+
+
+def channel_attention(qkv, heads, temperature, return_attn=False):
+    qkv = _c(qkv)
+    c3, h, w = qkv.shape
+    dim = c3 // 3
+    out = np.empty((dim, h, w), np.float32)
+    attn = np.empty((dim, dim // heads), np.float32)
+    rc = lib().or_channel_attention(_p(qkv), c3, h, w, heads, _p(_c(temperature)), _p(out),
+                                    _p(attn))
+    if rc:
+        raise OracleError("attention: channel / head counts")
+    return (out, attn) if return_attn else out
+
+
+def quantize_plane(x, bit_depth):
+    x = _c(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_quantize_plane(_p(x), x.size, bit_depth, out.ctypes.data_as(_u16p))
+    return out
+
+
+def f32_to_f16_bits(v: float) -> int:
+    return lib().or_f32_to_f16(v)
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return lib().or_f16_to_f32(h)
+
+
+def f16_round_trip(x):
+    x = _c(x)
+    y = np.empty_like(x)
+    lib().or_f16_round_trip(_p(x), x.size, _p(y))
+    return y

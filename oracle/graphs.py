@@ -1,0 +1,219 @@
+"""Graph-level oracle: the synthesis transforms as compositions of the oracle layer loops.
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+Each function restates one forward of the reference's ``src/model/synthesis.rs`` /
+``src/model/attention.rs`` op by op; ``p`` maps checkpoint names to numpy arrays (the layouts of
+``fuzz/fuzz_targets/common.rs:152-345``). Planar ``[c, h, w]`` float32 throughout.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import (add, channel_attention, conv2d, conv_transpose2d, denormalize, elu_gate, gate,
+               layer_norm_channels, mul, pixel_shuffle, quantize_plane, relu, relu6, sigmoid)
+
+
+def _ceil(a, b):
+    return -(-a // b)
+
+
+def crop(x, h, w):
+    """``BTensor::crop_par``: top-left ``h x w`` corner (src/nn/fast/tensor.rs:349-367)."""
+    if h > x.shape[1] or w > x.shape[2]:
+        raise ValueError("crop larger than tensor")
+    return np.ascontiguousarray(x[:, :h, :w])
+
+
+def conv3x3(p, name, x, groups=1, stride=1):
+    """``load::conv3x3`` layer (src/model/load.rs:46): pad 1."""
+    return conv2d(x, p[f"{name}.weight"], p.get(f"{name}.bias"), stride, (1, 1), groups)
+
+
+def conv1x1(p, name, x):
+    return conv2d(x, p[f"{name}.weight"], p.get(f"{name}.bias"), 1, (0, 0), 1)
+
+
+def conv3x3_t(p, name, x):
+    """``attention::conv3x3_t`` (src/model/attention.rs:78-91): k3 s2 p1 op1."""
+    return conv_transpose2d(x, p[f"{name}.weight"], p[f"{name}.bias"], 2, 1, 1)
+
+
+def res_au(p, pfx, x):
+    """``ResAu::forward`` (src/model/synthesis.rs:62-74): x * (1 + conv2(conv(relu6(x))))."""
+    w = p[f"{pfx}.conv.weight"]
+    groups = x.shape[0] // w.shape[1]
+    t = conv2d(relu6(x), w, None, 1, (1, 1), groups)
+    m = conv1x1(p, f"{pfx}.conv2", t)
+    return gate(x, m)
+
+
+def upsample(p, op, pfx, x):
+    """``Upsample::forward`` (src/model/synthesis.rs:117-171)."""
+    if op == "bop":
+        return conv_transpose2d(x, p[f"{pfx}.weight"], p[f"{pfx}.bias"], 2, 1, 0)
+    t = conv2d(x, p[f"{pfx}.conv.weight"], None, 1, (0, 0), 1, extra_pad=(0, 0, 1, 1))
+    return pixel_shuffle(t, 2)
+
+
+def residual_block(p, pfx, x):
+    """``ResidualBlock::forward`` (src/model/attention.rs:35-43)."""
+    t = relu(conv3x3(p, f"{pfx}.conv1", x))
+    return add(conv3x3(p, f"{pfx}.conv2", t), x)
+
+
+def cab(p, pfx, x):
+    """``Cab::forward`` (src/model/attention.rs:119-139): x + trunk(x) * sigmoid(mask(x))."""
+    trunk = residual_block(p, f"{pfx}.residual_trunk.0", x)
+    trunk = residual_block(p, f"{pfx}.residual_trunk.1", trunk)
+    m = conv3x3(p, f"{pfx}.subscale", x, stride=2)
+    m = residual_block(p, f"{pfx}.residual_mask2.0", m)
+    m = residual_block(p, f"{pfx}.residual_mask3.0", m)
+    m = conv3x3_t(p, f"{pfx}.upscale", m)
+    if m.shape != trunk.shape:
+        raise ValueError("CAB: odd feature map size")
+    return add(mul(trunk, sigmoid(m)), x)
+
+
+def transformer_block(p, pfx, x):
+    """``TransformerBlock::forward`` (src/model/attention.rs:328-372), heads 4, hidden 4d."""
+    dim = x.shape[0]
+    hidden = 4 * dim
+    t = layer_norm_channels(x, p[f"{pfx}.prep_data.norm1.weight"], p[f"{pfx}.prep_data.norm1.bias"])
+    t = conv1x1(p, f"{pfx}.prep_data.conv1", t)
+    t = conv2d(t, p[f"{pfx}.prep_data.conv2.weight"], None, 1, (1, 1), t.shape[0])
+    a = channel_attention(t, 4, p[f"{pfx}.attn.temperature"].ravel())
+    a = conv1x1(p, f"{pfx}.attn.project_out", a)
+    x = add(x, a)
+    t = layer_norm_channels(x, p[f"{pfx}.ffn.norm1.weight"], p[f"{pfx}.ffn.norm1.bias"])
+    t = conv1x1(p, f"{pfx}.ffn.project_in", t)
+    t = conv2d(t, p[f"{pfx}.ffn.dwconv.weight"], None, 1, (1, 1), t.shape[0])
+    f = elu_gate(t[:hidden], t[hidden:])
+    f = conv1x1(p, f"{pfx}.ffn.project_out", f)
+    return add(x, f)
+
+
+def tam(p, pfx, x, downsample):
+    """``Tam::forward`` (src/model/attention.rs:528-545)."""
+    if downsample:
+        x = conv3x3(p, f"{pfx}.ds_conv", x, stride=2)
+    x = transformer_block(p, f"{pfx}.TABs.0", x)
+    x = transformer_block(p, f"{pfx}.TABs.1", x)
+    if downsample:
+        x = conv3x3_t(p, f"{pfx}.us_conv", x)
+    return x
+
+
+def light_primary(p, op, y_hat, h, w):
+    """``LightPrimary::forward`` (src/model/synthesis.rs:550-580) -> ``[1, >=h, >=w]``."""
+    x = add(relu(conv3x3(p, "first_stage.0.0.conv1", y_hat)), y_hat)
+    x = upsample(p, op, "first_stage.1", x)
+    x = res_au(p, "first_stage.2", x)
+    x = crop(x, _ceil(h, 8), _ceil(w, 8))
+    x = upsample(p, op, "conv2_t", x)
+    x = crop(x, _ceil(h, 4), _ceil(w, 4))
+    x = res_au(p, "iact2", x)
+    x = conv3x3(p, "conv3", x)
+    x = res_au(p, "iact3", x)
+    x = conv1x1(p, "conv4", x)
+    return denormalize(pixel_shuffle(x, 4))
+
+
+def hop_primary(p, y_hat, h, w):
+    """``HopPrimary::forward`` (src/model/synthesis.rs:356-390)."""
+    x = residual_block(p, "first_stage.0.0", y_hat)
+    x = conv3x3_t(p, "first_stage.1", x)
+    x = res_au(p, "first_stage.2", x)
+    x = crop(x, _ceil(h, 8), _ceil(w, 8))
+    x = conv3x3_t(p, "conv2_t", x)
+    x = cab(p, "CAB", x)
+    x = crop(x, _ceil(h, 4), _ceil(w, 4))
+    x = res_au(p, "iact2", x)
+    x = conv1x1(p, "conv3_t", x)
+    x = pixel_shuffle(x, 2)
+    x = tam(p, "TAM", x, True)
+    x = crop(x, _ceil(h, 2), _ceil(w, 2))
+    x = res_au(p, "iact3", x)
+    x = conv3x3_t(p, "conv4_t", x)
+    return denormalize(x)
+
+
+def primary(p, op, y_hat, h, w):
+    """``SynthesisPrimary::forward`` (src/model/synthesis.rs:262-276)."""
+    if op == "hop":
+        return hop_primary(p, y_hat, h, w)
+    return light_primary(p, op, y_hat, h, w)
+
+
+def secondary(p, op, y_hat_luma, y_hat_chroma, h, w):
+    """``SynthesisSecondary::forward_with`` (src/model/synthesis.rs:1004-1038) with
+    ``LightSecondary``/``HopSecondary`` tails (:884-909, :755-773)."""
+    lh = min(y_hat_luma.shape[1], y_hat_chroma.shape[1])
+    lw = min(y_hat_luma.shape[2], y_hat_chroma.shape[2])
+    if y_hat_chroma.shape[1:] != (lh, lw):
+        raise ValueError("chroma latent larger than the luma latent")
+    x = np.concatenate([crop(y_hat_luma, lh, lw), y_hat_chroma], 0)
+    info = conv3x3(p, "first_stage.conv1", x)
+    x = np.concatenate([info, y_hat_chroma], 0)
+    if op == "hop":
+        x = conv3x3_t(p, "conv2_t", x)
+        x = cab(p, "CAB", x)
+        x = crop(x, _ceil(h, 8), _ceil(w, 8))
+        x = res_au(p, "iact2", x)
+        x = conv1x1(p, "conv3_t", x)
+        x = pixel_shuffle(x, 2)
+        x = tam(p, "TAM", x, False)
+        x = crop(x, _ceil(h, 4), _ceil(w, 4))
+        x = res_au(p, "iact3", x)
+        x = conv3x3_t(p, "conv4_t", x)
+        x = pixel_shuffle(x, 2)
+    else:
+        x = upsample(p, op, "conv2_t", x)
+        x = crop(x, _ceil(h, 8), _ceil(w, 8))
+        x = res_au(p, "iact2", x)
+        x = conv3x3(p, "conv3", x)
+        x = res_au(p, "iact3", x)
+        x = conv1x1(p, "conv4", x)
+        x = pixel_shuffle(x, 8)
+    return denormalize(x)
+
+
+def synthesize(py, puv, op, y_hat, uv_hat, height, width, tiles, sv=1, sh=1, out_h=None,
+               out_w=None):
+    """``synthesize_luma_into`` + ``synthesize_chroma_into`` (src/decoder/reconstruct.rs:379-464):
+    per tile, window the latents, run the nets, copy tile cores into the planes (chroma keeps the
+    rows/cols at multiples of ``sv``/``sh``). ``tiles`` are ``geometry.SynthesisTile``.
+    Returns ``(rec_y [out_h, out_w], rec_u, rec_v [ceil(out_h/sv), ceil(out_w/sw)])`` float32;
+    ``puv`` None skips chroma."""
+    out_h = height if out_h is None else out_h
+    out_w = width if out_w is None else out_w
+    rec_y = np.zeros((out_h, out_w), np.float32)
+    ch, cw = _ceil(out_h, sv), _ceil(out_w, sh)
+    rec_u = np.zeros((ch, cw), np.float32)
+    rec_v = np.zeros((ch, cw), np.float32)
+    for t in tiles:
+        img, lat, core = t.image, t.latent, t.core
+        ox, oy = t.core_offset
+        by = np.ascontiguousarray(y_hat[:, lat.y:lat.y + lat.height, lat.x:lat.x + lat.width])
+        ty = primary(py, op, by, img.height, img.width)[0]
+        rows = min(core.height, max(out_h - core.y, 0))
+        cols = min(core.width, max(out_w - core.x, 0))
+        rec_y[core.y:core.y + rows, core.x:core.x + cols] = ty[oy:oy + rows, ox:ox + cols]
+        if puv is None:
+            continue
+        buv = np.ascontiguousarray(uv_hat[:, lat.y:lat.y + lat.height, lat.x:lat.x + lat.width])
+        tuv = secondary(puv, op, by, buv, img.height, img.width)
+        for c, dst in enumerate((rec_u, rec_v)):
+            y0 = _ceil(core.y, sv) * sv
+            x0 = _ceil(core.x, sh) * sh
+            for py_ in range(y0, min(core.y + core.height, out_h), sv):
+                xs = np.arange(x0, min(core.x + core.width, out_w), sh)
+                dst[py_ // sv, xs // sh] = tuv[c, oy + py_ - core.y, ox + xs - core.x]
+    return rec_y, rec_u, rec_v
+
+
+__all__ = ["crop", "res_au", "upsample", "residual_block", "cab", "transformer_block", "tam",
+           "light_primary", "hop_primary", "primary", "secondary", "synthesize", "quantize_plane",
+           "math"]
