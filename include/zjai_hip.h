@@ -1,0 +1,237 @@
+/*
+ * zjai_hip.h -- C-ABI of the MI355X (gfx950) synthesis backend for zenjpegai.
+ *
+ * This is the drop-in boundary a `zenjpegai-hip` Rust crate binds (all `unsafe` stays in that
+ * crate; the main crate keeps `#![forbid(unsafe_code)]`). Plain pointers and sizes only.
+ *
+ * Conventions
+ *  - Every entry point returns an int32 status: ZJAI_OK (0) or a negative ZJAI_E_* code. The
+ *    codes map 1:1 to `zenjpegai::Error` variants (reference src/error.rs:8-33) plus a device
+ *    class; as with the reference's wgpu backend (gpu/src/error.rs:6-25), any failure other than
+ *    ZJAI_E_INVALID_ARGUMENT on a well-formed call means "fall back to the CPU engine".
+ *    zjai_last_error() returns the message of the context's last failure.
+ *  - Host tensors are planar float32 [c][h][w] (the reference's `Tensor<f32>`, src/tensor.rs:12).
+ *  - Weights use PyTorch layouts: conv [out][in/groups][kh][kw], transposed conv
+ *    [in][out][k][k] (src/nn/mod.rs:56-136). They are copied at creation; host buffers stay
+ *    the caller's. Device tensors are NHWC, owned by the context's pool.
+ *  - A context owns one HIP stream on one device and must be used by one host thread at a time
+ *    (the Rust side holds it behind a Mutex, as `GpuDecoder.workspace`, gpu/src/decoder.rs:212).
+ */
+#ifndef ZJAI_HIP_H
+#define ZJAI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define ZJAI_API __attribute__((visibility("default")))
+#else
+#define ZJAI_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define ZJAI_OK 0
+#define ZJAI_E_INVALID_ARGUMENT (-1) /* Error::InvalidArgument */
+#define ZJAI_E_UNSUPPORTED (-2)      /* Error::Unsupported */
+#define ZJAI_E_LIMIT (-3)            /* Error::LimitExceeded (device memory) */
+#define ZJAI_E_MODEL (-4)            /* Error::Model (bad weight shapes / missing tensors) */
+#define ZJAI_E_CANCELLED (-5)        /* Error::Cancelled */
+#define ZJAI_E_DEVICE (-6)           /* HIP runtime / device failure */
+
+/* Precision of a layer / net: storage type of weights and activations. Accumulation is f32. */
+#define ZJAI_F32 0  /* fp32 MFMA parity path */
+#define ZJAI_F16 1  /* f16 inputs, fp32 accumulate */
+#define ZJAI_BF16 2 /* bf16 inputs, fp32 accumulate */
+
+/* Operating points and components (reference src/header.rs:39, src/model/synthesis.rs). */
+#define ZJAI_OP_SOP 0
+#define ZJAI_OP_BOP 1
+#define ZJAI_OP_HOP 2
+#define ZJAI_COMP_Y 0
+#define ZJAI_COMP_UV 1
+
+/* Fused epilogue selectors (zjai_conv_forward_fused). */
+#define ZJAI_ACT_NONE 0
+#define ZJAI_ACT_RELU 1
+#define ZJAI_ACT_LEAKY_RELU 2
+#define ZJAI_ACT_SIGMOID 3
+#define ZJAI_RES_NONE 0
+#define ZJAI_RES_ADD 1  /* y = a + r1 */
+#define ZJAI_RES_GATE 2 /* y = r1 * (1 + a) */
+#define ZJAI_RES_CAB 3  /* y = r1 * sigmoid(a) + r2 */
+#define ZJAI_RES_MUL 4  /* y = r1 * a */
+
+typedef struct zjai_ctx zjai_ctx;
+typedef struct zjai_tensor zjai_tensor;
+typedef struct zjai_layer zjai_layer;
+typedef struct zjai_net zjai_net;
+typedef struct zjai_picture zjai_picture;
+
+/* ------------------------------------------------------------------ context / diagnostics */
+
+/* Replaces `Engine` construction (src/nn/fast/mod.rs:128-172) for the HIP backend: binds a
+ * device and creates its stream. flags: reserved, 0. */
+ZJAI_API int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out);
+ZJAI_API int32_t zjai_ctx_destroy(zjai_ctx* ctx);
+/* Copies the last failure message (NUL-terminated, truncated to len). Works with ctx == NULL
+ * for failures of zjai_ctx_create. */
+ZJAI_API int32_t zjai_last_error(const zjai_ctx* ctx, char* buf, size_t len);
+/* Blocks until the context's stream is idle. */
+ZJAI_API int32_t zjai_sync(zjai_ctx* ctx);
+/* Cooperative cancellation, the `enough::Stop` check between layers and tiles
+ * (src/decoder/api.rs:283-299): while set, running calls return ZJAI_E_CANCELLED at their next
+ * check. */
+ZJAI_API int32_t zjai_set_stop(zjai_ctx* ctx, int32_t stop);
+
+typedef struct zjai_stats {
+    float last_run_ms;        /* device time of the last zjai_picture_run (HIP events) */
+    int64_t kernel_launches;  /* launches issued by the context so far */
+    uint64_t pool_in_use;     /* device bytes held by live tensors */
+    uint64_t pool_peak;       /* high-water mark of pool_in_use */
+    uint64_t pool_cached;     /* device bytes held by the pool in total */
+} zjai_stats;
+/* Replaces the reference's `DecodeStats` probe (src/decoder/stats.rs:301) for device work. */
+ZJAI_API int32_t zjai_get_stats(zjai_ctx* ctx, zjai_stats* out);
+/* Returns cached pool blocks to the device (`release_buffers`, src/nn/fast/tensor.rs:122). */
+ZJAI_API int32_t zjai_release_buffers(zjai_ctx* ctx);
+
+/* ----------------------------------------------------------------------- device tensors */
+
+/* `BTensor::zeros` / `scratch` (src/nn/fast/tensor.rs:203-230) on the device: [c][h][w] stored
+ * NHWC with the channel stride padded to 8. */
+ZJAI_API int32_t zjai_tensor_create(zjai_ctx* ctx, int32_t c, int32_t h, int32_t w, int32_t precision,
+                           zjai_tensor** out);
+/* `BTensor::from_planar` (src/nn/fast/tensor.rs:251): host planar f32 [c][h][w] -> new device
+ * tensor. */
+ZJAI_API int32_t zjai_tensor_from_planar(zjai_ctx* ctx, const float* data, int32_t c, int32_t h,
+                                int32_t w, int32_t precision, zjai_tensor** out);
+/* `BTensor::to_planar` (src/nn/fast/tensor.rs:265): device tensor -> host planar f32
+ * (capacity `len` floats; needs c*h*w). Synchronises the stream. */
+ZJAI_API int32_t zjai_tensor_to_planar(zjai_ctx* ctx, const zjai_tensor* t, float* data, size_t len);
+ZJAI_API int32_t zjai_tensor_shape(const zjai_tensor* t, int32_t* c, int32_t* h, int32_t* w,
+                          int32_t* precision);
+/* `BTensor::crop_par` (src/nn/fast/tensor.rs:349): top-left h x w view (shares storage). */
+ZJAI_API int32_t zjai_tensor_crop(zjai_ctx* ctx, const zjai_tensor* t, int32_t h, int32_t w,
+                         zjai_tensor** out);
+/* `BTensor::cat` (src/nn/fast/tensor.rs:402): channel concatenation into a new tensor. */
+ZJAI_API int32_t zjai_tensor_cat(zjai_ctx* ctx, const zjai_tensor* const* parts, int32_t n,
+                        zjai_tensor** out);
+ZJAI_API int32_t zjai_tensor_destroy(zjai_tensor* t);
+
+/* ------------------------------------------------------------------------------- layers */
+
+/* `ConvLayer::with_extra_pad(Conv2d, &Engine, extra_pad)` (src/nn/fast/layers.rs:36) /
+ * `PackedConv::new` (src/nn/fast/conv.rs:524) and `PackedDepthwise::new`
+ * (src/nn/fast/depthwise.rs:103): weight [out][in/groups][kh][kw], bias nullable,
+ * extra_pad [top, left, bottom, right] or NULL. Supported: 1x1, 2x2, 3x3 stride 1; 3x3
+ * stride 2; depthwise 3x3. Other geometries return ZJAI_E_UNSUPPORTED. */
+ZJAI_API int32_t zjai_conv2d_create(zjai_ctx* ctx, int32_t in_ch, int32_t out_ch, int32_t kh, int32_t kw,
+                           int32_t stride, int32_t pad_h, int32_t pad_w, int32_t groups,
+                           const float* weight, const float* bias, const int32_t* extra_pad,
+                           int32_t precision, zjai_layer** out);
+/* `ConvTransposeLayer::new(ConvTranspose2d)` (src/nn/fast/layers.rs:136) /
+ * `PackedConvTranspose::new` (src/nn/fast/conv.rs:1919): weight [in][out][k][k]; stride 2
+ * with k in {3, 4}. */
+ZJAI_API int32_t zjai_conv_transpose2d_create(zjai_ctx* ctx, int32_t in_ch, int32_t out_ch, int32_t k,
+                                     int32_t stride, int32_t pad, int32_t out_pad,
+                                     const float* weight, const float* bias, int32_t precision,
+                                     zjai_layer** out);
+ZJAI_API int32_t zjai_layer_destroy(zjai_layer* layer);
+/* `ConvLayer::forward` / `ConvTransposeLayer::forward` (src/nn/fast/layers.rs:92, :162):
+ * new output tensor. */
+ZJAI_API int32_t zjai_conv_forward(zjai_ctx* ctx, const zjai_layer* layer, const zjai_tensor* x,
+                          zjai_tensor** out);
+/* Forward with a fused epilogue: act (ZJAI_ACT_*), then res (ZJAI_RES_*) against r1 / r2
+ * (tensors with the output's shape), optional pixel shuffle r (1 = none) and relu6 applied
+ * to x on load. Equals the reference's layer followed by its elementwise ops
+ * (src/nn/fast/layers.rs:174-289, src/nn/fast/math.rs:371-397). */
+ZJAI_API int32_t zjai_conv_forward_fused(zjai_ctx* ctx, const zjai_layer* layer, const zjai_tensor* x,
+                                int32_t act, int32_t res, const zjai_tensor* r1,
+                                const zjai_tensor* r2, int32_t pixel_shuffle,
+                                int32_t relu6_input, zjai_tensor** out);
+
+/* ------------------------------------------------------------------- elementwise (in place) */
+/* src/nn/fast/layers.rs:204-229, src/model/hyper_encoder.rs:24, src/nn/fast/math.rs:371-397 */
+ZJAI_API int32_t zjai_relu(zjai_ctx* ctx, zjai_tensor* x);
+ZJAI_API int32_t zjai_relu6(zjai_ctx* ctx, zjai_tensor* x);
+ZJAI_API int32_t zjai_leaky_relu(zjai_ctx* ctx, zjai_tensor* x);
+ZJAI_API int32_t zjai_sigmoid(zjai_ctx* ctx, zjai_tensor* x);
+ZJAI_API int32_t zjai_add_assign(zjai_ctx* ctx, zjai_tensor* dst, const zjai_tensor* src);
+ZJAI_API int32_t zjai_gate(zjai_ctx* ctx, zjai_tensor* x, const zjai_tensor* mask);
+ZJAI_API int32_t zjai_mul_assign(zjai_ctx* ctx, zjai_tensor* a, const zjai_tensor* b);
+ZJAI_API int32_t zjai_elu_gate(zjai_ctx* ctx, zjai_tensor* a, const zjai_tensor* b);
+/* `pixel_shuffle(&Engine, &BTensor, r)` (src/nn/fast/layers.rs:262). */
+ZJAI_API int32_t zjai_pixel_shuffle(zjai_ctx* ctx, const zjai_tensor* x, int32_t r, zjai_tensor** out);
+/* `math::layer_norm_channels` (src/nn/fast/math.rs:423), into a new tensor. */
+ZJAI_API int32_t zjai_layer_norm_channels(zjai_ctx* ctx, const zjai_tensor* x, const float* weight,
+                                 const float* bias, zjai_tensor** out);
+/* `math::channel_attention` (src/nn/fast/math.rs:512): qkv [3*dim] channels -> [dim]. */
+ZJAI_API int32_t zjai_channel_attention(zjai_ctx* ctx, const zjai_tensor* qkv, int32_t heads,
+                               const float* temperature, zjai_tensor** out);
+
+/* ------------------------------------------------------------------------ synthesis nets */
+
+/* `SynthesisPrimary::load` / `SynthesisSecondary::load` (src/model/synthesis.rs:242, :972) from
+ * named checkpoint tensors (names and shapes of fuzz/fuzz_targets/common.rs:260-345, e.g.
+ * "first_stage.0.0.conv1.weight"). shapes: ndims[i] dims each, concatenated in `dims`. */
+ZJAI_API int32_t zjai_net_create(zjai_ctx* ctx, int32_t op, int32_t component, int32_t precision,
+                        int32_t n_tensors, const char* const* names, const int32_t* ndims,
+                        const int32_t* dims, const float* const* data, zjai_net** out);
+ZJAI_API int32_t zjai_net_destroy(zjai_net* net);
+/* Output plane size of a net for an h x w target (>= h x w; the caller crops). */
+ZJAI_API int32_t zjai_net_out_size(const zjai_net* net, int32_t h, int32_t w, int32_t* oh, int32_t* ow);
+/* `SynthesisPrimary::forward_with` (src/model/synthesis.rs:262): y_hat [160][lh][lw] device
+ * tensor -> host planar [1][oh][ow] in [0, 255] (capacity `len` floats). */
+ZJAI_API int32_t zjai_primary_forward(zjai_ctx* ctx, const zjai_net* net, const zjai_tensor* y_hat,
+                             int32_t h, int32_t w, float* out, size_t len);
+/* `SynthesisSecondary::forward_with` (src/model/synthesis.rs:1004): luma [160] and chroma [96]
+ * latents -> host planar [2][oh][ow] in [0, 255]. */
+ZJAI_API int32_t zjai_secondary_forward(zjai_ctx* ctx, const zjai_net* net, const zjai_tensor* y_luma,
+                               const zjai_tensor* y_chroma, int32_t h, int32_t w, float* out,
+                               size_t len);
+
+/* ----------------------------------------------------------------------- picture driver */
+
+/* One synthesis tile (reference `SynthesisTile`, src/tools/tiles.rs:26-35). */
+typedef struct zjai_tile {
+    int32_t image_x, image_y, image_w, image_h;
+    int32_t latent_x, latent_y, latent_w, latent_h;
+    int32_t core_x, core_y, core_w, core_h;
+    int32_t core_off_x, core_off_y;
+} zjai_tile;
+
+/* Tile layout of a height x width picture (`synthesis_tiles`, src/tools/tiles.rs:39-119).
+ * tile_size == 0 disables tiling. With region_rows/cols > 0 tiles respect that grid of
+ * independent regions (`region_grid(hdr, 0, Plane::Image)`, src/tools/regions.rs:116-150).
+ * Writes up to `cap` tiles, *n = count (ZJAI_E_LIMIT if cap is too small). */
+ZJAI_API int32_t zjai_synthesis_tiles(int32_t height, int32_t width, int32_t latent_h, int32_t latent_w,
+                             int32_t tile_size, int32_t overlap, int32_t region_rows,
+                             int32_t region_cols, zjai_tile* tiles, int32_t cap, int32_t* n);
+
+/* The synthesis half of `reconstruct::synthesize_with` (src/decoder/reconstruct.rs:285-331) plus
+ * `quantize_plane` (src/decoder/output.rs:330): plans a picture of height x width from latents
+ * [160][lh][lw] (+ [96][lh][lw] when net_uv is given), tiles as given, chroma subsampling
+ * sv x sh, displayed size out_h x out_w, output bit depth (0 = float planes in [0, 255]). */
+ZJAI_API int32_t zjai_picture_create(zjai_ctx* ctx, const zjai_net* net_y, const zjai_net* net_uv,
+                            int32_t lh, int32_t lw, int32_t height, int32_t width,
+                            const zjai_tile* tiles, int32_t n_tiles, int32_t sv, int32_t sh,
+                            int32_t out_h, int32_t out_w, int32_t bit_depth, zjai_picture** out);
+ZJAI_API int32_t zjai_picture_destroy(zjai_picture* pic);
+/* Uploads the decoded latents once (planar f32; uv_hat may be NULL without net_uv). */
+ZJAI_API int32_t zjai_picture_upload(zjai_ctx* ctx, zjai_picture* pic, const float* y_hat,
+                            const float* uv_hat);
+/* Enqueues every tile on the context's stream (asynchronous; latents must be uploaded). */
+ZJAI_API int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic);
+/* Copies the planes out (synchronises): Y out_h*out_w, U/V ceil(out_h/sv)*ceil(out_w/sh)
+ * samples each, as float (bit_depth 0) or uint16. u/v may be NULL without net_uv. */
+ZJAI_API int32_t zjai_picture_download(zjai_ctx* ctx, zjai_picture* pic, void* y, void* u, void* v);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZJAI_HIP_H */

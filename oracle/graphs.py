@@ -106,8 +106,9 @@ def tam(p, pfx, x, downsample):
     return x
 
 
-def light_primary(p, op, y_hat, h, w):
-    """``LightPrimary::forward`` (src/model/synthesis.rs:550-580) -> ``[1, >=h, >=w]``."""
+def light_primary(p, op, y_hat, h, w, denorm=True):
+    """``LightPrimary::forward`` (src/model/synthesis.rs:550-580) -> ``[1, >=h, >=w]``.
+    ``denorm=False`` returns the values before ``denormalize`` (for conditioning bounds)."""
     x = add(relu(conv3x3(p, "first_stage.0.0.conv1", y_hat)), y_hat)
     x = upsample(p, op, "first_stage.1", x)
     x = res_au(p, "first_stage.2", x)
@@ -117,11 +118,11 @@ def light_primary(p, op, y_hat, h, w):
     x = res_au(p, "iact2", x)
     x = conv3x3(p, "conv3", x)
     x = res_au(p, "iact3", x)
-    x = conv1x1(p, "conv4", x)
-    return denormalize(pixel_shuffle(x, 4))
+    x = pixel_shuffle(conv1x1(p, "conv4", x), 4)
+    return denormalize(x) if denorm else x
 
 
-def hop_primary(p, y_hat, h, w):
+def hop_primary(p, y_hat, h, w, denorm=True):
     """``HopPrimary::forward`` (src/model/synthesis.rs:356-390)."""
     x = residual_block(p, "first_stage.0.0", y_hat)
     x = conv3x3_t(p, "first_stage.1", x)
@@ -137,17 +138,17 @@ def hop_primary(p, y_hat, h, w):
     x = crop(x, _ceil(h, 2), _ceil(w, 2))
     x = res_au(p, "iact3", x)
     x = conv3x3_t(p, "conv4_t", x)
-    return denormalize(x)
+    return denormalize(x) if denorm else x
 
 
-def primary(p, op, y_hat, h, w):
+def primary(p, op, y_hat, h, w, denorm=True):
     """``SynthesisPrimary::forward`` (src/model/synthesis.rs:262-276)."""
     if op == "hop":
-        return hop_primary(p, y_hat, h, w)
-    return light_primary(p, op, y_hat, h, w)
+        return hop_primary(p, y_hat, h, w, denorm)
+    return light_primary(p, op, y_hat, h, w, denorm)
 
 
-def secondary(p, op, y_hat_luma, y_hat_chroma, h, w):
+def secondary(p, op, y_hat_luma, y_hat_chroma, h, w, denorm=True):
     """``SynthesisSecondary::forward_with`` (src/model/synthesis.rs:1004-1038) with
     ``LightSecondary``/``HopSecondary`` tails (:884-909, :755-773)."""
     lh = min(y_hat_luma.shape[1], y_hat_chroma.shape[1])
@@ -177,7 +178,7 @@ def secondary(p, op, y_hat_luma, y_hat_chroma, h, w):
         x = res_au(p, "iact3", x)
         x = conv1x1(p, "conv4", x)
         x = pixel_shuffle(x, 8)
-    return denormalize(x)
+    return denormalize(x) if denorm else x
 
 
 def synthesize(py, puv, op, y_hat, uv_hat, height, width, tiles, sv=1, sh=1, out_h=None,

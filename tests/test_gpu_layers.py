@@ -1,0 +1,282 @@
+"""GPU parity of the operator layer (through the C-ABI) against the CPU oracle and the
+reference's fixtures.
+
+Tolerances (written per test):
+* fp32-MFMA convolutions: max |gpu - ref| <= 1e-4 * max|ref| (the per-layer bound of the
+  north-star contract); the MFMA summation order differs from the reference's serial FMA chain.
+* f16 / bf16 inputs (fp32 accumulate): 4e-3 / 3e-2 * max|ref| (input rounding of 2^-11 / 2^-8).
+* Elementwise ops, depthwise conv and layer norm in fp32 follow the reference's operation order
+  and are required to be bit-exact.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.golden import zjtb
+from zenjpegai_amd import _lib, nn, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-4, "f16": 4e-3, "bf16": 3e-2}
+
+
+@pytest.fixture(scope="module")
+def engines():
+    return {p: nn.Engine(0, p) for p in ("f32", "f16", "bf16")}
+
+
+def rel_err(got, want):
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(np.asarray(got, np.float64) - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def _pad_channels(x, w, groups, to=8):
+    """Zero-pads input channels per group to a multiple of `to` (weights padded to match), which
+    leaves the convolution's value unchanged."""
+    c = x.shape[0]
+    icg = c // groups
+    icg_p = -(-icg // to) * to
+    if icg_p == icg:
+        return x, w
+    xs = np.zeros((groups * icg_p,) + x.shape[1:], np.float32)
+    ws = np.zeros((w.shape[0], icg_p) + w.shape[2:], np.float32)
+    for g in range(groups):
+        xs[g * icg_p:g * icg_p + icg] = x[g * icg:(g + 1) * icg]
+    ws[:, :icg] = w
+    return xs, ws
+
+
+CONV_FIXTURES = [
+    ("conv3x3_s1_p1_bias", 1, (1, 1), 1),
+    ("conv3x3_s1_p1_g4_nobias", 1, (1, 1), 4),
+    ("conv3x3_depthwise", 1, (1, 1), 12),
+    ("conv1x1_nobias", 1, (0, 0), 1),
+    ("conv3x3_s2_p1_bias", 2, (1, 1), 1),
+    ("conv2x2_s1_p0", 1, (0, 0), 1),
+]
+
+
+@pytest.mark.parametrize("prec", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("name,stride,pad,groups", CONV_FIXTURES)
+def test_conv_reference_fixtures(engines, prec, name, stride, pad, groups):
+    eng = engines[prec]
+    t = zjtb.load(name)
+    x, w = t["x"], t["w"]
+    if groups != x.shape[0]:
+        x, w = _pad_channels(x, w, groups)
+    cin = x.shape[0]
+    layer = nn.ConvLayer(nn.Conv2d(cin, w.shape[0], w.shape[2:], stride, pad, groups, w,
+                                   t.get("b")), eng)
+    y = layer.forward(eng, nn.BTensor.from_planar(eng, x)).to_planar()
+    assert y.shape == t["y"].shape
+    assert rel_err(y, t["y"]) <= TOL[prec], name
+
+
+@pytest.mark.parametrize("prec", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("name,pad,out_pad", [("convt4x4_s2_p1_bias", 1, 0),
+                                              ("convt3x3_s2_p1_op1_bias", 1, 1)])
+def test_conv_transpose_reference_fixtures(engines, prec, name, pad, out_pad):
+    eng = engines[prec]
+    t = zjtb.load(name)
+    x, w = t["x"], t["w"]  # w [in][out][k][k]
+    cin = -(-x.shape[0] // 8) * 8
+    xp = np.zeros((cin,) + x.shape[1:], np.float32)
+    xp[:x.shape[0]] = x
+    wp = np.zeros((cin,) + w.shape[1:], np.float32)
+    wp[:w.shape[0]] = w
+    layer = nn.ConvTransposeLayer(nn.ConvTranspose2d(cin, w.shape[1], w.shape[2], 2, pad, out_pad,
+                                                     wp, t.get("b")), eng)
+    y = layer.forward(eng, nn.BTensor.from_planar(eng, xp)).to_planar()
+    assert y.shape == t["y"].shape
+    assert rel_err(y, t["y"]) <= TOL[prec], name
+
+
+def test_unsupported_geometry_is_reported(engines):
+    eng = engines["f32"]
+    t = zjtb.load("conv1x3_p01_bias")
+    w = np.zeros((8, 8, 1, 3), np.float32)
+    with pytest.raises(_lib.HipError) as e:
+        nn.ConvLayer(nn.Conv2d(8, 8, (1, 3), 1, (0, 1), 1, w), eng)
+    assert e.value.kind == "Unsupported"
+
+
+def _he(name, shape, fan_in, seed=11):
+    return synth.normal(seed, name, shape, np.sqrt(2.0 / fan_in))
+
+
+@pytest.mark.parametrize("prec", ["f32", "f16", "bf16"])
+def test_config1_conv3x3_128(engines, prec):
+    """BASELINE config 1 (Conv2d 3x3 s1 p1 128->128, U[-1,1] input, He weights, N(0,0.01)
+    bias) on a 64x64 crop of its input size."""
+    eng = engines[prec]
+    x = synth.uniform(1, "cfg1/x", (128, 64, 64), -1, 1)
+    w = _he("cfg1/w", (128, 128, 3, 3), 1152)
+    b = synth.normal(1, "cfg1/b", (128,), 0.01)
+    y = nn.ConvLayer(nn.Conv2d(128, 128, (3, 3), 1, (1, 1), 1, w, b), eng).forward(
+        eng, nn.BTensor.from_planar(eng, x)).to_planar()
+    want = oracle.conv2d(x, w, b, 1, (1, 1))
+    assert rel_err(y, want) <= TOL[prec]
+
+
+@pytest.mark.parametrize("prec", ["f32", "bf16"])
+def test_config2_convt4_leaky(engines, prec):
+    """BASELINE config 2 at full size: ConvT k4 s2 p1 192->128, 64^2 -> 128^2, then
+    LeakyReLU(0.01), fused into the epilogue."""
+    eng = engines[prec]
+    x = synth.laplace(2, "cfg2/x", (192, 64, 64), 1.0)
+    w = synth.normal(2, "cfg2/w", (192, 128, 4, 4), np.sqrt(2.0 / (192 * 4)))
+    b = synth.normal(2, "cfg2/b", (128,), 0.01)
+    layer = nn.ConvTransposeLayer(nn.ConvTranspose2d(192, 128, 4, 2, 1, 0, w, b), eng)
+    y = layer.forward_fused(eng, nn.BTensor.from_planar(eng, x), act=_lib.ACT_LEAKY_RELU).to_planar()
+    want = oracle.leaky_relu(oracle.conv_transpose2d(x, w, b, 2, 1, 0))
+    assert y.shape == (128, 128, 128)
+    assert rel_err(y, want) <= TOL[prec]
+
+
+def config3_oracle(x, p):
+    t = oracle.conv2d(x, p["c1w"], p["c1b"], 1, (1, 1))
+    t = oracle.leaky_relu(t)
+    t = oracle.add(oracle.conv2d(t, p["c2w"], p["c2b"], 1, (1, 1)), x)
+    g = oracle.sigmoid(oracle.conv2d(x, p["gw"], p["gb"], 1, (0, 0)))
+    return oracle.mul(t, g)
+
+
+def config3_params(c=192, seed=3):
+    return {"c1w": _he("cfg3/c1w", (c, c, 3, 3), c * 9, seed),
+            "c1b": synth.normal(seed, "cfg3/c1b", (c,), 0.01),
+            "c2w": _he("cfg3/c2w", (c, c, 3, 3), c * 9, seed),
+            "c2b": synth.normal(seed, "cfg3/c2b", (c,), 0.01),
+            "gw": _he("cfg3/gw", (c, c, 1, 1), c, seed),
+            "gb": synth.normal(seed, "cfg3/gb", (c,), 0.01)}
+
+
+def config3_gpu(eng, x, p):
+    c = x.shape[0]
+    c1 = nn.ConvLayer(nn.Conv2d(c, c, (3, 3), 1, (1, 1), 1, p["c1w"], p["c1b"]), eng)
+    c2 = nn.ConvLayer(nn.Conv2d(c, c, (3, 3), 1, (1, 1), 1, p["c2w"], p["c2b"]), eng)
+    gl = nn.ConvLayer(nn.Conv2d(c, c, (1, 1), 1, (0, 0), 1, p["gw"], p["gb"]), eng)
+    xt = nn.BTensor.from_planar(eng, x)
+    t = c1.forward_fused(eng, xt, act=_lib.ACT_LEAKY_RELU)
+    t = c2.forward_fused(eng, t, res=_lib.RES_ADD, r1=xt)
+    return gl.forward_fused(eng, xt, act=_lib.ACT_SIGMOID, res=_lib.RES_MUL, r1=t)
+
+
+@pytest.mark.parametrize("prec", ["f32", "bf16"])
+def test_config3_residual_sigmoid_gated_block(engines, prec):
+    """BASELINE config 3 (t = conv3x3(leaky(conv3x3(x))) + x; out = t * sigmoid(conv1x1(x)))
+    at 192 channels on a 48x48 crop."""
+    eng = engines[prec]
+    x = synth.uniform(3, "cfg3/x", (192, 48, 48), -2, 2)
+    p = config3_params()
+    y = config3_gpu(eng, x, p).to_planar()
+    assert rel_err(y, config3_oracle(x, p)) <= TOL[prec] * 3
+
+
+def test_fused_epilogues_match_op_sequences(engines):
+    eng = engines["f32"]
+    x = synth.normal(4, "ep/x", (64, 20, 24), 1.0)
+    r = synth.normal(4, "ep/r", (64, 20, 24), 1.0)
+    w = _he("ep/w", (64, 64, 3, 3), 576)
+    b = synth.normal(4, "ep/b", (64,), 0.1)
+    layer = nn.ConvLayer(nn.Conv2d(64, 64, (3, 3), 1, (1, 1), 1, w, b), eng)
+    xt, rt = nn.BTensor.from_planar(eng, x), nn.BTensor.from_planar(eng, r)
+    base = oracle.conv2d(x, w, b, 1, (1, 1))
+    cases = [
+        (dict(act=_lib.ACT_RELU, res=_lib.RES_ADD, r1=rt), oracle.add(oracle.relu(base), r)),
+        (dict(res=_lib.RES_GATE, r1=rt), oracle.gate(r, base)),
+        (dict(res=_lib.RES_CAB, r1=rt, r2=xt), oracle.add(oracle.mul(r, oracle.sigmoid(base)), x)),
+        (dict(relu6_input=True), oracle.conv2d(oracle.relu6(x), w, b, 1, (1, 1))),
+    ]
+    for kw, want in cases:
+        got = layer.forward_fused(eng, xt, **kw).to_planar()
+        assert rel_err(got, want) <= 1e-4, kw
+    ps = layer.forward_fused(eng, xt, pixel_shuffle=2).to_planar()
+    assert rel_err(ps, oracle.pixel_shuffle(base, 2)) <= 1e-4
+
+
+@pytest.mark.parametrize("cin,cout,groups", [(64, 64, 4), (32, 32, 2), (128, 128, 4), (96, 96, 6),
+                                             (160, 256, 1), (144, 48, 1)])
+def test_grouped_and_wide_convs(engines, cin, cout, groups):
+    eng = engines["f32"]
+    x = synth.normal(5, f"g/x{cin}", (cin, 19, 37), 1.0)
+    w = _he(f"g/w{cin}{groups}", (cout, cin // groups, 3, 3), cin // groups * 9)
+    y = nn.ConvLayer(nn.Conv2d(cin, cout, (3, 3), 1, (1, 1), groups, w), eng).forward(
+        eng, nn.BTensor.from_planar(eng, x)).to_planar()
+    assert rel_err(y, oracle.conv2d(x, w, None, 1, (1, 1), groups)) <= 1e-4
+
+
+def test_sop_upsample_conv2x2_extra_pad(engines):
+    eng = engines["f32"]
+    x = synth.normal(6, "up/x", (160, 9, 13), 1.0)
+    w = _he("up/w", (256, 160, 2, 2), 640)
+    layer = nn.ConvLayer(nn.Conv2d(160, 256, (2, 2), 1, (0, 0), 1, w), eng, (0, 0, 1, 1))
+    y = layer.forward_fused(eng, nn.BTensor.from_planar(eng, x), pixel_shuffle=2).to_planar()
+    want = oracle.pixel_shuffle(oracle.conv2d(x, w, None, 1, (0, 0), 1, (0, 0, 1, 1)), 2)
+    assert y.shape == want.shape == (64, 18, 26)
+    assert rel_err(y, want) <= 1e-4
+
+
+@pytest.mark.parametrize("k,op", [(3, 1), (4, 0)])
+def test_conv_transpose_odd_sizes(engines, k, op):
+    eng = engines["f32"]
+    x = synth.normal(7, "t/x", (64, 7, 11), 1.0)
+    w = synth.normal(7, "t/w", (64, 32, k, k), 0.1)
+    b = synth.normal(7, "t/b", (32,), 0.1)
+    y = nn.ConvTransposeLayer(nn.ConvTranspose2d(64, 32, k, 2, 1, op, w, b), eng).forward(
+        eng, nn.BTensor.from_planar(eng, x)).to_planar()
+    assert rel_err(y, oracle.conv_transpose2d(x, w, b, 2, 1, op)) <= 1e-4
+
+
+def test_elementwise_ops_are_bit_exact(engines):
+    eng = engines["f32"]
+    a = synth.normal(8, "el/a", (16, 9, 10), 3.0)
+    b = synth.normal(8, "el/b", (16, 9, 10), 1.0)
+    for fn, ref in [(nn.relu, oracle.relu), (nn.relu6, oracle.relu6), (nn.leaky_relu, oracle.leaky_relu),
+                    (nn.sigmoid, oracle.sigmoid)]:
+        t = nn.BTensor.from_planar(eng, a)
+        fn(eng, t)
+        assert np.array_equal(t.to_planar().view(np.uint32), ref(a).view(np.uint32)), fn.__name__
+    for fn, ref in [(nn.add_assign, oracle.add), (nn.gate, oracle.gate), (nn.mul_assign, oracle.mul),
+                    (nn.elu_gate, oracle.elu_gate)]:
+        t = nn.BTensor.from_planar(eng, a)
+        fn(eng, t, nn.BTensor.from_planar(eng, b))
+        assert np.array_equal(t.to_planar().view(np.uint32), ref(a, b).view(np.uint32)), fn.__name__
+    ps = nn.pixel_shuffle(eng, nn.BTensor.from_planar(eng, synth.normal(8, "el/p", (64, 3, 5))), 2)
+    assert np.array_equal(ps.to_planar(), oracle.pixel_shuffle(synth.normal(8, "el/p", (64, 3, 5)), 2))
+
+
+def test_depthwise_and_layer_norm_are_bit_exact(engines):
+    eng = engines["f32"]
+    x = synth.normal(9, "dw/x", (384, 11, 13), 1.0)
+    w = synth.normal(9, "dw/w", (384, 1, 3, 3), 0.3)
+    y = nn.ConvLayer(nn.Conv2d(384, 384, (3, 3), 1, (1, 1), 384, w), eng).forward(
+        eng, nn.BTensor.from_planar(eng, x)).to_planar()
+    assert np.array_equal(y.view(np.uint32), oracle.conv2d(x, w, None, 1, (1, 1), 384).view(np.uint32))
+    lw = synth.normal(9, "ln/w", (128,), 1.0)
+    lb = synth.normal(9, "ln/b", (128,), 1.0)
+    xl = synth.normal(9, "ln/x", (128, 7, 9), 2.0)
+    got = nn.layer_norm_channels(eng, nn.BTensor.from_planar(eng, xl), lw, lb).to_planar()
+    assert np.array_equal(got.view(np.uint32), oracle.layer_norm_channels(xl, lw, lb).view(np.uint32))
+
+
+@pytest.mark.parametrize("dim,h,w", [(128, 24, 40), (64, 33, 17)])
+def test_channel_attention(engines, dim, h, w):
+    eng = engines["f32"]
+    qkv = synth.normal(10, f"at/{dim}", (3 * dim, h, w), 1.0)
+    temp = np.array([0.7, 1.0, 1.3, 2.0], np.float32)
+    got = nn.channel_attention(eng, nn.BTensor.from_planar(eng, qkv), 4, temp).to_planar()
+    assert rel_err(got, oracle.channel_attention(qkv, 4, temp)) <= 1e-5
+
+
+def test_attention_one_position_kat(engines):
+    """src/nn/fast/math.rs:936-943 through the HIP path (dim padded to 8 with zero rows)."""
+    eng = engines["f32"]
+    q = np.zeros((24, 1, 1), np.float32)
+    # head 0 of 4: q rows (2, -3)... embed the KAT in channels 0-1 of each of q, k, v.
+    # With 4 heads of 2 channels: head 0 holds the KAT, the other heads are zeros.
+    q[0:2, 0, 0] = [2.0, -3.0]
+    q[8:10, 0, 0] = [0.5, 4.0]
+    q[16:18, 0, 0] = [10.0, 20.0]
+    got = nn.channel_attention(eng, nn.BTensor.from_planar(eng, q), 4, np.ones(4, np.float32)).to_planar()
+    assert got[0:2, 0, 0].tolist() == [15.0, 15.0]

@@ -1,0 +1,725 @@
+// The C-ABI (include/zjai_hip.h): handles, error mapping, tiling geometry and the picture
+// driver. No exception or abort crosses this boundary.
+
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+
+#include "runtime.h"
+
+using namespace zjai;
+
+struct zjai_ctx {
+    Context c;
+};
+struct zjai_tensor {
+    TensorP t;
+};
+struct zjai_layer {
+    LayerP l;
+};
+struct zjai_net {
+    NetP n;
+};
+
+namespace {
+
+std::mutex g_err_mu;
+std::string g_err;  // failures with no context (zjai_ctx_create)
+
+template <typename F>
+int32_t guard(zjai_ctx* ctx, F&& f) {
+    try {
+        f();
+        return ZJAI_OK;
+    } catch (const Error& e) {
+        if (ctx) ctx->c.last_error = e.what();
+        else {
+            std::lock_guard<std::mutex> g(g_err_mu);
+            g_err = e.what();
+        }
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        if (ctx) ctx->c.last_error = "host allocation failed";
+        return ZJAI_E_LIMIT;
+    } catch (const std::exception& e) {
+        if (ctx) ctx->c.last_error = e.what();
+        return ZJAI_E_DEVICE;
+    }
+}
+
+void need(bool ok, const char* msg) {
+    if (!ok) throw Error(ZJAI_E_INVALID_ARGUMENT, msg);
+}
+
+TensorP planar_upload(Context& c, const float* data, int ch, int h, int w, int dtype) {
+    need(data != nullptr, "null data");
+    need(ch > 0 && h > 0 && w > 0, "bad shape");
+    need(ch % 4 == 0, "channel count must be a multiple of 4");
+    need(dtype >= DT_F32 && dtype <= DT_BF16, "precision");
+    TensorP t = c.alloc(ch, h, w, dtype);
+    const size_t n = (size_t)ch * h * w;
+    float* stage = (float*)c.pool.alloc(n * 4);
+    std::shared_ptr<void> keep(stage, [&c](void* q) { c.pool.release(q); });
+    ZJAI_HIP(hipMemcpyAsync(stage, data, n * 4, hipMemcpyHostToDevice, c.stream));
+    ZJAI_HIP(launch_planar_to_nhwc(stage, ch, h, w, 0, 0, h, w, t->v, dtype, c.stream));
+    ++c.launches;
+    ZJAI_HIP(hipStreamSynchronize(c.stream));
+    return t;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------- context
+extern "C" int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out) {
+    (void)flags;
+    if (!out) return ZJAI_E_INVALID_ARGUMENT;
+    *out = nullptr;
+    zjai_ctx* ctx = new (std::nothrow) zjai_ctx();
+    if (!ctx) return ZJAI_E_LIMIT;
+    const int32_t rc = guard(nullptr, [&] {
+        int n = 0;
+        hipError_t e = hipGetDeviceCount(&n);
+        if (e != hipSuccess || n == 0)
+            throw Error(ZJAI_E_DEVICE, std::string("no HIP device: ") + hipGetErrorString(e));
+        if (device < 0 || device >= n) throw Error(ZJAI_E_INVALID_ARGUMENT, "device index out of range");
+        hipDeviceProp_t prop;
+        ZJAI_HIP(hipGetDeviceProperties(&prop, device));
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            throw Error(ZJAI_E_UNSUPPORTED, std::string("kernels are built for gfx950, device is ") + prop.gcnArchName);
+        ZJAI_HIP(hipSetDevice(device));
+        ctx->c.device = device;
+        ZJAI_HIP(hipStreamCreateWithFlags(&ctx->c.stream, hipStreamNonBlocking));
+        ZJAI_HIP(hipEventCreate(&ctx->c.ev0));
+        ZJAI_HIP(hipEventCreate(&ctx->c.ev1));
+    });
+    if (rc != ZJAI_OK) {
+        delete ctx;
+        return rc;
+    }
+    *out = ctx;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_ctx_destroy(zjai_ctx* ctx) {
+    if (!ctx) return ZJAI_OK;
+    if (ctx->c.stream) (void)hipStreamSynchronize(ctx->c.stream);
+    if (ctx->c.ev0) (void)hipEventDestroy(ctx->c.ev0);
+    if (ctx->c.ev1) (void)hipEventDestroy(ctx->c.ev1);
+    if (ctx->c.stream) (void)hipStreamDestroy(ctx->c.stream);
+    delete ctx;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_last_error(const zjai_ctx* ctx, char* buf, size_t len) {
+    if (!buf || len == 0) return ZJAI_E_INVALID_ARGUMENT;
+    std::string m;
+    if (ctx) m = ctx->c.last_error;
+    else {
+        std::lock_guard<std::mutex> g(g_err_mu);
+        m = g_err;
+    }
+    const size_t n = std::min(len - 1, m.size());
+    std::memcpy(buf, m.data(), n);
+    buf[n] = 0;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_sync(zjai_ctx* ctx) {
+    if (!ctx) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] { ZJAI_HIP(hipStreamSynchronize(ctx->c.stream)); });
+}
+
+extern "C" int32_t zjai_set_stop(zjai_ctx* ctx, int32_t stop) {
+    if (!ctx) return ZJAI_E_INVALID_ARGUMENT;
+    ctx->c.stop = stop;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_get_stats(zjai_ctx* ctx, zjai_stats* out) {
+    if (!ctx || !out) return ZJAI_E_INVALID_ARGUMENT;
+    out->last_run_ms = ctx->c.last_ms;
+    out->kernel_launches = ctx->c.launches;
+    out->pool_in_use = ctx->c.pool.in_use();
+    out->pool_peak = ctx->c.pool.peak();
+    out->pool_cached = ctx->c.pool.cached();
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_release_buffers(zjai_ctx* ctx) {
+    if (!ctx) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
+        ctx->c.pool.trim();
+    });
+}
+
+// -------------------------------------------------------------------------------- tensors
+extern "C" int32_t zjai_tensor_create(zjai_ctx* ctx, int32_t c, int32_t h, int32_t w,
+                                      int32_t precision, zjai_tensor** out) {
+    if (!ctx || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(precision >= DT_F32 && precision <= DT_BF16, "precision");
+        need(c > 0 && h > 0 && w > 0, "bad shape");
+        TensorP t = ctx->c.alloc(c, h, w, precision);
+        ZJAI_HIP(hipMemsetAsync(t->v.p, 0, (size_t)h * t->v.row * dtype_size(precision), ctx->c.stream));
+        *out = new zjai_tensor{t};
+    });
+}
+
+extern "C" int32_t zjai_tensor_from_planar(zjai_ctx* ctx, const float* data, int32_t c, int32_t h,
+                                           int32_t w, int32_t precision, zjai_tensor** out) {
+    if (!ctx || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] { *out = new zjai_tensor{planar_upload(ctx->c, data, c, h, w, precision)}; });
+}
+
+extern "C" int32_t zjai_tensor_to_planar(zjai_ctx* ctx, const zjai_tensor* t, float* data, size_t len) {
+    if (!ctx || !t || !data) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        const Tensor& x = *t->t;
+        const size_t n = (size_t)x.c * x.h * x.w;
+        need(len >= n, "output buffer too small");
+        if (n == 0) return;
+        float* stage = (float*)ctx->c.pool.alloc(n * 4);
+        std::shared_ptr<void> keep(stage, [ctx](void* q) { ctx->c.pool.release(q); });
+        ZJAI_HIP(launch_nhwc_to_planar(x.v, x.dtype, x.c, x.h, x.w, stage, ctx->c.stream));
+        ++ctx->c.launches;
+        ZJAI_HIP(hipMemcpyAsync(data, stage, n * 4, hipMemcpyDeviceToHost, ctx->c.stream));
+        ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
+    });
+}
+
+extern "C" int32_t zjai_tensor_shape(const zjai_tensor* t, int32_t* c, int32_t* h, int32_t* w,
+                                     int32_t* precision) {
+    if (!t) return ZJAI_E_INVALID_ARGUMENT;
+    if (c) *c = t->t->c;
+    if (h) *h = t->t->h;
+    if (w) *w = t->t->w;
+    if (precision) *precision = t->t->dtype;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_tensor_crop(zjai_ctx* ctx, const zjai_tensor* t, int32_t h, int32_t w,
+                                    zjai_tensor** out) {
+    if (!ctx || !t || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] { *out = new zjai_tensor{crop_view(t->t, h, w)}; });
+}
+
+extern "C" int32_t zjai_tensor_cat(zjai_ctx* ctx, const zjai_tensor* const* parts, int32_t n,
+                                   zjai_tensor** out) {
+    if (!ctx || !parts || n <= 0 || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        int c = 0;
+        const Tensor& f = *parts[0]->t;
+        for (int i = 0; i < n; ++i) {
+            const Tensor& p = *parts[i]->t;
+            need(p.h == f.h && p.w == f.w && p.dtype == f.dtype, "cat: shapes differ");
+            need(p.c % 4 == 0, "cat: channel counts must be multiples of 4");
+            c += p.c;
+        }
+        TensorP y = ctx->c.alloc(c, f.h, f.w, f.dtype);
+        int c0 = 0;
+        for (int i = 0; i < n; ++i) {
+            const Tensor& p = *parts[i]->t;
+            ZJAI_HIP(launch_copy(p.v, channel_view(y, c0, p.c)->v, p.dtype, p.c, p.h, p.w, ctx->c.stream));
+            ++ctx->c.launches;
+            c0 += p.c;
+        }
+        *out = new zjai_tensor{y};
+    });
+}
+
+extern "C" int32_t zjai_tensor_destroy(zjai_tensor* t) {
+    delete t;
+    return ZJAI_OK;
+}
+
+// --------------------------------------------------------------------------------- layers
+extern "C" int32_t zjai_conv2d_create(zjai_ctx* ctx, int32_t in_ch, int32_t out_ch, int32_t kh,
+                                      int32_t kw, int32_t stride, int32_t pad_h, int32_t pad_w,
+                                      int32_t groups, const float* weight, const float* bias,
+                                      const int32_t* extra_pad, int32_t precision, zjai_layer** out) {
+    if (!ctx || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        *out = new zjai_layer{make_conv(ctx->c, in_ch, out_ch, kh, kw, stride, pad_h, pad_w, groups, weight,
+                                        bias, extra_pad, precision, false)};
+    });
+}
+
+extern "C" int32_t zjai_conv_transpose2d_create(zjai_ctx* ctx, int32_t in_ch, int32_t out_ch, int32_t k,
+                                                int32_t stride, int32_t pad, int32_t out_pad,
+                                                const float* weight, const float* bias,
+                                                int32_t precision, zjai_layer** out) {
+    if (!ctx || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        *out = new zjai_layer{make_conv_transpose(ctx->c, in_ch, out_ch, k, stride, pad, out_pad, weight, bias,
+                                                  precision)};
+    });
+}
+
+extern "C" int32_t zjai_layer_destroy(zjai_layer* layer) {
+    delete layer;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_conv_forward(zjai_ctx* ctx, const zjai_layer* layer, const zjai_tensor* x,
+                                     zjai_tensor** out) {
+    if (!ctx || !layer || !x || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] { *out = new zjai_tensor{conv_forward(ctx->c, *layer->l, x->t, Epilogue{})}; });
+}
+
+extern "C" int32_t zjai_conv_forward_fused(zjai_ctx* ctx, const zjai_layer* layer, const zjai_tensor* x,
+                                           int32_t act, int32_t res, const zjai_tensor* r1,
+                                           const zjai_tensor* r2, int32_t pixel_shuffle,
+                                           int32_t relu6_input, zjai_tensor** out) {
+    if (!ctx || !layer || !x || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(act >= ACT_NONE && act <= ACT_SIGMOID, "act");
+        need(res >= RES_NONE && res <= RES_MUL, "res");
+        Epilogue e;
+        e.act = act;
+        e.res = res;
+        e.r1 = r1 ? r1->t.get() : nullptr;
+        e.r2 = r2 ? r2->t.get() : nullptr;
+        e.ps = pixel_shuffle <= 0 ? 1 : pixel_shuffle;
+        e.relu6_in = relu6_input ? 1 : 0;
+        *out = new zjai_tensor{conv_forward(ctx->c, *layer->l, x->t, e)};
+    });
+}
+
+// ---------------------------------------------------------------------------- elementwise
+static int32_t eltwise(zjai_ctx* ctx, int op, zjai_tensor* x, const zjai_tensor* s) {
+    if (!ctx || !x) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        const Tensor& a = *x->t;
+        if (op >= EL_ADD) {
+            need(s != nullptr, "second operand missing");
+            const Tensor& b = *s->t;
+            need(a.c == b.c && a.h == b.h && a.w == b.w && a.dtype == b.dtype, "shapes differ");
+        }
+        need(a.c % 4 == 0, "channel count must be a multiple of 4");
+        ZJAI_HIP(launch_eltwise(op, a.v, s ? s->t->v : a.v, a.dtype, a.c, a.h, a.w, ctx->c.stream));
+        ++ctx->c.launches;
+    });
+}
+
+extern "C" int32_t zjai_relu(zjai_ctx* ctx, zjai_tensor* x) { return eltwise(ctx, EL_RELU, x, nullptr); }
+extern "C" int32_t zjai_relu6(zjai_ctx* ctx, zjai_tensor* x) { return eltwise(ctx, EL_RELU6, x, nullptr); }
+extern "C" int32_t zjai_leaky_relu(zjai_ctx* ctx, zjai_tensor* x) { return eltwise(ctx, EL_LEAKY, x, nullptr); }
+extern "C" int32_t zjai_sigmoid(zjai_ctx* ctx, zjai_tensor* x) { return eltwise(ctx, EL_SIGMOID, x, nullptr); }
+extern "C" int32_t zjai_add_assign(zjai_ctx* ctx, zjai_tensor* d, const zjai_tensor* s) { return eltwise(ctx, EL_ADD, d, s); }
+extern "C" int32_t zjai_gate(zjai_ctx* ctx, zjai_tensor* x, const zjai_tensor* m) { return eltwise(ctx, EL_GATE, x, m); }
+extern "C" int32_t zjai_mul_assign(zjai_ctx* ctx, zjai_tensor* a, const zjai_tensor* b) { return eltwise(ctx, EL_MUL, a, b); }
+extern "C" int32_t zjai_elu_gate(zjai_ctx* ctx, zjai_tensor* a, const zjai_tensor* b) { return eltwise(ctx, EL_ELU_GATE, a, b); }
+
+extern "C" int32_t zjai_pixel_shuffle(zjai_ctx* ctx, const zjai_tensor* x, int32_t r, zjai_tensor** out) {
+    if (!ctx || !x || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        const Tensor& a = *x->t;
+        need(r > 0 && a.c % (r * r) == 0, "pixel_shuffle: channels not divisible by r^2");
+        const int co = a.c / (r * r);
+        need(co % 4 == 0, "pixel_shuffle: output channels must be a multiple of 4");
+        TensorP y = ctx->c.alloc(co, a.h * r, a.w * r, a.dtype);
+        ZJAI_HIP(launch_pixel_shuffle(a.v, y->v, a.dtype, co, a.h, a.w, r, ctx->c.stream));
+        ++ctx->c.launches;
+        *out = new zjai_tensor{y};
+    });
+}
+
+extern "C" int32_t zjai_layer_norm_channels(zjai_ctx* ctx, const zjai_tensor* x, const float* weight,
+                                            const float* bias, zjai_tensor** out) {
+    if (!ctx || !x || !weight || !bias || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        const Tensor& a = *x->t;
+        need(a.c % 4 == 0, "layer norm: channel count must be a multiple of 4");
+        float* d = (float*)ctx->c.pool.alloc(sizeof(float) * 2 * a.c);
+        std::shared_ptr<void> keep(d, [ctx](void* q) { ctx->c.pool.release(q); });
+        ZJAI_HIP(hipMemcpyAsync(d, weight, sizeof(float) * a.c, hipMemcpyHostToDevice, ctx->c.stream));
+        ZJAI_HIP(hipMemcpyAsync(d + a.c, bias, sizeof(float) * a.c, hipMemcpyHostToDevice, ctx->c.stream));
+        TensorP y = ctx->c.alloc(a.c, a.h, a.w, a.dtype);
+        ZJAI_HIP(launch_layer_norm(a.v, y->v, a.dtype, a.c, a.h, a.w, d, d + a.c, ctx->c.stream));
+        ++ctx->c.launches;
+        ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
+        *out = new zjai_tensor{y};
+    });
+}
+
+extern "C" int32_t zjai_channel_attention(zjai_ctx* ctx, const zjai_tensor* qkv, int32_t heads,
+                                          const float* temperature, zjai_tensor** out) {
+    if (!ctx || !qkv || !temperature || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        const Tensor& a = *qkv->t;
+        need(heads > 0 && a.c % (3 * heads) == 0, "attention: channel / head counts");
+        const int dim = a.c / 3, c = dim / heads;
+        need(dim % 8 == 0, "attention: dim must be a multiple of 8");
+        need(heads * (c * c + 2 * c) <= 256 * 20, "attention: head size too large");
+        // attn . v as a 1x1 conv over v with the block-diagonal attention matrix as its weight
+        // (identity projection folded in).
+        std::vector<float> eye((size_t)dim * dim, 0.0f);
+        for (int i = 0; i < dim; ++i) eye[(size_t)i * dim + i] = 1.0f;
+        LayerP L = make_conv(ctx->c, dim, dim, 1, 1, 1, 0, 0, 1, eye.data(), nullptr, nullptr, a.dtype, true);
+        float* temp = (float*)ctx->c.pool.alloc(sizeof(float) * heads);
+        std::shared_ptr<void> kt(temp, [ctx](void* q) { ctx->c.pool.release(q); });
+        ZJAI_HIP(hipMemcpyAsync(temp, temperature, sizeof(float) * heads, hipMemcpyHostToDevice, ctx->c.stream));
+        const int nchunk = attention_gram_chunks(a.h, a.w);
+        const int total = heads * (c * c + 2 * c);
+        double* partial = (double*)ctx->c.pool.alloc(sizeof(double) * (size_t)std::max(nchunk, 1) * total);
+        std::shared_ptr<void> kp(partial, [ctx](void* q) { ctx->c.pool.release(q); });
+        float* scratch = (float*)ctx->c.pool.alloc(sizeof(float) * (size_t)(dim * c + dim * dim));
+        std::shared_ptr<void> ks(scratch, [ctx](void* q) { ctx->c.pool.release(q); });
+        ZJAI_HIP(launch_attention_gram(a.v, a.dtype, dim, heads, a.h, a.w, partial, ctx->c.stream));
+        ZJAI_HIP(launch_attention_softmax_fold(partial, nchunk, dim, heads, temp, L->w_f32, scratch,
+                                               scratch + dim * c, ctx->c.stream));
+        ctx->c.launches += 2;
+        pack_1x1_device(ctx->c, *L, scratch + dim * c);
+        TensorP y = conv_forward(ctx->c, *L, channel_view(qkv->t, 2 * dim, dim), Epilogue{});
+        ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
+        *out = new zjai_tensor{y};
+    });
+}
+
+// ----------------------------------------------------------------------------------- nets
+extern "C" int32_t zjai_net_create(zjai_ctx* ctx, int32_t op, int32_t component, int32_t precision,
+                                   int32_t n_tensors, const char* const* names, const int32_t* ndims,
+                                   const int32_t* dims, const float* const* data, zjai_net** out) {
+    if (!ctx || !out || n_tensors < 0 || (n_tensors && (!names || !ndims || !dims || !data)))
+        return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(precision >= DT_F32 && precision <= DT_BF16, "precision");
+        std::map<std::string, Param> P;
+        const int32_t* d = dims;
+        for (int i = 0; i < n_tensors; ++i) {
+            need(names[i] != nullptr && ndims[i] >= 0 && ndims[i] <= 8, "tensor descriptor");
+            Param p;
+            p.shape.assign(d, d + ndims[i]);
+            d += ndims[i];
+            p.data = data[i];
+            P[names[i]] = p;
+        }
+        *out = new zjai_net{build_net(ctx->c, op, component, precision, P)};
+    });
+}
+
+extern "C" int32_t zjai_net_destroy(zjai_net* net) {
+    delete net;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_net_out_size(const zjai_net* net, int32_t h, int32_t w, int32_t* oh, int32_t* ow) {
+    if (!net || !oh || !ow || h <= 0 || w <= 0) return ZJAI_E_INVALID_ARGUMENT;
+    if (net->n->comp == COMP_Y) primary_out_size(net->n->op, h, w, oh, ow);
+    else secondary_out_size(net->n->op, h, w, oh, ow);
+    return ZJAI_OK;
+}
+
+static void run_to_host(zjai_ctx* ctx, const zjai_net* net, const TensorP& a, const TensorP& b, int h, int w,
+                        float* out, size_t len) {
+    const bool primary = net->n->comp == COMP_Y;
+    int oh, ow;
+    if (primary) primary_out_size(net->n->op, h, w, &oh, &ow);
+    else secondary_out_size(net->n->op, h, w, &oh, &ow);
+    const int planes = primary ? 1 : 2;
+    const size_t n = (size_t)planes * oh * ow;
+    need(out && len >= n, "output buffer too small");
+    need(h > 0 && w > 0, "target size");
+    float* dev = (float*)ctx->c.pool.alloc(n * 4);
+    std::shared_ptr<void> keep(dev, [ctx](void* q) { ctx->c.pool.release(q); });
+    PlaneOut po;
+    po.plane = dev;
+    po.row = ow;
+    po.cstride = (long long)oh * ow;
+    po.win_h = oh;
+    po.win_w = ow;
+    if (primary) primary_forward(ctx->c, *net->n, a, h, w, po);
+    else secondary_forward(ctx->c, *net->n, a, b, h, w, po);
+    ZJAI_HIP(hipMemcpyAsync(out, dev, n * 4, hipMemcpyDeviceToHost, ctx->c.stream));
+    ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
+}
+
+extern "C" int32_t zjai_primary_forward(zjai_ctx* ctx, const zjai_net* net, const zjai_tensor* y_hat,
+                                        int32_t h, int32_t w, float* out, size_t len) {
+    if (!ctx || !net || !y_hat) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(net->n->comp == COMP_Y, "not a primary net");
+        need(y_hat->t->dtype == net->n->dtype, "latent precision differs from the net");
+        run_to_host(ctx, net, y_hat->t, nullptr, h, w, out, len);
+    });
+}
+
+extern "C" int32_t zjai_secondary_forward(zjai_ctx* ctx, const zjai_net* net, const zjai_tensor* y_luma,
+                                          const zjai_tensor* y_chroma, int32_t h, int32_t w, float* out,
+                                          size_t len) {
+    if (!ctx || !net || !y_luma || !y_chroma) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(net->n->comp == COMP_UV, "not a secondary net");
+        run_to_host(ctx, net, y_luma->t, y_chroma->t, h, w, out, len);
+    });
+}
+
+// ------------------------------------------------------------------------ tiling geometry
+// synthesis_tiles / region_tiles / latent_extent (src/tools/tiles.rs:39-229) and the image
+// region grid of independent regions (src/tools/regions.rs:47-150).
+namespace {
+
+struct Area {
+    int x, y, w, h;
+};
+
+bool contains(const Area& r, int x, int y) { return r.x <= x && x < r.x + r.w && r.y <= y && y < r.y + r.h; }
+
+int latent_extent(int pos, int len, int latent_len) {
+    if (len % 16 && ceil_div(pos + len, 16) < latent_len)
+        throw Error(ZJAI_E_INVALID_ARGUMENT, "unaligned synthesis tile inside the picture");
+    return ceil_div(len, 16);
+}
+
+std::vector<std::pair<int, int>> axis_coords(int size, int n) {
+    const int region = (ceil_div(size, 128) / n) * 128;
+    std::vector<std::pair<int, int>> out;
+    for (int i = 0; i < n; ++i) out.push_back({i * region, i + 1 < n ? (i + 1) * region : size});
+    return out;
+}
+
+}  // namespace
+
+extern "C" int32_t zjai_synthesis_tiles(int32_t height, int32_t width, int32_t latent_h, int32_t latent_w,
+                                        int32_t tile_size, int32_t overlap, int32_t region_rows,
+                                        int32_t region_cols, zjai_tile* tiles, int32_t cap, int32_t* n) {
+    if (!n || height <= 0 || width <= 0 || latent_h <= 0 || latent_w <= 0 || cap < 0 || (cap && !tiles))
+        return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] {
+        std::vector<zjai_tile> out;
+        auto push = [&](Area img, Area lat, Area core, int ox, int oy) {
+            out.push_back(zjai_tile{img.x, img.y, img.w, img.h, lat.x, lat.y, lat.w, lat.h, core.x, core.y,
+                                    core.w, core.h, ox, oy});
+        };
+        if (tile_size <= 0) {
+            Area img{0, 0, width, height};
+            push(img, Area{0, 0, latent_w, latent_h}, img, 0, 0);
+        } else {
+            const int tile_h = std::min(tile_size, height), tile_w = std::min(tile_size, width);
+            const int half = overlap / 2;
+            if (region_rows > 0 && region_cols > 0) {
+                std::vector<Area> regions;
+                for (auto& vy : axis_coords(height, region_rows))
+                    for (auto& vx : axis_coords(width, region_cols))
+                        regions.push_back(Area{vx.first, vy.first, vx.second - vx.first, vy.second - vy.first});
+                for (int ty = 0; ty < height; ty += tile_h)
+                    for (int tx = 0; tx < width; tx += tile_w) {
+                        int x = tx, y = ty, w = std::min(tile_w, width - tx), h = std::min(tile_h, height - ty);
+                        const int x_end = x + w - 1, y_end = y + h - 1;
+                        for (const Area& r : regions) {
+                            if (!(contains(r, x, y) && contains(r, x_end, y_end))) continue;
+                            if (y > r.y) {
+                                if (y < half) throw Error(ZJAI_E_INVALID_ARGUMENT, "tile overlap");
+                                y -= half;
+                                h += half;
+                            }
+                            if (x > r.x) {
+                                if (x < half) throw Error(ZJAI_E_INVALID_ARGUMENT, "tile overlap");
+                                x -= half;
+                                w += half;
+                            }
+                            if (y_end < r.y + r.h - 1) h += std::min(half, std::max(height - (y + h), 0));
+                            if (x_end < r.x + r.w - 1) w += std::min(half, std::max(width - (x + w), 0));
+                        }
+                        if (x + w > width || y + h > height)
+                            throw Error(ZJAI_E_INVALID_ARGUMENT, "synthesis tile outside the picture");
+                        Area lat{x / 16, y / 16, latent_extent(x, w, latent_w), latent_extent(y, h, latent_h)};
+                        if (lat.x + lat.w > latent_w || lat.y + lat.h > latent_h)
+                            throw Error(ZJAI_E_INVALID_ARGUMENT, "synthesis tile outside the latent");
+                        int cx = x, cy = y, cw = w, chh = h, left = 0, top = 0;
+                        const int bx = x + w - 1, by = y + h - 1;
+                        for (const Area& r : regions) {
+                            if (!(contains(r, cx, cy) && contains(r, bx, by))) continue;
+                            if (cy > r.y) {
+                                top += half;
+                                cy += half;
+                                if (chh < half) throw Error(ZJAI_E_INVALID_ARGUMENT, "tile overlap");
+                                chh -= half;
+                            }
+                            if (cx > r.x) {
+                                left += half;
+                                cx += half;
+                                if (cw < half) throw Error(ZJAI_E_INVALID_ARGUMENT, "tile overlap");
+                                cw -= half;
+                            }
+                            chh = std::min(chh, tile_h);
+                            cw = std::min(cw, tile_w);
+                        }
+                        if (cw == 0 || chh == 0 || left + cw > w || top + chh > h)
+                            throw Error(ZJAI_E_INVALID_ARGUMENT, "synthesis tile is all overlap");
+                        push(Area{x, y, w, h}, lat, Area{cx, cy, cw, chh}, left, top);
+                    }
+            } else {
+                if (tile_h <= overlap || tile_w <= overlap)
+                    throw Error(ZJAI_E_INVALID_ARGUMENT, "synthesis tile not larger than its overlap");
+                for (int y = 0; y < height - overlap; y += tile_h - overlap)
+                    for (int x = 0; x < width - overlap; x += tile_w - overlap) {
+                        Area img{x, y, std::min(tile_w, width - x), std::min(tile_h, height - y)};
+                        Area lat{x / 16, y / 16, latent_extent(img.x, img.w, latent_w),
+                                 latent_extent(img.y, img.h, latent_h)};
+                        if (lat.x + lat.w > latent_w || lat.y + lat.h > latent_h)
+                            throw Error(ZJAI_E_INVALID_ARGUMENT, "synthesis tile outside the latent");
+                        const int left = img.x == 0 ? 0 : half, top = img.y == 0 ? 0 : half;
+                        const int right = img.x + img.w >= width ? 0 : half;
+                        const int bottom = img.y + img.h >= height ? 0 : half;
+                        if (img.w <= left + right || img.h <= top + bottom)
+                            throw Error(ZJAI_E_INVALID_ARGUMENT, "synthesis tile is all overlap");
+                        push(img, lat, Area{img.x + left, img.y + top, img.w - left - right, img.h - top - bottom},
+                             left, top);
+                    }
+            }
+        }
+        *n = (int32_t)out.size();
+        if ((int)out.size() > cap) throw Error(ZJAI_E_LIMIT, "tile buffer too small");
+        std::copy(out.begin(), out.end(), tiles);
+    });
+}
+
+// --------------------------------------------------------------------------------- picture
+struct zjai_picture {
+    NetP net_y, net_uv;
+    int lh = 0, lw = 0, height = 0, width = 0, sv = 1, sh = 1, out_h = 0, out_w = 0, bit_depth = 0;
+    std::vector<zjai_tile> tiles;
+    float* y_hat = nullptr;   // device planar [160][lh][lw]
+    float* uv_hat = nullptr;  // device planar [96][lh][lw]
+    void* out_y = nullptr;    // device planes
+    void* out_uv = nullptr;   // [2][ch][cw]
+    bool uploaded = false;
+    ~zjai_picture() {
+        if (y_hat) (void)hipFree(y_hat);
+        if (uv_hat) (void)hipFree(uv_hat);
+        if (out_y) (void)hipFree(out_y);
+        if (out_uv) (void)hipFree(out_uv);
+    }
+    size_t sample_bytes() const { return bit_depth ? 2 : 4; }
+    int ch() const { return ceil_div(out_h, sv); }
+    int cw() const { return ceil_div(out_w, sh); }
+};
+
+extern "C" int32_t zjai_picture_create(zjai_ctx* ctx, const zjai_net* net_y, const zjai_net* net_uv,
+                                       int32_t lh, int32_t lw, int32_t height, int32_t width,
+                                       const zjai_tile* tiles, int32_t n_tiles, int32_t sv, int32_t sh,
+                                       int32_t out_h, int32_t out_w, int32_t bit_depth, zjai_picture** out) {
+    if (!ctx || !net_y || !out || !tiles || n_tiles <= 0) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(net_y->n->comp == COMP_Y, "net_y is not a primary net");
+        need(!net_uv || (net_uv->n->comp == COMP_UV && net_uv->n->op == net_y->n->op), "net_uv mismatch");
+        need(!net_uv || net_uv->n->dtype == net_y->n->dtype, "nets differ in precision");
+        need(lh > 0 && lw > 0 && height > 0 && width > 0, "sizes");
+        need(sv >= 1 && sv <= 2 && sh >= 1 && sh <= 2, "chroma subsampling");
+        need(out_h > 0 && out_w > 0 && out_h <= height && out_w <= width, "displayed size");
+        need(bit_depth == 0 || (bit_depth >= 8 && bit_depth <= 16), "bit depth");
+        auto* p = new zjai_picture();
+        std::unique_ptr<zjai_picture> own(p);
+        p->net_y = net_y->n;
+        if (net_uv) p->net_uv = net_uv->n;
+        p->lh = lh; p->lw = lw; p->height = height; p->width = width; p->sv = sv; p->sh = sh;
+        p->out_h = out_h; p->out_w = out_w; p->bit_depth = bit_depth;
+        p->tiles.assign(tiles, tiles + n_tiles);
+        for (const zjai_tile& t : p->tiles) {
+            need(t.latent_x >= 0 && t.latent_y >= 0 && t.latent_w > 0 && t.latent_h > 0 &&
+                     t.latent_x + t.latent_w <= lw && t.latent_y + t.latent_h <= lh,
+                 "tile latent window outside the latent");
+            need(t.image_w > 0 && t.image_h > 0 && t.core_w > 0 && t.core_h > 0, "tile sizes");
+            int oh, ow;
+            primary_out_size(p->net_y->op, t.image_h, t.image_w, &oh, &ow);
+            need(t.core_off_y >= 0 && t.core_off_x >= 0 && t.core_off_y + t.core_h <= oh &&
+                     t.core_off_x + t.core_w <= ow,
+                 "synthesis tile smaller than its core");
+            need(t.core_x >= 0 && t.core_y >= 0, "tile core position");
+        }
+        ZJAI_HIP(hipMalloc(&p->y_hat, sizeof(float) * 160 * (size_t)lh * lw));
+        if (p->net_uv) ZJAI_HIP(hipMalloc(&p->uv_hat, sizeof(float) * 96 * (size_t)lh * lw));
+        ZJAI_HIP(hipMalloc(&p->out_y, p->sample_bytes() * (size_t)out_h * out_w));
+        ZJAI_HIP(hipMemset(p->out_y, 0, p->sample_bytes() * (size_t)out_h * out_w));
+        if (p->net_uv) {
+            ZJAI_HIP(hipMalloc(&p->out_uv, p->sample_bytes() * 2 * (size_t)p->ch() * p->cw()));
+            ZJAI_HIP(hipMemset(p->out_uv, 0, p->sample_bytes() * 2 * (size_t)p->ch() * p->cw()));
+        }
+        *out = own.release();
+    });
+}
+
+extern "C" int32_t zjai_picture_destroy(zjai_picture* pic) {
+    delete pic;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_picture_upload(zjai_ctx* ctx, zjai_picture* pic, const float* y_hat, const float* uv_hat) {
+    if (!ctx || !pic || !y_hat) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(!pic->net_uv || uv_hat, "chroma latent missing");
+        ZJAI_HIP(hipMemcpyAsync(pic->y_hat, y_hat, sizeof(float) * 160 * (size_t)pic->lh * pic->lw,
+                                hipMemcpyHostToDevice, ctx->c.stream));
+        if (pic->net_uv)
+            ZJAI_HIP(hipMemcpyAsync(pic->uv_hat, uv_hat, sizeof(float) * 96 * (size_t)pic->lh * pic->lw,
+                                    hipMemcpyHostToDevice, ctx->c.stream));
+        ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
+        pic->uploaded = true;
+    });
+}
+
+extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
+    if (!ctx || !pic) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(pic->uploaded, "latents not uploaded");
+        Context& c = ctx->c;
+        const int dt = pic->net_y->dtype;
+        ZJAI_HIP(hipEventRecord(c.ev0, c.stream));
+        for (const zjai_tile& t : pic->tiles) {
+            c.check_stop();
+            TensorP by = c.alloc(160, t.latent_h, t.latent_w, dt);
+            ZJAI_HIP(launch_planar_to_nhwc(pic->y_hat, 160, pic->lh, pic->lw, t.latent_x, t.latent_y, t.latent_h,
+                                           t.latent_w, by->v, dt, c.stream));
+            ++c.launches;
+            // synthesize_luma_into (src/decoder/reconstruct.rs:379-411): core rows/cols that
+            // fall inside the displayed picture.
+            PlaneOut py;
+            py.plane = pic->out_y;
+            py.row = pic->out_w;
+            py.win_y0 = t.core_off_y;
+            py.win_x0 = t.core_off_x;
+            py.win_h = std::min(t.core_h, std::max(pic->out_h - t.core_y, 0));
+            py.win_w = std::min(t.core_w, std::max(pic->out_w - t.core_x, 0));
+            py.dst_y0 = t.core_y;
+            py.dst_x0 = t.core_x;
+            py.bit_depth = pic->bit_depth;
+            primary_forward(c, *pic->net_y, by, t.image_h, t.image_w, py);
+            if (pic->net_uv) {
+                TensorP buv = c.alloc(96, t.latent_h, t.latent_w, dt);
+                ZJAI_HIP(launch_planar_to_nhwc(pic->uv_hat, 96, pic->lh, pic->lw, t.latent_x, t.latent_y,
+                                               t.latent_h, t.latent_w, buv->v, dt, c.stream));
+                ++c.launches;
+                // synthesize_chroma_into (src/decoder/reconstruct.rs:416-464)
+                PlaneOut pu = py;
+                pu.plane = pic->out_uv;
+                pu.row = pic->cw();
+                pu.cstride = (long long)pic->ch() * pic->cw();
+                pu.sv = pic->sv;
+                pu.sh = pic->sh;
+                secondary_forward(c, *pic->net_uv, by, buv, t.image_h, t.image_w, pu);
+            }
+        }
+        ZJAI_HIP(hipEventRecord(c.ev1, c.stream));
+        ZJAI_HIP(hipEventSynchronize(c.ev1));
+        ZJAI_HIP(hipEventElapsedTime(&c.last_ms, c.ev0, c.ev1));
+    });
+}
+
+extern "C" int32_t zjai_picture_download(zjai_ctx* ctx, zjai_picture* pic, void* y, void* u, void* v) {
+    if (!ctx || !pic || !y) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        const size_t sb = pic->sample_bytes();
+        ZJAI_HIP(hipMemcpyAsync(y, pic->out_y, sb * (size_t)pic->out_h * pic->out_w, hipMemcpyDeviceToHost,
+                                ctx->c.stream));
+        if (pic->net_uv) {
+            need(u && v, "chroma outputs missing");
+            const size_t n = (size_t)pic->ch() * pic->cw();
+            ZJAI_HIP(hipMemcpyAsync(u, pic->out_uv, sb * n, hipMemcpyDeviceToHost, ctx->c.stream));
+            ZJAI_HIP(hipMemcpyAsync(v, (char*)pic->out_uv + sb * n, sb * n, hipMemcpyDeviceToHost, ctx->c.stream));
+        }
+        ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
+    });
+}

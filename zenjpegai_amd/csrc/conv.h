@@ -1,0 +1,67 @@
+// Launch description of the implicit-GEMM convolution kernels (host and device).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "device.h"
+
+namespace zjai {
+
+// Activation applied to the accumulator before the residual operation.
+enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_LEAKY = 2, ACT_SIGMOID = 3 };
+
+// Residual operation of the epilogue (r1, r2 are views with the output's geometry):
+//   RES_ADD  y = a + r1                   (ResidualBlock / LightResidualBlock / TAM skip)
+//   RES_GATE y = r1 * (1 + a)             (ResAU gate, src/nn/fast/layers.rs:195-201)
+//   RES_CAB  y = r1 * sigmoid(a) + r2     (CAB, src/model/attention.rs:130-137)
+//   RES_MUL  y = r1 * a
+enum Res : int { RES_NONE = 0, RES_ADD = 1, RES_GATE = 2, RES_CAB = 3, RES_MUL = 4 };
+
+// Where the epilogue writes.
+enum Out : int { OUT_NHWC = 0, OUT_PLANE = 1 };
+
+struct ConvParams {
+    // Input view and its valid extent (reads outside [0,H) x [0,W) are zero padding).
+    View x;
+    int H, W;
+    // Output extent in conv-output coordinates (before pixel shuffle).
+    int OH, OW;
+    View y;  // OUT_NHWC destination (after pixel shuffle)
+    // Packed weights: [phase][group][chunk][nblk][tap][16][CK] in the storage type; bias f32.
+    const void* w;
+    const float* bias;
+    int cin_g, cout_g, groups, nchunks, nblk_g;
+    long long phase_stride;  // elements between phases (transposed conv)
+    int pad_t, pad_l;
+    int relu6_in;  // clamp(x, 0, 6) on load (ResAU's relu6)
+    // Epilogue.
+    int act, res;
+    View r1, r2;
+    int ps;  // pixel shuffle factor (1 = none)
+    int out_mode;
+    // OUT_PLANE: planar destination. Channel c of the (shuffled) output goes to
+    // plane + c * pl_cstride; the kept window [win_y0, win_y0 + win_h) x [win_x0, ...) of the
+    // output lands at (dst_y0, dst_x0), keeping rows/cols that are multiples of sv / sh.
+    void* plane;
+    long long pl_row, pl_cstride;
+    int win_y0, win_x0, win_h, win_w, dst_y0, dst_x0, sv, sh;
+    int denorm;     // x * 128 + 127.5 clamped to [0, 255]
+    int bit_depth;  // 0: store f32; else quantise to u16 at this depth
+    // Transposed conv (stride 2): tap tables per output phase (py * 2 + px).
+    int ntaps[4];
+    int tap_dy[4][4], tap_dx[4][4];
+};
+
+// Kernel configuration: waves along channels (WC) x along rows (WP), each wave CF channel
+// blocks of 16 x PF output rows of 16 columns.
+struct TileCfg {
+    int wc, wp, cf, pf;
+};
+
+enum ConvKind : int { CK_1x1 = 0, CK_2x2 = 1, CK_3x3 = 2, CK_3x3_S2 = 3, CK_T3 = 4 };
+
+hipError_t launch_conv(int kind, int dtype, TileCfg cfg, const ConvParams& p, hipStream_t s);
+bool conv_cfg_supported(int kind, int dtype, TileCfg cfg);
+
+}  // namespace zjai

@@ -1,0 +1,360 @@
+// Implicit-GEMM convolution on CDNA4 matrix cores (gfx950).
+//
+// One workgroup computes TY = WP*PF output rows x 16 output columns x NB = WC*CF blocks of 16
+// output channels. GEMM roles: M = output channels (the weights are the A operand), N = output
+// positions (the input halo is the B operand), K = input channels x taps.
+//
+// Per input-channel chunk (64 bytes of channels per pixel: 16 f32 or 32 f16/bf16) the workgroup
+// stages the input halo [HY][HX][64 B] and the packed weights [NB][taps][16][64 B] in LDS, then
+// every wave runs, per tap, one 16-byte LDS read per operand fragment and CF x PF MFMAs:
+//   f32:      4 x v_mfma_f32_16x16x4_f32 (lane group g holds channels 4g..4g+3)
+//   f16/bf16: 1 x v_mfma_f32_16x16x32_{f16,bf16} (lane group g holds channels 8g..8g+7)
+// A and B fragments use the same lane-group -> channel map, so each MFMA sums matching channels.
+// Accumulators start at the bias; the epilogue applies activation, residual op, pixel shuffle,
+// denormalisation and quantisation, and stores NHWC activations or planar picture samples.
+//
+// Transposed stride-2 convolutions run as four output phases (blockIdx.z & 3): each phase is a
+// stride-1 gather over the input with at most 2x2 taps whose input offsets lie in {-1, 0, 1},
+// so the halo is the 3x3 one and only the tap table differs.
+
+#include "conv.h"
+
+namespace zjai {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Mma;
+template <> struct Mma<float> {
+    static __device__ __forceinline__ void run(f32x4& acc, u32x4 a, u32x4 b) {
+        const f32x4 av = __builtin_bit_cast(f32x4, a), bv = __builtin_bit_cast(f32x4, b);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[0], bv[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[1], bv[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[2], bv[2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[3], bv[3], acc, 0, 0, 0);
+    }
+};
+template <> struct Mma<_Float16> {
+    static __device__ __forceinline__ void run(f32x4& acc, u32x4 a, u32x4 b) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                     __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
+    }
+};
+template <> struct Mma<__bf16> {
+    static __device__ __forceinline__ void run(f32x4& acc, u32x4 a, u32x4 b) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                      __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+    }
+};
+
+// clamp(v, 0, 6) on a 16-byte vector of the storage type (ResAU's relu6 on load).
+template <typename T> __device__ __forceinline__ u32x4 relu6_vec(u32x4 v);
+template <> __device__ __forceinline__ u32x4 relu6_vec<float>(u32x4 v) {
+    f32x4 f = __builtin_bit_cast(f32x4, v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float e = f[i];
+        e = e < 0.0f ? 0.0f : e;
+        e = e > 6.0f ? 6.0f : e;
+        f[i] = e;
+    }
+    return __builtin_bit_cast(u32x4, f);
+}
+template <> __device__ __forceinline__ u32x4 relu6_vec<_Float16>(u32x4 v) {
+    f16x8 h = __builtin_bit_cast(f16x8, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        _Float16 e = h[i];
+        e = e < (_Float16)0.0f ? (_Float16)0.0f : e;
+        e = e > (_Float16)6.0f ? (_Float16)6.0f : e;
+        h[i] = e;
+    }
+    return __builtin_bit_cast(u32x4, h);
+}
+template <> __device__ __forceinline__ u32x4 relu6_vec<__bf16>(u32x4 v) {
+    bf16x8 h = __builtin_bit_cast(bf16x8, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float e = (float)h[i];
+        e = e < 0.0f ? 0.0f : e;
+        e = e > 6.0f ? 6.0f : e;
+        h[i] = (__bf16)e;
+    }
+    return __builtin_bit_cast(u32x4, h);
+}
+
+__device__ __forceinline__ float apply_act(int act, float v) {
+    if (act == ACT_RELU) return fmaxf(v, 0.0f);
+    if (act == ACT_LEAKY) return v < 0.0f ? v * 0.01f : v;
+    if (act == ACT_SIGMOID) return sigmoidf_ref(v);
+    return v;
+}
+
+template <typename T>
+__device__ __forceinline__ void epilogue_store(const ConvParams& p, int oy, int ox, int oc0,
+                                               int nvalid, f32x4 v) {
+    // Activation, then the residual operation, each as separate IEEE operations.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = apply_act(p.act, v[i]);
+    if (p.res != RES_NONE) {
+        const long long o1 = (long long)oy * p.r1.row + (long long)ox * p.r1.cs + p.r1.c_off + oc0;
+        f32x4 r1;
+        if (nvalid == 4) {
+            r1 = load4<T>((const T*)p.r1.p + o1);
+        } else {
+            for (int i = 0; i < 4; ++i) r1[i] = i < nvalid ? to_f32(((const T*)p.r1.p)[o1 + i]) : 0.0f;
+        }
+        if (p.res == RES_ADD) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = v[i] + r1[i];
+        } else if (p.res == RES_GATE) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { const float g = 1.0f + v[i]; v[i] = r1[i] * g; }
+        } else if (p.res == RES_MUL) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = r1[i] * v[i];
+        } else if (p.res == RES_CAB) {
+            const long long o2 = (long long)oy * p.r2.row + (long long)ox * p.r2.cs + p.r2.c_off + oc0;
+            f32x4 r2;
+            if (nvalid == 4) {
+                r2 = load4<T>((const T*)p.r2.p + o2);
+            } else {
+                for (int i = 0; i < 4; ++i) r2[i] = i < nvalid ? to_f32(((const T*)p.r2.p)[o2 + i]) : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float s = sigmoidf_ref(v[i]);
+                const float t = r1[i] * s;
+                v[i] = t + r2[i];
+            }
+        }
+    }
+    if (p.out_mode == OUT_NHWC) {
+        T* y = (T*)p.y.p;
+        if (p.ps == 1) {
+            const long long o = (long long)oy * p.y.row + (long long)ox * p.y.cs + p.y.c_off + oc0;
+            if (nvalid == 4) {
+                store4<T>(y + o, v);
+            } else {
+                for (int i = 0; i < nvalid; ++i) y[o + i] = from_f32<T>(v[i]);
+            }
+        } else {
+            const int r = p.ps, rr = r * r;
+            for (int i = 0; i < nvalid; ++i) {
+                const int oc = oc0 + i, c = oc / rr, sub = oc - c * rr;
+                const int Y = oy * r + sub / r, X = ox * r + sub % r;
+                y[(long long)Y * p.y.row + (long long)X * p.y.cs + p.y.c_off + c] = from_f32<T>(v[i]);
+            }
+        }
+        return;
+    }
+    // Planar picture output (last layer): pixel shuffle, denormalise, crop to the kept window,
+    // chroma subsampling, f32 or quantised u16.
+    const int r = p.ps, rr = r * r;
+    for (int i = 0; i < nvalid; ++i) {
+        const int oc = oc0 + i, c = oc / rr, sub = oc - c * rr;
+        const int Y = oy * r + sub / r, X = ox * r + sub % r;
+        const int wy = Y - p.win_y0, wx = X - p.win_x0;
+        if (wy < 0 || wy >= p.win_h || wx < 0 || wx >= p.win_w) continue;
+        const int py = p.dst_y0 + wy, px = p.dst_x0 + wx;
+        if (py % p.sv || px % p.sh) continue;
+        float s = v[i];
+        if (p.denorm) {
+            s = s * 128.0f;
+            s = s + 127.5f;
+            s = s < 0.0f ? 0.0f : s;
+            s = s > 255.0f ? 255.0f : s;
+        }
+        const long long o = (long long)c * p.pl_cstride + (long long)(py / p.sv) * p.pl_row + px / p.sh;
+        if (p.bit_depth == 0) {
+            ((float*)p.plane)[o] = s;
+        } else {
+            // quantize_plane (src/decoder/output.rs:330-342): rint(clamp(x,0,255)/255*max).
+            const float mx = (float)((1u << p.bit_depth) - 1u);
+            float q = s < 0.0f ? 0.0f : s;
+            q = q > 255.0f ? 255.0f : q;
+            q = q / 255.0f;
+            q = q * mx;
+            q = rintf(q);
+            q = q < 0.0f ? 0.0f : q;
+            q = q > mx ? mx : q;
+            ((uint16_t*)p.plane)[o] = (uint16_t)q;
+        }
+    }
+}
+
+template <typename T, int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF>
+__global__ void __launch_bounds__(WC * WP * 64)
+conv_igemm(const ConvParams p) {
+    constexpr int NT = WC * WP * 64;
+    constexpr int TY = WP * PF;
+    constexpr int HY = (TY - 1) * S + KH;
+    constexpr int HX = 15 * S + KW;
+    constexpr int NTAP = TR ? 4 : KH * KW;
+    constexpr int NB = WC * CF;
+    constexpr int VEC = 16 / (int)sizeof(T);
+    constexpr int CK = 4 * VEC;
+    constexpr int HALO_U = HY * HX * 4;
+    constexpr int W_U = NB * NTAP * 64;
+    __shared__ u32x4 s_halo[HALO_U];
+    __shared__ u32x4 s_w[W_U];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wc = wave % WC, wp = wave / WC;
+    const int col = lane & 15, grp = lane >> 4;
+
+    const int nt = TR ? (int)(blockIdx.z >> 2) : (int)blockIdx.z;
+    const int phase = TR ? (int)(blockIdx.z & 3) : 0;
+    const int gb = nt * NB;
+    const int g = gb / p.nblk_g, nb0 = gb - g * p.nblk_g;
+    const int ox0 = blockIdx.x * 16, oy0 = blockIdx.y * TY;
+
+    int ntap = NTAP;
+    int tdy[NTAP], tdx[NTAP];
+#pragma unroll
+    for (int t = 0; t < NTAP; ++t) {
+        if (TR) {
+            tdy[t] = p.tap_dy[phase][t];
+            tdx[t] = p.tap_dx[phase][t];
+        } else {
+            tdy[t] = t / KW;
+            tdx[t] = t % KW;
+        }
+    }
+    if (TR) ntap = p.ntaps[phase];
+
+    f32x4 acc[CF][PF];
+#pragma unroll
+    for (int cf = 0; cf < CF; ++cf) {
+        const int ocl = (nb0 + wc * CF + cf) * 16 + grp * 4;
+        f32x4 b;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            b[i] = (p.bias && ocl + i < p.cout_g) ? p.bias[g * p.cout_g + ocl + i] : 0.0f;
+#pragma unroll
+        for (int pf = 0; pf < PF; ++pf) acc[cf][pf] = b;
+    }
+
+    const int iy0 = TR ? oy0 - 1 : oy0 * S - p.pad_t;
+    const int ix0 = TR ? ox0 - 1 : ox0 * S - p.pad_l;
+    const T* xg = (const T*)p.x.p;
+    const T* wg = (const T*)p.w + phase * p.phase_stride;
+    const long long xbase = (long long)p.x.c_off + (long long)g * p.cin_g;
+
+    for (int chunk = 0; chunk < p.nchunks; ++chunk) {
+        __syncthreads();
+        const int cl0 = chunk * CK;
+        for (int u = tid; u < HALO_U; u += NT) {
+            const int pix = u >> 2, q = u & 3;
+            const int hy = pix / HX, hx = pix - hy * HX;
+            const int iy = iy0 + hy, ix = ix0 + hx, cl = cl0 + q * VEC;
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (iy >= 0 && iy < p.H && ix >= 0 && ix < p.W && cl < p.cin_g) {
+                v = *(const u32x4*)(xg + (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + cl);
+                if (p.relu6_in) v = relu6_vec<T>(v);
+            }
+            s_halo[u] = v;
+        }
+        const u32x4* wsrc = (const u32x4*)(wg + ((long long)(g * p.nchunks + chunk) * p.nblk_g + nb0) *
+                                                     (long long)(NTAP * 16 * CK));
+        for (int u = tid; u < W_U; u += NT) s_w[u] = wsrc[u];
+        __syncthreads();
+
+        for (int t = 0; t < ntap; ++t) {
+            const int ky = tdy[t], kx = tdx[t];
+            u32x4 a[CF], b[PF];
+#pragma unroll
+            for (int cf = 0; cf < CF; ++cf) a[cf] = s_w[((wc * CF + cf) * NTAP + t) * 64 + col * 4 + grp];
+#pragma unroll
+            for (int pf = 0; pf < PF; ++pf) {
+                const int hy = (wp * PF + pf) * S + ky, hx = col * S + kx;
+                b[pf] = s_halo[(hy * HX + hx) * 4 + grp];
+            }
+#pragma unroll
+            for (int cf = 0; cf < CF; ++cf)
+#pragma unroll
+                for (int pf = 0; pf < PF; ++pf) Mma<T>::run(acc[cf][pf], a[cf], b[pf]);
+        }
+    }
+
+#pragma unroll
+    for (int cf = 0; cf < CF; ++cf) {
+        const int ocl = (nb0 + wc * CF + cf) * 16 + grp * 4;
+        if (ocl >= p.cout_g) continue;
+        const int nvalid = min(4, p.cout_g - ocl);
+#pragma unroll
+        for (int pf = 0; pf < PF; ++pf) {
+            const int r = wp * PF + pf;
+            int oy, ox;
+            if (TR) {
+                oy = 2 * (oy0 + r) + (phase >> 1);
+                ox = 2 * (ox0 + col) + (phase & 1);
+            } else {
+                oy = oy0 + r;
+                ox = ox0 + col;
+            }
+            if (oy >= p.OH || ox >= p.OW) continue;
+            epilogue_store<T>(p, oy, ox, g * p.cout_g + ocl, nvalid, acc[cf][pf]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Launch dispatch.
+// ---------------------------------------------------------------------------------------------
+template <typename T, int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF>
+static hipError_t go(const ConvParams& p, hipStream_t s) {
+    constexpr int TY = WP * PF;
+    const int gh = TR ? (p.OH + 1) / 2 : p.OH;
+    const int gw = TR ? (p.OW + 1) / 2 : p.OW;
+    const int ntiles = p.groups * p.nblk_g / (WC * CF);
+    dim3 grid((gw + 15) / 16, (gh + TY - 1) / TY, ntiles * (TR ? 4 : 1));
+    hipLaunchKernelGGL((conv_igemm<T, KH, KW, S, TR, WC, WP, CF, PF>), grid, dim3(WC * WP * 64), 0, s, p);
+    return hipGetLastError();
+}
+
+template <typename T, int WC, int WP, int CF, int PF>
+static hipError_t go_kind(int kind, const ConvParams& p, hipStream_t s) {
+    switch (kind) {
+        case CK_1x1: return go<T, 1, 1, 1, false, WC, WP, CF, PF>(p, s);
+        case CK_2x2: return go<T, 2, 2, 1, false, WC, WP, CF, PF>(p, s);
+        case CK_3x3: return go<T, 3, 3, 1, false, WC, WP, CF, PF>(p, s);
+        case CK_3x3_S2: return go<T, 3, 3, 2, false, WC, WP, CF, PF>(p, s);
+        case CK_T3: return go<T, 3, 3, 1, true, WC, WP, CF, PF>(p, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+// Instantiated tile shapes: (wc, wp, cf, pf).
+//   {2,2,2,4}: 64 channels x 8 rows  (dense layers)
+//   {1,4,2,2}: 32 channels x 8 rows  (32-channel groups / outputs)
+//   {1,4,1,2}: 16 channels x 8 rows  (16-channel groups / narrow outputs)
+#define ZJAI_CFGS(X) X(2, 2, 2, 4) X(1, 4, 2, 2) X(1, 4, 1, 2)
+
+bool conv_cfg_supported(int kind, int dtype, TileCfg c) {
+    (void)kind;
+    (void)dtype;
+#define ZJAI_CHECK(a, b, cc, d) if (c.wc == a && c.wp == b && c.cf == cc && c.pf == d) return true;
+    ZJAI_CFGS(ZJAI_CHECK)
+#undef ZJAI_CHECK
+    return false;
+}
+
+template <typename T>
+static hipError_t go_cfg(int kind, TileCfg c, const ConvParams& p, hipStream_t s) {
+#define ZJAI_GO(a, b, cc, d) \
+    if (c.wc == a && c.wp == b && c.cf == cc && c.pf == d) return go_kind<T, a, b, cc, d>(kind, p, s);
+    ZJAI_CFGS(ZJAI_GO)
+#undef ZJAI_GO
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_conv(int kind, int dtype, TileCfg cfg, const ConvParams& p, hipStream_t s) {
+    switch (dtype) {
+        case DT_F32: return go_cfg<float>(kind, cfg, p, s);
+        case DT_F16: return go_cfg<_Float16>(kind, cfg, p, s);
+        case DT_BF16: return go_cfg<__bf16>(kind, cfg, p, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace zjai

@@ -1,0 +1,442 @@
+// The synthesis transforms as fused launch sequences.
+//
+// Each forward restates a reference forward (src/model/synthesis.rs, src/model/attention.rs)
+// with its elementwise steps folded into the conv epilogues:
+//   LightResidualBlock  relu(conv(x)) + x          -> one conv, ACT_RELU + RES_ADD
+//   ResidualBlock       conv2(relu(conv1(x))) + x  -> conv ACT_RELU; conv RES_ADD
+//   ResAU               x * (1 + conv2(conv(relu6(x))))
+//                                                  -> conv with relu6 on load; 1x1 RES_GATE
+//                                                     written in place over x
+//   Upsample (SOP)      pad(0,1,0,1), conv2x2, pixel_shuffle(2) -> one conv, ps = 2
+//   CAB                 x + trunk * sigmoid(mask)  -> upscale convT with RES_CAB
+//   crop                                           -> a view (no copy)
+//   cat                                            -> producers write channel slices
+//   last layer          pixel shuffle + denormalise + tile-core crop + chroma subsampling +
+//                       quantisation -> the last conv's epilogue writes picture samples
+//   channel attention   attn . v then project_out  -> project_out folded with attn into one
+//                                                     1x1 conv over v (+ skip)
+
+#include "runtime.h"
+
+namespace zjai {
+
+// ------------------------------------------------------------------------------- building
+namespace {
+
+struct Builder {
+    Context& ctx;
+    Net& net;
+    const std::map<std::string, Param>& P;
+
+    const Param& get(const std::string& name, std::vector<int> shape) {
+        auto it = P.find(name);
+        if (it == P.end()) throw Error(ZJAI_E_MODEL, name + ": missing");
+        if (!shape.empty() && it->second.shape != shape) throw Error(ZJAI_E_MODEL, name + ": unexpected shape");
+        if (!it->second.data) throw Error(ZJAI_E_MODEL, name + ": no data");
+        return it->second;
+    }
+    const float* bias(const std::string& pfx, int n, bool required) {
+        auto it = P.find(pfx + ".bias");
+        if (it == P.end()) {
+            if (required) throw Error(ZJAI_E_MODEL, pfx + ".bias: missing");
+            return nullptr;
+        }
+        return get(pfx + ".bias", {n}).data;
+    }
+    // load::conv (src/model/load.rs:11-43)
+    void conv(const std::string& pfx, int cin, int cout, int kh, int kw, int stride, int pad,
+              int groups, bool with_bias, const int* extra = nullptr, bool keep_f32 = false) {
+        const Param& w = get(pfx + ".weight", {cout, cin / groups, kh, kw});
+        const float* b = with_bias ? bias(pfx, cout, true) : nullptr;
+        net.L[pfx] = make_conv(ctx, cin, cout, kh, kw, stride, pad, pad, groups, w.data, b, extra,
+                               net.dtype, keep_f32);
+    }
+    void conv3x3(const std::string& pfx, int cin, int cout, int groups, bool b) {
+        conv(pfx, cin, cout, 3, 3, 1, 1, groups, b);
+    }
+    void conv1x1(const std::string& pfx, int cin, int cout, bool b, bool keep_f32 = false) {
+        conv(pfx, cin, cout, 1, 1, 1, 0, 1, b, nullptr, keep_f32);
+    }
+    // load::conv_transpose (src/model/load.rs:70-89): always biased.
+    void conv_t(const std::string& pfx, int cin, int cout, int k, int pad, int out_pad) {
+        const Param& w = get(pfx + ".weight", {cin, cout, k, k});
+        const float* b = bias(pfx, cout, true);
+        net.L[pfx] = make_conv_transpose(ctx, cin, cout, k, 2, pad, out_pad, w.data, b, net.dtype);
+    }
+    void vec(const std::string& name, int n, std::vector<int> shape) {
+        const Param& p = get(name, shape);
+        float* d = nullptr;
+        ZJAI_HIP(hipMalloc(&d, sizeof(float) * n));
+        ZJAI_HIP(hipMemcpy(d, p.data, sizeof(float) * n, hipMemcpyHostToDevice));
+        net.vec[name] = d;
+    }
+    // ResAu::load (src/model/synthesis.rs:33-60): the weight's dim 1 decides the groups.
+    void res_au(const std::string& pfx, int chs) {
+        auto it = P.find(pfx + ".conv.weight");
+        if (it == P.end() || it->second.shape.size() != 4) throw Error(ZJAI_E_MODEL, pfx + ".conv.weight: missing or malformed");
+        const int per_group = it->second.shape[1];
+        if (per_group <= 0 || chs % per_group) throw Error(ZJAI_E_MODEL, pfx + ".conv.weight: missing or malformed");
+        conv3x3(pfx + ".conv", chs, chs, chs / per_group, false);
+        conv1x1(pfx + ".conv2", chs, chs, false);
+    }
+    void res_block(const std::string& pfx, int c) {
+        conv3x3(pfx + ".conv1", c, c, 1, true);
+        conv3x3(pfx + ".conv2", c, c, 1, true);
+    }
+    void upsample(int op, const std::string& pfx, int cin, int cout) {
+        if (op == OP_BOP) {
+            conv_t(pfx, cin, cout, 4, 1, 0);
+        } else {
+            static const int extra[4] = {0, 0, 1, 1};  // F.pad(x, (0, 1, 0, 1))
+            conv(pfx + ".conv", cin, cout * 4, 2, 2, 1, 0, 1, false, extra);
+        }
+    }
+    void cab(const std::string& pfx, int c) {
+        res_block(pfx + ".residual_trunk.0", c);
+        res_block(pfx + ".residual_trunk.1", c);
+        conv(pfx + ".subscale", c, c, 3, 3, 2, 1, 1, true);
+        res_block(pfx + ".residual_mask2.0", c);
+        res_block(pfx + ".residual_mask3.0", c);
+        conv_t(pfx + ".upscale", c, c, 3, 1, 1);
+    }
+    void transformer_block(const std::string& p, int dim) {
+        const int hidden = dim * 4;
+        vec(p + ".prep_data.norm1.weight", dim, {dim});
+        vec(p + ".prep_data.norm1.bias", dim, {dim});
+        conv1x1(p + ".prep_data.conv1", dim, 3 * dim, false);
+        conv(p + ".prep_data.conv2", 3 * dim, 3 * dim, 3, 3, 1, 1, 3 * dim, false);
+        vec(p + ".attn.temperature", 4, {4, 1, 1});
+        conv1x1(p + ".attn.project_out", dim, dim, false, true);
+        vec(p + ".ffn.norm1.weight", dim, {dim});
+        vec(p + ".ffn.norm1.bias", dim, {dim});
+        conv1x1(p + ".ffn.project_in", dim, 2 * hidden, false);
+        conv(p + ".ffn.dwconv", 2 * hidden, 2 * hidden, 3, 3, 1, 1, 2 * hidden, false);
+        conv1x1(p + ".ffn.project_out", hidden, dim, false);
+    }
+    void tam(const std::string& pfx, int dim, bool ds) {
+        if (ds) {
+            conv(pfx + ".ds_conv", dim, dim, 3, 3, 2, 1, 1, true);
+            conv_t(pfx + ".us_conv", dim, dim, 3, 1, 1);
+        }
+        transformer_block(pfx + ".TABs.0", dim);
+        transformer_block(pfx + ".TABs.1", dim);
+    }
+};
+
+}  // namespace
+
+Net::~Net() {
+    for (auto& kv : vec) (void)hipFree(kv.second);
+}
+
+NetP build_net(Context& ctx, int op, int comp, int dtype, const std::map<std::string, Param>& params) {
+    if (op < OP_SOP || op > OP_HOP || comp < COMP_Y || comp > COMP_UV)
+        throw Error(ZJAI_E_INVALID_ARGUMENT, "net: unknown operating point / component");
+    auto net = std::make_shared<Net>();
+    net->op = op;
+    net->comp = comp;
+    net->dtype = dtype;
+    Builder b{ctx, *net, params};
+    if (comp == COMP_Y && op != OP_HOP) {
+        // LightPrimary::load (src/model/synthesis.rs:526-548)
+        const int c1 = 64, c2 = op == OP_SOP ? 32 : 64, c3 = op == OP_SOP ? 32 : 96;
+        b.conv3x3("first_stage.0.0.conv1", 160, 160, 1, true);
+        b.upsample(op, "first_stage.1", 160, c1);
+        b.res_au("first_stage.2", c1);
+        b.upsample(op, "conv2_t", c1, c2);
+        b.res_au("iact2", c2);
+        b.conv3x3("conv3", c2, c3, 1, true);
+        b.res_au("iact3", c3);
+        b.conv1x1("conv4", c3, 16, false);
+    } else if (comp == COMP_Y) {
+        // HopPrimary::load (src/model/synthesis.rs:339-354)
+        const int c = 128;
+        b.res_block("first_stage.0.0", 160);
+        b.conv_t("first_stage.1", 160, c, 3, 1, 1);
+        b.res_au("first_stage.2", c);
+        b.conv_t("conv2_t", c, c, 3, 1, 1);
+        b.cab("CAB", c);
+        b.res_au("iact2", c);
+        b.conv1x1("conv3_t", c, 4 * c, true);
+        b.tam("TAM", c, true);
+        b.res_au("iact3", c);
+        b.conv_t("conv4_t", c, 1, 3, 1, 1);
+    } else {
+        // SynthesisSecondary::load (src/model/synthesis.rs:972-990)
+        b.conv3x3("first_stage.conv1", 256, 48, 1, true);
+        if (op == OP_HOP) {
+            const int c = 64;  // HopSecondary::load (:740-753)
+            b.conv_t("conv2_t", 144, c, 3, 1, 1);
+            b.cab("CAB", c);
+            b.res_au("iact2", c);
+            b.conv1x1("conv3_t", c, 4 * c, true);
+            b.tam("TAM", c, false);
+            b.res_au("iact3", c);
+            b.conv_t("conv4_t", c, 8, 3, 1, 1);
+        } else {
+            // LightSecondary::load (:871-888)
+            const int c2 = op == OP_SOP ? 32 : 64, c3 = op == OP_SOP ? 32 : 128;
+            b.upsample(op, "conv2_t", 144, c2);
+            b.res_au("iact2", c2);
+            b.conv3x3("conv3", c2, c3, 1, true);
+            b.res_au("iact3", c3);
+            b.conv1x1("conv4", c3, 128, false);
+        }
+    }
+    return net;
+}
+
+// -------------------------------------------------------------------------------- forward
+namespace {
+
+struct Fwd {
+    Context& ctx;
+    const Net& net;
+
+    const Layer& L(const std::string& name) const {
+        auto it = net.L.find(name);
+        if (it == net.L.end()) throw Error(ZJAI_E_MODEL, name + ": layer missing");
+        return *it->second;
+    }
+    TensorP conv(const std::string& name, const TensorP& x, Epilogue e = Epilogue{},
+                 const TensorP& dst = nullptr, const PlaneOut* plane = nullptr) {
+        return conv_forward(ctx, L(name), x, e, dst, plane);
+    }
+    // ResAu::forward (src/model/synthesis.rs:62-74); the gate overwrites x.
+    TensorP res_au(const std::string& pfx, const TensorP& x) {
+        Epilogue e1;
+        e1.relu6_in = 1;
+        TensorP t = conv(pfx + ".conv", x, e1);
+        Epilogue e2;
+        e2.res = RES_GATE;
+        e2.r1 = x.get();
+        conv(pfx + ".conv2", t, e2, x);
+        return x;
+    }
+    // ResidualBlock::forward (src/model/attention.rs:35-43)
+    TensorP res_block(const std::string& pfx, const TensorP& x) {
+        Epilogue e1;
+        e1.act = ACT_RELU;
+        TensorP t = conv(pfx + ".conv1", x, e1);
+        Epilogue e2;
+        e2.res = RES_ADD;
+        e2.r1 = x.get();
+        return conv(pfx + ".conv2", t, e2);
+    }
+    // Upsample::forward (src/model/synthesis.rs:158-166)
+    TensorP upsample(const std::string& pfx, const TensorP& x) {
+        if (net.op == OP_BOP) return conv(pfx, x);
+        Epilogue e;
+        e.ps = 2;
+        return conv(pfx + ".conv", x, e);
+    }
+    // Cab::forward (src/model/attention.rs:119-139)
+    TensorP cab(const std::string& pfx, const TensorP& x) {
+        TensorP trunk = res_block(pfx + ".residual_trunk.0", x);
+        trunk = res_block(pfx + ".residual_trunk.1", trunk);
+        TensorP m = conv(pfx + ".subscale", x);
+        m = res_block(pfx + ".residual_mask2.0", m);
+        m = res_block(pfx + ".residual_mask3.0", m);
+        int oh, ow;
+        L(pfx + ".upscale").out_size(m->h, m->w, &oh, &ow);
+        if (oh != trunk->h || ow != trunk->w) throw Error(ZJAI_E_INVALID_ARGUMENT, "CAB: odd feature map size");
+        Epilogue e;
+        e.res = RES_CAB;
+        e.r1 = trunk.get();
+        e.r2 = x.get();
+        return conv(pfx + ".upscale", m, e);
+    }
+    TensorP layer_norm(const std::string& pfx, const TensorP& x) {
+        TensorP y = ctx.alloc(x->c, x->h, x->w, x->dtype);
+        ZJAI_HIP(launch_layer_norm(x->v, y->v, x->dtype, x->c, x->h, x->w, net.vec.at(pfx + ".weight"),
+                                   net.vec.at(pfx + ".bias"), ctx.stream));
+        ++ctx.launches;
+        return y;
+    }
+    // TransformerBlock::forward (src/model/attention.rs:328-372)
+    TensorP transformer_block(const std::string& p, TensorP x) {
+        const int dim = x->c, heads = 4, hidden = 4 * dim;
+        TensorP t = layer_norm(p + ".prep_data.norm1", x);
+        t = conv(p + ".prep_data.conv1", t);
+        t = conv(p + ".prep_data.conv2", t);  // depthwise 3x3
+        // channel_attention + project_out: fold attn into the projection, run it on v.
+        const int nchunk = attention_gram_chunks(t->h, t->w);
+        const int c = dim / heads, total = heads * (c * c + 2 * c);
+        double* partial = (double*)ctx.pool.alloc(sizeof(double) * (size_t)nchunk * total);
+        std::shared_ptr<void> pk(partial, [this](void* q) { ctx.pool.release(q); });
+        ZJAI_HIP(launch_attention_gram(t->v, t->dtype, dim, heads, t->h, t->w, partial, ctx.stream));
+        float* scratch = (float*)ctx.pool.alloc(sizeof(float) * (size_t)(dim * c + dim * dim));
+        std::shared_ptr<void> sk(scratch, [this](void* q) { ctx.pool.release(q); });
+        const Layer& proj = L(p + ".attn.project_out");
+        ZJAI_HIP(launch_attention_softmax_fold(partial, nchunk, dim, heads, net.vec.at(p + ".attn.temperature"),
+                                               proj.w_f32, scratch, scratch + dim * c, ctx.stream));
+        ctx.launches += 2;
+        pack_1x1_device(ctx, proj, scratch + dim * c);
+        Epilogue ea;
+        ea.res = RES_ADD;
+        ea.r1 = x.get();
+        conv(p + ".attn.project_out", channel_view(t, 2 * dim, dim), ea, x);
+        t.reset();
+        // x = x + ffn(x)
+        TensorP u = layer_norm(p + ".ffn.norm1", x);
+        u = conv(p + ".ffn.project_in", u);
+        const Layer& dw = L(p + ".ffn.dwconv");
+        TensorP f = ctx.alloc(hidden, u->h, u->w, u->dtype);
+        ZJAI_HIP(launch_depthwise3x3(u->v, f->v, u->dtype, 2 * hidden, u->h, u->w, dw.dw_w, dw.bias, hidden, ctx.stream));
+        ++ctx.launches;
+        u.reset();
+        Epilogue ef;
+        ef.res = RES_ADD;
+        ef.r1 = x.get();
+        conv(p + ".ffn.project_out", f, ef, x);
+        return x;
+    }
+    // Tam::forward (src/model/attention.rs:528-545)
+    TensorP tam(const std::string& pfx, TensorP x, bool ds) {
+        if (ds) x = conv(pfx + ".ds_conv", x);
+        x = transformer_block(pfx + ".TABs.0", x);
+        x = transformer_block(pfx + ".TABs.1", x);
+        if (ds) x = conv(pfx + ".us_conv", x);
+        return x;
+    }
+};
+
+}  // namespace
+
+void primary_out_size(int op, int h, int w, int* oh, int* ow) {
+    if (op == OP_HOP) {
+        *oh = 2 * ceil_div(h, 2);
+        *ow = 2 * ceil_div(w, 2);
+    } else {
+        *oh = 4 * ceil_div(h, 4);
+        *ow = 4 * ceil_div(w, 4);
+    }
+}
+
+void secondary_out_size(int op, int h, int w, int* oh, int* ow) {
+    if (op == OP_HOP) {
+        *oh = 4 * ceil_div(h, 4);
+        *ow = 4 * ceil_div(w, 4);
+    } else {
+        *oh = 8 * ceil_div(h, 8);
+        *ow = 8 * ceil_div(w, 8);
+    }
+}
+
+void primary_forward(Context& ctx, const Net& net, const TensorP& y_hat, int h, int w, const PlaneOut& out) {
+    if (net.comp != COMP_Y) throw Error(ZJAI_E_INVALID_ARGUMENT, "primary forward on a chroma net");
+    if (y_hat->c != 160) throw Error(ZJAI_E_INVALID_ARGUMENT, "primary: latent must have 160 channels");
+    Fwd f{ctx, net};
+    const int h8 = ceil_div(h, 8), w8 = ceil_div(w, 8), h4 = ceil_div(h, 4), w4 = ceil_div(w, 4);
+    if (net.op != OP_HOP) {
+        // LightPrimary::forward (src/model/synthesis.rs:550-580)
+        Epilogue e0;
+        e0.act = ACT_RELU;
+        e0.res = RES_ADD;
+        e0.r1 = y_hat.get();
+        TensorP x = f.conv("first_stage.0.0.conv1", y_hat, e0);
+        ctx.check_stop();
+        x = f.upsample("first_stage.1", x);
+        x = f.res_au("first_stage.2", x);
+        x = crop_view(x, h8, w8);
+        ctx.check_stop();
+        x = f.upsample("conv2_t", x);
+        x = crop_view(x, h4, w4);
+        ctx.check_stop();
+        x = f.res_au("iact2", x);
+        ctx.check_stop();
+        x = f.conv("conv3", x);
+        ctx.check_stop();
+        x = f.res_au("iact3", x);
+        ctx.check_stop();
+        Epilogue e;
+        e.ps = 4;
+        f.conv("conv4", x, e, nullptr, &out);
+        return;
+    }
+    // HopPrimary::forward (src/model/synthesis.rs:356-390)
+    TensorP x = f.res_block("first_stage.0.0", y_hat);
+    ctx.check_stop();
+    x = f.conv("first_stage.1", x);
+    x = f.res_au("first_stage.2", x);
+    x = crop_view(x, h8, w8);
+    ctx.check_stop();
+    x = f.conv("conv2_t", x);
+    x = f.cab("CAB", x);
+    x = crop_view(x, h4, w4);
+    ctx.check_stop();
+    x = f.res_au("iact2", x);
+    ctx.check_stop();
+    Epilogue e3;
+    e3.ps = 2;
+    x = f.conv("conv3_t", x, e3);
+    ctx.check_stop();
+    x = f.tam("TAM", x, true);
+    x = crop_view(x, ceil_div(h, 2), ceil_div(w, 2));
+    ctx.check_stop();
+    x = f.res_au("iact3", x);
+    ctx.check_stop();
+    f.conv("conv4_t", x, Epilogue{}, nullptr, &out);
+}
+
+void secondary_forward(Context& ctx, const Net& net, const TensorP& y_luma, const TensorP& y_chroma,
+                       int h, int w, const PlaneOut& out) {
+    if (net.comp != COMP_UV) throw Error(ZJAI_E_INVALID_ARGUMENT, "secondary forward on a luma net");
+    if (y_luma->c != 160 || y_chroma->c != 96)
+        throw Error(ZJAI_E_INVALID_ARGUMENT, "secondary: latents must have 160 / 96 channels");
+    if (y_luma->dtype != net.dtype || y_chroma->dtype != net.dtype)
+        throw Error(ZJAI_E_INVALID_ARGUMENT, "secondary: latent precision differs from the net");
+    // SynthesisSecondary::forward_with (src/model/synthesis.rs:1004-1038)
+    const int lh = std::min(y_luma->h, y_chroma->h), lw = std::min(y_luma->w, y_chroma->w);
+    if (y_chroma->h != lh || y_chroma->w != lw)
+        throw Error(ZJAI_E_INVALID_ARGUMENT, "chroma latent larger than the luma latent");
+    Fwd f{ctx, net};
+    const int dt = net.dtype;
+    TensorP cat = ctx.alloc(256, lh, lw, dt);
+    ZJAI_HIP(launch_copy(y_luma->v, cat->v, dt, 160, lh, lw, ctx.stream));
+    ZJAI_HIP(launch_copy(y_chroma->v, channel_view(cat, 160, 96)->v, dt, 96, lh, lw, ctx.stream));
+    TensorP x = ctx.alloc(144, lh, lw, dt);
+    f.conv("first_stage.conv1", cat, Epilogue{}, channel_view(x, 0, 48));
+    ZJAI_HIP(launch_copy(y_chroma->v, channel_view(x, 48, 96)->v, dt, 96, lh, lw, ctx.stream));
+    ctx.launches += 3;
+    cat.reset();
+    ctx.check_stop();
+    const int h8 = ceil_div(h, 8), w8 = ceil_div(w, 8);
+    if (net.op == OP_HOP) {
+        // HopSecondary::forward (:755-773)
+        x = f.conv("conv2_t", x);
+        x = f.cab("CAB", x);
+        x = crop_view(x, h8, w8);
+        ctx.check_stop();
+        x = f.res_au("iact2", x);
+        ctx.check_stop();
+        Epilogue e3;
+        e3.ps = 2;
+        x = f.conv("conv3_t", x, e3);
+        ctx.check_stop();
+        x = f.tam("TAM", x, false);
+        x = crop_view(x, ceil_div(h, 4), ceil_div(w, 4));
+        ctx.check_stop();
+        x = f.res_au("iact3", x);
+        ctx.check_stop();
+        Epilogue e4;
+        e4.ps = 2;
+        f.conv("conv4_t", x, e4, nullptr, &out);
+        return;
+    }
+    // LightSecondary::forward (:890-909)
+    x = f.upsample("conv2_t", x);
+    x = crop_view(x, h8, w8);
+    ctx.check_stop();
+    x = f.res_au("iact2", x);
+    ctx.check_stop();
+    x = f.conv("conv3", x);
+    ctx.check_stop();
+    x = f.res_au("iact3", x);
+    ctx.check_stop();
+    Epilogue e;
+    e.ps = 8;
+    f.conv("conv4", x, e, nullptr, &out);
+}
+
+}  // namespace zjai

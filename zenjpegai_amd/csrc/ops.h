@@ -1,0 +1,55 @@
+// Bandwidth-bound kernels of the synthesis path (layout, elementwise, depthwise, layer norm,
+// channel attention). Host-callable launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "device.h"
+
+namespace zjai {
+
+enum EltOp : int {
+    EL_RELU = 0,     // max(x, 0)
+    EL_RELU6 = 1,    // clamp(x, 0, 6)
+    EL_LEAKY = 2,    // x < 0 ? 0.01 x : x
+    EL_SIGMOID = 3,  // 1 / (1 + exp(-x))
+    EL_ADD = 4,      // x = x + s
+    EL_GATE = 5,     // x = x * (1 + s)
+    EL_MUL = 6,      // x = x * s
+    EL_ELU_GATE = 7, // x = elu(x) * s
+};
+
+// Planar f32 [C][LH][LW] window (x0, y0, w, h) -> NHWC view of dtype.
+hipError_t launch_planar_to_nhwc(const float* src, int C, int LH, int LW, int x0, int y0, int h,
+                                 int w, View dst, int dtype, hipStream_t s);
+// NHWC view -> planar f32 [C][h][w].
+hipError_t launch_nhwc_to_planar(View src, int dtype, int C, int h, int w, float* dst,
+                                 hipStream_t s);
+// x = op(x[, s]) over an h x w x C region.
+hipError_t launch_eltwise(int op, View x, View src, int dtype, int C, int h, int w, hipStream_t s);
+// NHWC copy of C channels over h x w (channel offsets / crops / concatenation).
+hipError_t launch_copy(View src, View dst, int dtype, int C, int h, int w, hipStream_t s);
+// Pixel shuffle NHWC -> NHWC: out channel c at (y*r+dy, x*r+dx) = in channel c*r*r+dy*r+dx.
+hipError_t launch_pixel_shuffle(View src, View dst, int dtype, int C_out, int h, int w, int r,
+                                hipStream_t s);
+// Depthwise 3x3, stride 1, pad 1, weights [C][9] f32, optional bias. With elu_half > 0 the
+// output keeps channels [0, elu_half) = elu(dw(c)) * dw(c + elu_half) (the FFN gate).
+hipError_t launch_depthwise3x3(View src, View dst, int dtype, int C, int h, int w,
+                               const float* weight, const float* bias, int elu_half,
+                               hipStream_t s);
+// Layer norm over channels per position (f64 sums), src -> dst.
+hipError_t launch_layer_norm(View src, View dst, int dtype, int C, int h, int w,
+                             const float* weight, const float* bias, hipStream_t s);
+// Channel attention, phase 1: per-head Gram partial sums over position chunks.
+// qkv view holds 3*dim channels. Writes partial[nchunk][heads][c*c + 2c] f64.
+int attention_gram_chunks(int h, int w);
+hipError_t launch_attention_gram(View qkv, int dtype, int dim, int heads, int h, int w,
+                                 double* partial, hipStream_t s);
+// Phase 2: reduce partials, normalise, temperature, softmax -> attn [dim][c] f32, then fold the
+// output projection: wfold[o][head*c + j] = sum_i proj[o][head*c + i] * attn[head*c + i][j].
+hipError_t launch_attention_softmax_fold(const double* partial, int nchunk, int dim, int heads,
+                                         const float* temperature, const float* proj,
+                                         float* attn, float* wfold, hipStream_t s);
+
+}  // namespace zjai

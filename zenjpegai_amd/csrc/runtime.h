@@ -1,0 +1,172 @@
+// Host runtime of the HIP synthesis backend: context (one stream), device buffer pool,
+// activation tensors, packed layers, synthesis nets and pictures.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "conv.h"
+#include "ops.h"
+#include "../../include/zjai_hip.h"
+
+namespace zjai {
+
+// Error carrying one of the ZJAI_E_* status codes across the C++ internals; the C-ABI catches
+// it and returns the code (no exception crosses the ABI).
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+#define ZJAI_HIP(call)                                                                        \
+    do {                                                                                      \
+        hipError_t e_ = (call);                                                               \
+        if (e_ != hipSuccess)                                                                 \
+            throw ::zjai::Error(e_ == hipErrorOutOfMemory ? ZJAI_E_LIMIT : ZJAI_E_DEVICE,     \
+                                std::string(#call ": ") + hipGetErrorString(e_));             \
+    } while (0)
+
+inline int dtype_size(int dt) { return dt == DT_F32 ? 4 : 2; }
+inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Caching device allocator: freed blocks go back to a per-size free list and are reused, so a
+// steady-state decode allocates nothing (the reference's buffer pool, src/nn/fast/tensor.rs:21-119,
+// keeps its host buffers the same way).
+class Pool {
+public:
+    void* alloc(size_t bytes);
+    void release(void* p);
+    void trim();
+    size_t in_use() const { return in_use_; }
+    size_t peak() const { return peak_; }
+    size_t cached() const { return cached_; }
+    ~Pool();
+
+private:
+    static size_t bucket(size_t bytes);
+    std::multimap<size_t, void*> free_;
+    std::map<void*, size_t> live_;
+    size_t in_use_ = 0, peak_ = 0, cached_ = 0;
+};
+
+struct Context;
+
+// Device activation (NHWC view). `owner` blocks return to the pool when the tensor dies.
+struct Tensor {
+    Context* ctx = nullptr;
+    void* base = nullptr;  // pool block (owner) or nullptr for views
+    View v{};
+    int dtype = DT_F32, c = 0, h = 0, w = 0;
+    std::shared_ptr<void> keep;  // keeps the underlying block alive for views
+    int cs() const { return v.cs; }
+};
+using TensorP = std::shared_ptr<Tensor>;
+
+struct Context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    Pool pool;
+    std::string last_error;
+    volatile int stop = 0;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    float last_ms = 0.0f;
+    long long launches = 0;
+
+    TensorP alloc(int c, int h, int w, int dtype);
+    void check_stop();
+};
+
+// View of the top-left h x w corner (`BTensor::crop_par`, src/nn/fast/tensor.rs:349-367).
+TensorP crop_view(const TensorP& t, int h, int w);
+// View of channels [c0, c0 + n) of t.
+TensorP channel_view(const TensorP& t, int c0, int n);
+
+// A convolution packed for the implicit-GEMM kernels (PackedConv / PackedConvTranspose /
+// PackedDepthwise equivalents).
+struct Layer {
+    bool transposed = false, depthwise = false;
+    int cin = 0, cout = 0, kh = 0, kw = 0, stride = 1, pad_h = 0, pad_w = 0, groups = 1;
+    int k = 0, pad = 0, out_pad = 0;
+    int extra[4] = {0, 0, 0, 0};
+    int dtype = DT_F32;
+    int kind = 0;
+    TileCfg cfg{};
+    int nblk_g = 0, nchunks = 0;
+    long long phase_stride = 0;
+    int ntaps[4] = {0, 0, 0, 0}, tap_dy[4][4] = {}, tap_dx[4][4] = {};
+    void* wpk = nullptr;       // packed weights (storage dtype)
+    float* bias = nullptr;     // f32 [cout] or null
+    float* dw_w = nullptr;     // depthwise [9][C]
+    float* w_f32 = nullptr;    // f32 [cout][cin] copy (1x1 only, for attention folding)
+    size_t wpk_bytes = 0;
+    ~Layer();
+
+    void out_size(int h, int w, int* oh, int* ow) const;
+};
+using LayerP = std::shared_ptr<Layer>;
+
+LayerP make_conv(Context& ctx, int cin, int cout, int kh, int kw, int stride, int pad_h,
+                 int pad_w, int groups, const float* weight, const float* bias,
+                 const int extra[4], int dtype, bool keep_f32);
+LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, int pad,
+                           int out_pad, const float* weight, const float* bias, int dtype);
+
+// Fused epilogue description for one conv launch.
+struct Epilogue {
+    int act = ACT_NONE, res = RES_NONE, ps = 1, relu6_in = 0;
+    const Tensor* r1 = nullptr;
+    const Tensor* r2 = nullptr;
+};
+
+// Planar picture destination of a last layer.
+struct PlaneOut {
+    void* plane = nullptr;
+    long long row = 0, cstride = 0;
+    int win_y0 = 0, win_x0 = 0, win_h = 0, win_w = 0, dst_y0 = 0, dst_x0 = 0, sv = 1, sh = 1;
+    int denorm = 1, bit_depth = 0;
+};
+
+// Runs a layer on x. With `dst` null a new tensor is allocated; with `plane` set the output
+// goes to the planar destination instead.
+TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilogue& e,
+                     const TensorP& dst = nullptr, const PlaneOut* plane = nullptr);
+
+// Device pack of an f32 [O][I] 1x1 weight into a layer's packed layout (attention fold).
+void pack_1x1_device(Context& ctx, const Layer& L, const float* w_dev);
+
+// ---------------------------------------------------------------------------- synthesis nets
+enum Op : int { OP_SOP = 0, OP_BOP = 1, OP_HOP = 2 };
+enum Comp : int { COMP_Y = 0, COMP_UV = 1 };
+
+struct Param {
+    std::vector<int> shape;
+    const float* data;
+};
+
+struct Net {
+    int op = 0, comp = 0, dtype = DT_F32;
+    std::map<std::string, LayerP> L;
+    std::map<std::string, float*> vec;  // device f32 vectors (layer norm, temperature)
+    ~Net();
+};
+using NetP = std::shared_ptr<Net>;
+
+NetP build_net(Context& ctx, int op, int comp, int dtype, const std::map<std::string, Param>& params);
+// `SynthesisPrimary::forward_with`: y_hat -> planar [1][oh][ow] into `out` (f32 plane or
+// picture window per PlaneOut).
+void primary_forward(Context& ctx, const Net& net, const TensorP& y_hat, int h, int w,
+                     const PlaneOut& out);
+// `SynthesisSecondary::forward_with`: (luma latent, chroma latent) -> planar [2][oh][ow].
+void secondary_forward(Context& ctx, const Net& net, const TensorP& y_luma,
+                       const TensorP& y_chroma, int h, int w, const PlaneOut& out);
+void primary_out_size(int op, int h, int w, int* oh, int* ow);
+void secondary_out_size(int op, int h, int w, int* oh, int* ow);
+
+}  // namespace zjai

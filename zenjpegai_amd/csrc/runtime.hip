@@ -1,0 +1,440 @@
+// Host runtime: device pool, tensors, weight packing and conv launches.
+
+#include "runtime.h"
+
+#include <cmath>
+#include <cstring>
+
+namespace zjai {
+
+// ------------------------------------------------------------------------------------ pool
+size_t Pool::bucket(size_t bytes) {
+    // 256-byte granularity below 1 MiB, 64 KiB granularity above: tile shapes repeat, so exact
+    // sizes recur and blocks are reused without much slack.
+    if (bytes <= (1u << 20)) return (bytes + 255) & ~size_t(255);
+    return (bytes + 65535) & ~size_t(65535);
+}
+
+void* Pool::alloc(size_t bytes) {
+    const size_t b = bucket(bytes ? bytes : 256);
+    auto it = free_.lower_bound(b);
+    void* p = nullptr;
+    size_t got = 0;
+    // Reuse a cached block of the same size, or one at most 1.5x larger.
+    if (it != free_.end() && it->first <= b + b / 2) {
+        p = it->second;
+        got = it->first;
+        free_.erase(it);
+    } else {
+        hipError_t e = hipMalloc(&p, b);
+        if (e == hipErrorOutOfMemory) {
+            trim();
+            e = hipMalloc(&p, b);
+        }
+        if (e != hipSuccess)
+            throw Error(e == hipErrorOutOfMemory ? ZJAI_E_LIMIT : ZJAI_E_DEVICE,
+                        std::string("hipMalloc: ") + hipGetErrorString(e));
+        got = b;
+        cached_ += b;
+    }
+    live_[p] = got;
+    in_use_ += got;
+    if (in_use_ > peak_) peak_ = in_use_;
+    return p;
+}
+
+void Pool::release(void* p) {
+    auto it = live_.find(p);
+    if (it == live_.end()) return;
+    in_use_ -= it->second;
+    free_.emplace(it->second, p);
+    live_.erase(it);
+}
+
+void Pool::trim() {
+    (void)hipDeviceSynchronize();
+    for (auto& kv : free_) {
+        (void)hipFree(kv.second);
+        cached_ -= kv.first;
+    }
+    free_.clear();
+}
+
+Pool::~Pool() {
+    for (auto& kv : free_) (void)hipFree(kv.second);
+    for (auto& kv : live_) (void)hipFree(kv.first);
+}
+
+// --------------------------------------------------------------------------------- tensors
+TensorP Context::alloc(int c, int h, int w, int dtype) {
+    if (c <= 0 || h < 0 || w < 0) throw Error(ZJAI_E_INVALID_ARGUMENT, "tensor: bad shape");
+    auto t = std::make_shared<Tensor>();
+    t->ctx = this;
+    t->dtype = dtype;
+    t->c = c;
+    t->h = h;
+    t->w = w;
+    t->v.cs = round_up(c, 8);
+    t->v.row = (long long)w * t->v.cs;
+    t->v.c_off = 0;
+    const size_t bytes = (size_t)h * (size_t)t->v.row * dtype_size(dtype);
+    void* p = pool.alloc(bytes);
+    Context* self = this;
+    t->keep = std::shared_ptr<void>(p, [self](void* q) { self->pool.release(q); });
+    t->base = p;
+    t->v.p = p;
+    return t;
+}
+
+void Context::check_stop() {
+    if (stop) throw Error(ZJAI_E_CANCELLED, "cancelled");
+}
+
+TensorP crop_view(const TensorP& t, int h, int w) {
+    if (h > t->h || w > t->w || h < 0 || w < 0)
+        throw Error(ZJAI_E_INVALID_ARGUMENT, "crop larger than tensor");
+    if (h == t->h && w == t->w) return t;
+    auto v = std::make_shared<Tensor>(*t);
+    v->h = h;
+    v->w = w;
+    return v;
+}
+
+TensorP channel_view(const TensorP& t, int c0, int n) {
+    if (c0 < 0 || n <= 0 || c0 + n > t->c) throw Error(ZJAI_E_INVALID_ARGUMENT, "channel range");
+    auto v = std::make_shared<Tensor>(*t);
+    v->c = n;
+    v->v.c_off = t->v.c_off + c0;
+    return v;
+}
+
+// ------------------------------------------------------------------------ weight conversion
+// f32 -> f16 bits, round to nearest even, the reference's integer algorithm
+// (src/weights/f16.rs:12-53).
+static uint16_t f32_to_f16_bits(float v) {
+    uint32_t b;
+    std::memcpy(&b, &v, 4);
+    const uint16_t sign = (uint16_t)((b >> 16) & 0x8000);
+    const int exp = (int)((b >> 23) & 0xff);
+    const uint32_t mant = b & 0x007fffff;
+    if (exp == 255) {
+        uint16_t payload = (uint16_t)((mant >> 13) | 0x200);
+        return (uint16_t)(sign | 0x7c00 | (mant ? payload : 0));
+    }
+    const int e = exp - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00);
+    if (e <= 0) {
+        if (e < -10) return sign;
+        const uint32_t m = mant | 0x00800000;
+        const uint32_t shift = (uint32_t)(14 - e);
+        const uint32_t dropped = m & ((1u << shift) - 1);
+        const uint32_t half = 1u << (shift - 1);
+        uint32_t r = m >> shift;
+        if (dropped > half || (dropped == half && (r & 1))) r += 1;
+        return (uint16_t)(sign | r);
+    }
+    const uint32_t dropped = mant & 0x1fff;
+    uint32_t r = mant >> 13;
+    if (dropped > 0x1000 || (dropped == 0x1000 && (r & 1))) r += 1;
+    return (uint16_t)(sign | (((uint32_t)e << 10) + r));
+}
+
+// f32 -> bf16 bits, round to nearest even (NaN kept quiet).
+static uint16_t f32_to_bf16_bits(float v) {
+    uint32_t b;
+    std::memcpy(&b, &v, 4);
+    if ((b & 0x7fffffff) > 0x7f800000) return (uint16_t)((b >> 16) | 0x40);
+    const uint32_t r = b + 0x7fff + ((b >> 16) & 1);
+    return (uint16_t)(r >> 16);
+}
+
+// Converts an f32 staging vector to the storage dtype and uploads it.
+static void* upload_as(Context& ctx, const std::vector<float>& host, int dtype, size_t* bytes_out) {
+    const size_t n = host.size();
+    void* dev = nullptr;
+    if (dtype == DT_F32) {
+        ZJAI_HIP(hipMalloc(&dev, n * 4));
+        ZJAI_HIP(hipMemcpy(dev, host.data(), n * 4, hipMemcpyHostToDevice));
+        *bytes_out = n * 4;
+    } else {
+        std::vector<uint16_t> h(n);
+        for (size_t i = 0; i < n; ++i)
+            h[i] = dtype == DT_F16 ? f32_to_f16_bits(host[i]) : f32_to_bf16_bits(host[i]);
+        ZJAI_HIP(hipMalloc(&dev, n * 2));
+        ZJAI_HIP(hipMemcpy(dev, h.data(), n * 2, hipMemcpyHostToDevice));
+        *bytes_out = n * 2;
+    }
+    (void)ctx;
+    return dev;
+}
+
+static float* upload_f32(const float* p, size_t n) {
+    float* dev = nullptr;
+    ZJAI_HIP(hipMalloc(&dev, n * 4));
+    ZJAI_HIP(hipMemcpy(dev, p, n * 4, hipMemcpyHostToDevice));
+    return dev;
+}
+
+Layer::~Layer() {
+    if (wpk) (void)hipFree(wpk);
+    if (bias) (void)hipFree(bias);
+    if (dw_w) (void)hipFree(dw_w);
+    if (w_f32) (void)hipFree(w_f32);
+}
+
+void Layer::out_size(int h, int w, int* oh, int* ow) const {
+    if (transposed) {
+        *oh = (h - 1) * stride + k + out_pad - 2 * pad;
+        *ow = (w - 1) * stride + k + out_pad - 2 * pad;
+    } else {
+        *oh = (h + extra[0] + extra[2] + 2 * pad_h - kh) / stride + 1;
+        *ow = (w + extra[1] + extra[3] + 2 * pad_w - kw) / stride + 1;
+    }
+}
+
+static TileCfg pick_cfg(int cout_g) {
+    if (cout_g <= 16) return TileCfg{1, 4, 1, 2};
+    if (cout_g <= 32) return TileCfg{1, 4, 2, 2};
+    return TileCfg{2, 2, 2, 4};
+}
+
+LayerP make_conv(Context& ctx, int cin, int cout, int kh, int kw, int stride, int pad_h,
+                 int pad_w, int groups, const float* weight, const float* bias,
+                 const int extra[4], int dtype, bool keep_f32) {
+    if (groups <= 0 || cin <= 0 || cout <= 0 || cin % groups || cout % groups || stride <= 0 ||
+        kh <= 0 || kw <= 0 || pad_h < 0 || pad_w < 0)
+        throw Error(ZJAI_E_MODEL, "conv2d: inconsistent channel/group/kernel configuration");
+    if (dtype < DT_F32 || dtype > DT_BF16) throw Error(ZJAI_E_INVALID_ARGUMENT, "precision");
+    if (!weight) throw Error(ZJAI_E_INVALID_ARGUMENT, "conv2d: null weight");
+    auto L = std::make_shared<Layer>();
+    L->cin = cin; L->cout = cout; L->kh = kh; L->kw = kw; L->stride = stride;
+    L->pad_h = pad_h; L->pad_w = pad_w; L->groups = groups; L->dtype = dtype;
+    if (extra) for (int i = 0; i < 4; ++i) {
+        if (extra[i] < 0) throw Error(ZJAI_E_INVALID_ARGUMENT, "extra pad");
+        L->extra[i] = extra[i];
+    }
+    const int cin_g = cin / groups, cout_g = cout / groups;
+    const bool no_extra = !(L->extra[0] | L->extra[1] | L->extra[2] | L->extra[3]);
+    if (groups == cin && groups == cout && kh == 3 && kw == 3 && stride == 1 && pad_h == 1 &&
+        pad_w == 1 && no_extra) {
+        if (cin % 4) throw Error(ZJAI_E_UNSUPPORTED, "depthwise: channels not a multiple of 4");
+        L->depthwise = true;
+        std::vector<float> t((size_t)9 * cin);
+        for (int c = 0; c < cin; ++c)
+            for (int k = 0; k < 9; ++k) t[(size_t)k * cin + c] = weight[(size_t)c * 9 + k];
+        L->dw_w = upload_f32(t.data(), t.size());
+        if (bias) L->bias = upload_f32(bias, cout);
+        return L;
+    }
+    if (kh == 1 && kw == 1 && stride == 1) L->kind = CK_1x1;
+    else if (kh == 2 && kw == 2 && stride == 1) L->kind = CK_2x2;
+    else if (kh == 3 && kw == 3 && stride == 1) L->kind = CK_3x3;
+    else if (kh == 3 && kw == 3 && stride == 2) L->kind = CK_3x3_S2;
+    else throw Error(ZJAI_E_UNSUPPORTED, "conv2d: kernel geometry without a HIP kernel");
+    const int vec = 16 / dtype_size(dtype);
+    if (cin_g % vec) throw Error(ZJAI_E_UNSUPPORTED, "conv2d: channels per group not vector aligned");
+    L->cfg = pick_cfg(cout_g);
+    const int NB = L->cfg.wc * L->cfg.cf;
+    const int CK = 64 / dtype_size(dtype);
+    const int T = kh * kw;
+    L->nblk_g = round_up(ceil_div(cout_g, 16), NB);
+    L->nchunks = ceil_div(cin_g, CK);
+    std::vector<float> pk((size_t)groups * L->nchunks * L->nblk_g * T * 16 * CK, 0.0f);
+    for (int g = 0; g < groups; ++g)
+        for (int ocl = 0; ocl < cout_g; ++ocl)
+            for (int icl = 0; icl < cin_g; ++icl)
+                for (int ky = 0; ky < kh; ++ky)
+                    for (int kx = 0; kx < kw; ++kx) {
+                        const int ch = icl / CK, kk = icl % CK, nb = ocl / 16, r = ocl % 16;
+                        const int t = ky * kw + kx;
+                        const size_t dst = ((((size_t)g * L->nchunks + ch) * L->nblk_g + nb) * T + t) * 16 * CK +
+                                           (size_t)r * CK + kk;
+                        pk[dst] = weight[(((size_t)(g * cout_g + ocl) * cin_g + icl) * kh + ky) * kw + kx];
+                    }
+    L->wpk = upload_as(ctx, pk, dtype, &L->wpk_bytes);
+    if (bias) L->bias = upload_f32(bias, cout);
+    if (keep_f32 && L->kind == CK_1x1 && groups == 1) L->w_f32 = upload_f32(weight, (size_t)cout * cin);
+    return L;
+}
+
+LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, int pad,
+                           int out_pad, const float* weight, const float* bias, int dtype) {
+    if (stride <= 0 || k <= 0 || pad < 0 || pad >= k || out_pad < 0 || out_pad >= stride ||
+        cin <= 0 || cout <= 0)
+        throw Error(ZJAI_E_MODEL, "conv_transpose2d: unsupported geometry");
+    if (dtype < DT_F32 || dtype > DT_BF16) throw Error(ZJAI_E_INVALID_ARGUMENT, "precision");
+    if (!weight) throw Error(ZJAI_E_INVALID_ARGUMENT, "conv_transpose2d: null weight");
+    if (stride != 2) throw Error(ZJAI_E_UNSUPPORTED, "conv_transpose2d: only stride 2 has a HIP kernel");
+    auto L = std::make_shared<Layer>();
+    L->transposed = true;
+    L->cin = cin; L->cout = cout; L->k = k; L->stride = stride; L->pad = pad;
+    L->out_pad = out_pad; L->dtype = dtype; L->groups = 1; L->kind = CK_T3;
+    // Per output phase (py, px): the taps whose stride parity reaches it, ky then kx ascending
+    // (reference src/nn/reference.rs:175-199), with their input row/col offsets.
+    int ky_list[2][4], nky[2] = {0, 0}, dy_list[2][4];
+    for (int pp = 0; pp < 2; ++pp)
+        for (int kk = 0; kk < k; ++kk) {
+            const int d = pp + pad - kk;
+            if (((d % 2) + 2) % 2) continue;
+            const int off = (d >= 0 ? d / 2 : -((-d) / 2)) + 1;
+            if (off < 0 || off > 2 || nky[pp] >= 2)
+                throw Error(ZJAI_E_UNSUPPORTED, "conv_transpose2d: tap reach beyond the 3x3 halo");
+            ky_list[pp][nky[pp]] = kk;
+            dy_list[pp][nky[pp]] = off;
+            ++nky[pp];
+        }
+    for (int ph = 0; ph < 4; ++ph) {
+        const int py = ph >> 1, px = ph & 1;
+        int n = 0;
+        for (int a = 0; a < nky[py]; ++a)
+            for (int b = 0; b < nky[px]; ++b) {
+                L->tap_dy[ph][n] = dy_list[py][a];
+                L->tap_dx[ph][n] = dy_list[px][b];
+                ++n;
+            }
+        L->ntaps[ph] = n;
+    }
+    const int vec = 16 / dtype_size(dtype);
+    if (cin % vec) throw Error(ZJAI_E_UNSUPPORTED, "conv_transpose2d: channels not vector aligned");
+    L->cfg = pick_cfg(cout);
+    const int NB = L->cfg.wc * L->cfg.cf;
+    const int CK = 64 / dtype_size(dtype);
+    L->nblk_g = round_up(ceil_div(cout, 16), NB);
+    L->nchunks = ceil_div(cin, CK);
+    L->phase_stride = (long long)L->nchunks * L->nblk_g * 4 * 16 * CK;
+    std::vector<float> pk((size_t)4 * L->phase_stride, 0.0f);
+    for (int ph = 0; ph < 4; ++ph) {
+        const int py = ph >> 1, px = ph & 1;
+        int t = 0;
+        for (int a = 0; a < nky[py]; ++a)
+            for (int b = 0; b < nky[px]; ++b, ++t) {
+                const int ky = ky_list[py][a], kx = ky_list[px][b];
+                for (int oc = 0; oc < cout; ++oc)
+                    for (int ic = 0; ic < cin; ++ic) {
+                        const int ch = ic / CK, kk = ic % CK, nb = oc / 16, r = oc % 16;
+                        const size_t dst = (size_t)ph * L->phase_stride +
+                                           ((((size_t)ch * L->nblk_g + nb) * 4 + t) * 16 + r) * CK + kk;
+                        pk[dst] = weight[(((size_t)ic * cout + oc) * k + ky) * k + kx];
+                    }
+            }
+    }
+    L->wpk = upload_as(ctx, pk, dtype, &L->wpk_bytes);
+    if (bias) L->bias = upload_f32(bias, cout);
+    return L;
+}
+
+// ------------------------------------------------------------------------------ conv launch
+static View view_of(const Tensor* t) { return t ? t->v : View{nullptr, 0, 0, 0}; }
+
+TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilogue& e,
+                     const TensorP& dst, const PlaneOut* plane) {
+    if (x->c != L.cin) throw Error(ZJAI_E_INVALID_ARGUMENT, "conv: input channel count mismatch");
+    if (x->dtype != L.dtype) throw Error(ZJAI_E_INVALID_ARGUMENT, "conv: input precision mismatch");
+    int OH, OW;
+    L.out_size(x->h, x->w, &OH, &OW);
+    if (OH <= 0 || OW <= 0) throw Error(ZJAI_E_INVALID_ARGUMENT, "conv: input smaller than the kernel");
+    const int ps = e.ps > 0 ? e.ps : 1;
+    if (L.cout % (ps * ps)) throw Error(ZJAI_E_INVALID_ARGUMENT, "pixel_shuffle: channels not divisible by r^2");
+    for (const Tensor* r : {e.r1, e.r2}) {
+        if (!r) continue;
+        if (r->c != L.cout || r->h != OH || r->w != OW || r->dtype != L.dtype)
+            throw Error(ZJAI_E_INVALID_ARGUMENT, "conv epilogue: residual shape differs");
+    }
+    if ((e.res != RES_NONE && !e.r1) || (e.res == RES_CAB && !e.r2))
+        throw Error(ZJAI_E_INVALID_ARGUMENT, "conv epilogue: missing residual");
+    TensorP y;
+    if (!plane) {
+        if (dst) {
+            if (dst->c != L.cout / (ps * ps) || dst->h != OH * ps || dst->w != OW * ps || dst->dtype != L.dtype)
+                throw Error(ZJAI_E_INVALID_ARGUMENT, "conv: destination shape differs");
+            y = dst;
+        } else {
+            y = ctx.alloc(L.cout / (ps * ps), OH * ps, OW * ps, L.dtype);
+        }
+    }
+    if (L.depthwise) {
+        if (e.act || e.res || ps != 1 || e.relu6_in || plane)
+            throw Error(ZJAI_E_UNSUPPORTED, "depthwise: fused epilogue");
+        ZJAI_HIP(launch_depthwise3x3(x->v, y->v, L.dtype, L.cin, x->h, x->w, L.dw_w, L.bias, 0, ctx.stream));
+        ++ctx.launches;
+        return y;
+    }
+    ConvParams p{};
+    p.x = x->v;
+    p.H = x->h;
+    p.W = x->w;
+    p.OH = OH;
+    p.OW = OW;
+    p.y = y ? y->v : View{nullptr, 0, 0, 0};
+    p.w = L.wpk;
+    p.bias = L.bias;
+    p.cin_g = L.cin / L.groups;
+    p.cout_g = L.cout / L.groups;
+    p.groups = L.groups;
+    p.nchunks = L.nchunks;
+    p.nblk_g = L.nblk_g;
+    p.phase_stride = L.phase_stride;
+    p.pad_t = L.pad_h + L.extra[0];
+    p.pad_l = L.pad_w + L.extra[1];
+    p.relu6_in = e.relu6_in;
+    p.act = e.act;
+    p.res = e.res;
+    p.r1 = view_of(e.r1);
+    p.r2 = view_of(e.r2);
+    p.ps = ps;
+    if (plane) {
+        p.out_mode = OUT_PLANE;
+        p.plane = plane->plane;
+        p.pl_row = plane->row;
+        p.pl_cstride = plane->cstride;
+        p.win_y0 = plane->win_y0;
+        p.win_x0 = plane->win_x0;
+        p.win_h = plane->win_h;
+        p.win_w = plane->win_w;
+        p.dst_y0 = plane->dst_y0;
+        p.dst_x0 = plane->dst_x0;
+        p.sv = plane->sv;
+        p.sh = plane->sh;
+        p.denorm = plane->denorm;
+        p.bit_depth = plane->bit_depth;
+    } else {
+        p.out_mode = OUT_NHWC;
+        p.sv = p.sh = 1;
+    }
+    for (int ph = 0; ph < 4; ++ph) {
+        p.ntaps[ph] = L.ntaps[ph];
+        for (int t = 0; t < 4; ++t) {
+            p.tap_dy[ph][t] = L.tap_dy[ph][t];
+            p.tap_dx[ph][t] = L.tap_dx[ph][t];
+        }
+    }
+    ZJAI_HIP(launch_conv(L.kind, L.dtype, L.cfg, p, ctx.stream));
+    ++ctx.launches;
+    return y;
+}
+
+// ----------------------------------------------------------------------- device 1x1 packing
+template <typename T>
+__global__ void k_pack_1x1(const float* w, int O, int I, int nblk, int CK, T* dst) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= O * I) return;
+    const int o = i / I, ic = i - o * I;
+    const int ch = ic / CK, kk = ic - ch * CK;
+    dst[(((long long)ch * nblk + o / 16) * 16 + o % 16) * CK + kk] = from_f32<T>(w[i]);
+}
+
+void pack_1x1_device(Context& ctx, const Layer& L, const float* w_dev) {
+    if (L.kind != CK_1x1 || L.groups != 1 || L.depthwise || L.transposed)
+        throw Error(ZJAI_E_INVALID_ARGUMENT, "pack_1x1: not a dense 1x1 layer");
+    const int n = L.cout * L.cin, CK = 64 / dtype_size(L.dtype);
+    const dim3 g((n + 255) / 256);
+    switch (L.dtype) {
+        case DT_F32: k_pack_1x1<float><<<g, 256, 0, ctx.stream>>>(w_dev, L.cout, L.cin, L.nblk_g, CK, (float*)L.wpk); break;
+        case DT_F16: k_pack_1x1<_Float16><<<g, 256, 0, ctx.stream>>>(w_dev, L.cout, L.cin, L.nblk_g, CK, (_Float16*)L.wpk); break;
+        default: k_pack_1x1<__bf16><<<g, 256, 0, ctx.stream>>>(w_dev, L.cout, L.cin, L.nblk_g, CK, (__bf16*)L.wpk); break;
+    }
+    ZJAI_HIP(hipGetLastError());
+    ++ctx.launches;
+}
+
+}  // namespace zjai

@@ -1,0 +1,200 @@
+"""Graph-level surface: the synthesis transforms (``src/model/synthesis.rs``) and the picture
+driver (``src/decoder/reconstruct.rs`` synthesis half + ``quantize_plane``), over the C-ABI."""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import HipError, check, lib
+from .nn import BTensor, Engine, _f32, _fp
+
+
+def _net_create(eng: Engine, op: str, component: int, params: dict):
+    names, ndims, dims, ptrs, keep = [], [], [], [], []
+    for name, arr in params.items():
+        a = _f32(arr)
+        keep.append(a)
+        names.append(name.encode())
+        ndims.append(a.ndim)
+        dims.extend(a.shape)
+        ptrs.append(a.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    n = len(names)
+    c_names = (ctypes.c_char_p * n)(*names)
+    c_ndims = (ctypes.c_int32 * n)(*ndims)
+    c_dims = (ctypes.c_int32 * max(len(dims), 1))(*dims)
+    c_ptrs = (ctypes.POINTER(ctypes.c_float) * n)(*ptrs)
+    h = ctypes.c_void_p()
+    check(lib().zjai_net_create(eng.handle, _lib.OPS[op], component, eng.dtype, n, c_names,
+                                c_ndims, c_dims, c_ptrs, ctypes.byref(h)), eng.handle)
+    return h
+
+
+class _Net:
+    component = 0
+
+    def __init__(self, eng: Engine, params: dict, op: str):
+        self.eng = eng
+        self.op = op
+        self._h = _net_create(eng, op, self.component, params)
+
+    @classmethod
+    def load(cls, params: dict, op: str, eng: Engine):
+        """``SynthesisPrimary::load(ck, op, eng)`` / ``SynthesisSecondary::load``: ``params``
+        maps checkpoint names to arrays."""
+        return cls(eng, params, op)
+
+    def out_size(self, h: int, w: int):
+        oh, ow = ctypes.c_int32(), ctypes.c_int32()
+        check(lib().zjai_net_out_size(self._h, h, w, ctypes.byref(oh), ctypes.byref(ow)),
+              self.eng.handle)
+        return oh.value, ow.value
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib().zjai_net_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+
+class SynthesisPrimary(_Net):
+    """Luma synthesis (``SynthesisPrimary``, src/model/synthesis.rs:233-312)."""
+    component = 0
+
+    def forward(self, eng: Engine, y_hat: BTensor, h: int, w: int) -> np.ndarray:
+        """``y_hat [160, H, W]`` -> ``[1, >=h, >=w]`` in [0, 255] (the caller crops)."""
+        oh, ow = self.out_size(h, w)
+        out = np.empty((1, oh, ow), np.float32)
+        check(lib().zjai_primary_forward(eng.handle, self._h, y_hat._h, h, w, _fp(out),
+                                         out.size), eng.handle)
+        return out
+
+
+class SynthesisSecondary(_Net):
+    """Chroma synthesis (``SynthesisSecondary``, src/model/synthesis.rs:709-1038)."""
+    component = 1
+
+    def forward(self, eng: Engine, y_hat_luma: BTensor, y_hat_chroma: BTensor, h: int,
+                w: int) -> np.ndarray:
+        oh, ow = self.out_size(h, w)
+        out = np.empty((2, oh, ow), np.float32)
+        check(lib().zjai_secondary_forward(eng.handle, self._h, y_hat_luma._h, y_hat_chroma._h,
+                                           h, w, _fp(out), out.size), eng.handle)
+        return out
+
+
+@dataclass(frozen=True)
+class Area:
+    x: int
+    y: int
+    width: int
+    height: int
+
+
+@dataclass(frozen=True)
+class SynthesisTile:
+    """``tools::tiles::SynthesisTile`` (src/tools/tiles.rs:26-35)."""
+    image: Area
+    latent: Area
+    core: Area
+    core_offset: tuple
+
+
+def synthesis_tiles(height, width, latent_h, latent_w, tiling=None, region_grid=None):
+    """``synthesis_tiles`` (src/tools/tiles.rs:39-119) computed by the library. ``tiling`` is
+    ``(tile_size, overlap)`` or None; ``region_grid`` is ``(rows, cols)`` of independent regions
+    or None."""
+    size, overlap = tiling if tiling else (0, 0)
+    rows, cols = region_grid if region_grid else (0, 0)
+    cap = 4096
+    buf = (_lib.ZjaiTile * cap)()
+    n = ctypes.c_int32()
+    check(lib().zjai_synthesis_tiles(height, width, latent_h, latent_w, size, overlap, rows, cols,
+                                     buf, cap, ctypes.byref(n)), None)
+    out = []
+    for t in buf[:n.value]:
+        out.append(SynthesisTile(Area(t.image_x, t.image_y, t.image_w, t.image_h),
+                                 Area(t.latent_x, t.latent_y, t.latent_w, t.latent_h),
+                                 Area(t.core_x, t.core_y, t.core_w, t.core_h),
+                                 (t.core_off_x, t.core_off_y)))
+    return out
+
+
+def _tile_array(tiles):
+    arr = (_lib.ZjaiTile * len(tiles))()
+    for i, t in enumerate(tiles):
+        arr[i] = _lib.ZjaiTile(t.image.x, t.image.y, t.image.width, t.image.height,
+                               t.latent.x, t.latent.y, t.latent.width, t.latent.height,
+                               t.core.x, t.core.y, t.core.width, t.core.height,
+                               t.core_offset[0], t.core_offset[1])
+    return arr
+
+
+class Picture:
+    """A planned whole-picture synthesis: latents uploaded once, every tile on one stream,
+    tile cores written (and quantised) straight into the output planes."""
+
+    def __init__(self, eng: Engine, primary: SynthesisPrimary,
+                 secondary: SynthesisSecondary | None, lh: int, lw: int, height: int,
+                 width: int, tiles, sv: int = 1, sh: int = 1, out_h: int | None = None,
+                 out_w: int | None = None, bit_depth: int = 0):
+        self.eng = eng
+        self.primary, self.secondary = primary, secondary
+        self.lh, self.lw, self.height, self.width = lh, lw, height, width
+        self.sv, self.sh, self.bit_depth = sv, sh, bit_depth
+        self.out_h = height if out_h is None else out_h
+        self.out_w = width if out_w is None else out_w
+        self.tiles = list(tiles)
+        self._tiles = _tile_array(self.tiles)
+        self._h = ctypes.c_void_p()
+        check(lib().zjai_picture_create(eng.handle, primary._h, secondary._h if secondary else None,
+                                        lh, lw, height, width, self._tiles, len(self.tiles), sv,
+                                        sh, self.out_h, self.out_w, bit_depth,
+                                        ctypes.byref(self._h)), eng.handle)
+
+    def upload(self, y_hat: np.ndarray, uv_hat: np.ndarray | None = None):
+        self._y = _f32(y_hat)
+        self._uv = _f32(uv_hat)
+        assert self._y.shape == (160, self.lh, self.lw)
+        check(lib().zjai_picture_upload(self.eng.handle, self._h, _fp(self._y), _fp(self._uv)),
+              self.eng.handle)
+
+    def run(self):
+        check(lib().zjai_picture_run(self.eng.handle, self._h), self.eng.handle)
+
+    def download(self):
+        dt = np.uint16 if self.bit_depth else np.float32
+        y = np.empty((self.out_h, self.out_w), dt)
+        ch, cw = -(-self.out_h // self.sv), -(-self.out_w // self.sh)
+        u = np.empty((ch, cw), dt) if self.secondary else None
+        v = np.empty((ch, cw), dt) if self.secondary else None
+        check(lib().zjai_picture_download(
+            self.eng.handle, self._h, y.ctypes.data_as(ctypes.c_void_p),
+            u.ctypes.data_as(ctypes.c_void_p) if u is not None else None,
+            v.ctypes.data_as(ctypes.c_void_p) if v is not None else None), self.eng.handle)
+        return y, u, v
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib().zjai_picture_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+
+def synthesize(eng: Engine, primary, secondary, y_hat, uv_hat, height, width, tiles, sv=1, sh=1,
+               out_h=None, out_w=None, bit_depth=0):
+    """``reconstruct::synthesize_with`` (src/decoder/reconstruct.rs:285-331) followed by
+    ``quantize_plane`` when ``bit_depth`` > 0: returns ``(rec_y, rec_u, rec_v)``."""
+    lh, lw = y_hat.shape[1:]
+    pic = Picture(eng, primary, secondary, lh, lw, height, width, tiles, sv, sh, out_h, out_w,
+                  bit_depth)
+    pic.upload(y_hat, uv_hat)
+    pic.run()
+    return pic.download()
