@@ -1,0 +1,236 @@
+"""Benchmark of the MI355X synthesis path (one JSON line on stdout).
+
+Workload (``config.workload``): BASELINE config 5 -- HOP luma + chroma synthesis of a 3840x2160
+4:2:0 picture, 10-bit output, tiled as the reference's encoder signals it for independent
+regions (2x3 regions, tile 640, overlap 128: 24 tiles), He-normal random-init weights, latents
+round(Laplace(0, 1.5)) at /16 resolution. One step = one whole-picture synthesis with the
+latents already resident in HBM (``Picture.run``: every tile on one HIP stream, 10-bit planes
+written by the last layers' epilogues).
+
+``value`` is the fp32-MFMA parity path (the reference computes in f32). Extra lines in ``extra``:
+the same picture on the f16 / bf16 paths and BASELINE config 4 (SOP luma 1024x1024, 8-bit).
+
+``roofline``: one profiled step (HIP events around every launch on the library's stream); the
+dominant kernel is the one with the largest summed time; achieved = its algorithmic FLOPs (all
+taps, padding included) / its summed time. ``traffic``: HBM bytes per launch of that kernel
+from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes summarised in ``profiles/`` (null if absent).
+
+``cpu_baseline``: the CPU oracle (the reference's ``nn::reference`` loops restated in C++,
+OpenMP over output channels) timed on a bounded sample of the same workload -- one synthesis
+tile of the config-5 layout, luma + chroma -- on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "synthesis decode Mpixel/s at 1MP & 4MP; conv TFLOP/s + % MFMA peak (1 GPU)"
+PEAK_TFLOPS = {"f32": 157.3, "f16": 2500.0, "bf16": 2500.0}
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_workload(name, eng):
+    from zenjpegai_amd import model, synth
+    if name == "cfg5":
+        h, w, op, sv, sh, bits = 2160, 3840, "hop", 2, 2, 10
+        lh, lw = 135, 240
+        tiles = model.synthesis_tiles(h, w, lh, lw, (640, 128), (2, 3))
+        uv = True
+    elif name == "cfg4":
+        h, w, op, sv, sh, bits = 1024, 1024, "sop", 1, 1, 8
+        lh, lw = 64, 64
+        tiles = model.synthesis_tiles(h, w, lh, lw, None)
+        uv = False
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    py = synth.random_params(op, "y", seed=1)
+    y = synth.latent(1, f"{name}/y", 160, lh, lw)
+    prim = model.SynthesisPrimary.load(py, op, eng)
+    sec, uvl, puv = None, None, None
+    if uv:
+        puv = synth.random_params(op, "uv", seed=1)
+        sec = model.SynthesisSecondary.load(puv, op, eng)
+        uvl = synth.latent(1, f"{name}/uv", 96, lh, lw)
+    pic = model.Picture(eng, prim, sec, lh, lw, h, w, tiles, sv, sh, bit_depth=bits)
+    pic.upload(y, uvl)
+    return pic, dict(h=h, w=w, op=op, tiles=len(tiles), bits=bits, sv=sv, sh=sh,
+                     latent=(lh, lw), py=py, y=y, uvl=uvl, puv=puv, tile_list=tiles)
+
+
+def time_steps(eng, pic, steps, warmup):
+    for _ in range(warmup):
+        pic.run()
+    eng.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        pic.run()
+    eng.sync()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def profile_step(eng, pic):
+    eng.profile_begin()
+    pic.run()
+    recs = eng.profile_end()
+    by = {}
+    for name, flops, nbytes, ms in recs:
+        d = by.setdefault(name, {"count": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
+        d["count"] += 1
+        d["ms"] += ms
+        d["flops"] += flops
+        d["bytes"] += nbytes
+    return by
+
+
+def read_traffic(kernel, workload):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        e = t.get(workload, {}).get(kernel)
+        return None if e is None else float(e["bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def cpu_baseline(info, seconds_cap=60.0):
+    """Times the oracle on one config-5 tile (Y + UV)."""
+    import oracle.graphs as og
+    t = max(info["tile_list"], key=lambda t: t.image.width * t.image.height)
+    lat = t.latent
+    y = info["y"][:, lat.y:lat.y + lat.height, lat.x:lat.x + lat.width].copy()
+    t0 = time.perf_counter()
+    og.primary(info["py"], info["op"], y, t.image.height, t.image.width)
+    if info["puv"] is not None:
+        uv = info["uvl"][:, lat.y:lat.y + lat.height, lat.x:lat.x + lat.width].copy()
+        og.secondary(info["puv"], info["op"], y, uv, t.image.height, t.image.width)
+    dt = time.perf_counter() - t0
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    mpix = t.image.width * t.image.height / dt / 1e6
+    return {"value": round(mpix, 4), "unit": "Mpixel/s", "cores": cores, "kind": "port",
+            "sample": (f"one {t.image.width}x{t.image.height} synthesis tile of the config-5 "
+                       f"layout (HOP Y+UV), oracle nn::reference loops, {dt:.1f} s"),
+            "seconds": round(dt, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="cfg5", choices=["cfg5", "cfg4"])
+    ap.add_argument("--precision", default="f32", choices=["f32", "f16", "bf16"])
+    ap.add_argument("--no-extra", action="store_true", help="skip the extra precision / cfg4 runs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--profile-out", default=None, help="write the per-kernel profile (JSON)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only; the synthesis tiles would shard "
+              "across GPUs with no collective (see DESIGN.md), but no multi-GPU figure is "
+              "produced.", file=sys.stderr)
+        sys.exit(2)
+
+    from zenjpegai_amd import nn
+
+    eng = nn.Engine(0, args.precision)
+    log(f"[bench] building workload {args.workload} ({args.precision})")
+    pic, info = make_workload(args.workload, eng)
+    log(f"[bench] {info['tiles']} tiles; warmup {args.warmup}, timing {args.steps} steps")
+    ms = time_steps(eng, pic, args.steps, args.warmup)
+    pixels = info["h"] * info["w"]
+    value = pixels / (ms / 1e3) / 1e6
+    log(f"[bench] {ms:.2f} ms/step -> {value:.2f} Mpixel/s")
+    prof = profile_step(eng, pic)
+    total_ms = sum(d["ms"] for d in prof.values())
+    conv = {k: d for k, d in prof.items() if k.startswith("conv_igemm")}
+    conv_flops = sum(d["flops"] for d in conv.values())
+    conv_ms = sum(d["ms"] for d in conv.values())
+    dom_name, dom = max(prof.items(), key=lambda kv: kv[1]["ms"])
+    if dom["flops"] > 0:
+        ach = dom["flops"] / (dom["ms"] / 1e3) / 1e12
+        peak = PEAK_TFLOPS[args.precision]
+        roof = {"bound": "mfma", "achieved": round(ach, 3), "peak": peak, "unit": "TFLOP/s"}
+    else:
+        ach = dom["bytes"] / (dom["ms"] / 1e3) / 1e9
+        peak = PEAK_HBM_GBS
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": peak, "unit": "GB/s"}
+    roof["frac"] = round(ach / peak, 4)
+    roof["traffic"] = read_traffic(dom_name, args.workload)
+    roof["kernel"] = dom_name
+    roof["launches"] = dom["count"]
+    roof["avg_launch_us"] = round(dom["ms"] * 1e3 / dom["count"], 2)
+    roof["algorithmic_per_launch"] = round((dom["flops"] or dom["bytes"]) / dom["count"], 1)
+    if args.profile_out:
+        with open(args.profile_out, "w") as f:
+            json.dump({"workload": args.workload, "precision": args.precision, "kernels": prof},
+                      f, indent=1, sort_keys=True)
+
+    extra = {
+        "device_ms_per_step": round(eng.stats()["last_run_ms"], 3),
+        "profiled_kernel_ms": round(total_ms, 3),
+        "conv_tflops": round(conv_flops / (conv_ms / 1e3) / 1e12, 3) if conv_ms else None,
+        "conv_frac_of_peak": round(conv_flops / (conv_ms / 1e3) / 1e12 / PEAK_TFLOPS[args.precision], 4) if conv_ms else None,
+        "conv_share_of_kernel_time": round(conv_ms / total_ms, 4) if total_ms else None,
+        "launches_per_step": sum(d["count"] for d in prof.values()),
+    }
+    if not args.no_extra:
+        for prec in ("bf16", "f16"):
+            if prec == args.precision:
+                continue
+            e2 = nn.Engine(0, prec)
+            p2, _ = make_workload(args.workload, e2)
+            ms2 = time_steps(e2, p2, args.steps, args.warmup)
+            pr2 = profile_step(e2, p2)
+            cv = {k: d for k, d in pr2.items() if k.startswith("conv_igemm")}
+            cf, cm = sum(d["flops"] for d in cv.values()), sum(d["ms"] for d in cv.values())
+            extra[f"{args.workload}_{prec}_mpix_s"] = round(pixels / (ms2 / 1e3) / 1e6, 3)
+            extra[f"{args.workload}_{prec}_conv_tflops"] = round(cf / (cm / 1e3) / 1e12, 3)
+            log(f"[bench] {prec}: {ms2:.2f} ms/step")
+            del p2, e2
+        if args.workload != "cfg4":
+            e3 = nn.Engine(0, args.precision)
+            p3, i3 = make_workload("cfg4", e3)
+            ms3 = time_steps(e3, p3, max(args.steps, 10), args.warmup)
+            extra[f"cfg4_sop_1mp_{args.precision}_mpix_s"] = round(i3["h"] * i3["w"] / (ms3 / 1e3) / 1e6, 3)
+            log(f"[bench] cfg4: {ms3:.3f} ms/step")
+            del p3, e3
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] timing the CPU oracle on one tile")
+        cpu = cpu_baseline(info)
+        log(f"[bench] cpu: {cpu}")
+
+    out = {
+        "metric": METRIC, "value": round(value, 3), "unit": "Mpixel/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": args.precision, "data": "synthetic (He-normal random-init weights, Laplace latents)",
+        "config": {
+            "workload": ("cfg5: HOP Y+UV synthesis 3840x2160 4:2:0 10-bit, 2x3 independent "
+                         "regions, tile 640 / overlap 128 (24 tiles), latents resident in HBM"
+                         if args.workload == "cfg5" else
+                         "cfg4: SOP luma synthesis 1024x1024 8-bit, untiled, latent resident"),
+            "picture": f"{info['w']}x{info['h']}", "tiles": info["tiles"],
+            "precision_path": args.precision},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -96,6 +96,19 @@ typedef struct zjai_stats {
 } zjai_stats;
 /* Replaces the reference's `DecodeStats` probe (src/decoder/stats.rs:301) for device work. */
 ZJAI_API int32_t zjai_get_stats(zjai_ctx* ctx, zjai_stats* out);
+/* Per-launch profile, the device-side counterpart of the reference's GPU `Timing` / per-dispatch
+ * profile (gpu/src/synthesis.rs:758): between begin and end every kernel launch of the context
+ * is bracketed by HIP events on its stream. zjai_profile_end synchronises and writes up to `cap`
+ * records (kernel name as profilers print it, algorithmic FLOPs and compulsory HBM bytes of the
+ * launch, measured milliseconds); *n = number of launches profiled. */
+typedef struct zjai_prof_record {
+    char name[96];
+    double flops;
+    double bytes;
+    float ms;
+} zjai_prof_record;
+ZJAI_API int32_t zjai_profile_begin(zjai_ctx* ctx);
+ZJAI_API int32_t zjai_profile_end(zjai_ctx* ctx, zjai_prof_record* out, int32_t cap, int32_t* n);
 /* Returns cached pool blocks to the device (`release_buffers`, src/nn/fast/tensor.rs:122). */
 ZJAI_API int32_t zjai_release_buffers(zjai_ctx* ctx);
 

@@ -47,6 +47,11 @@ class ZjaiStats(ctypes.Structure):
                 ("pool_cached", ctypes.c_uint64)]
 
 
+class ZjaiProfRecord(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 96), ("flops", ctypes.c_double),
+                ("bytes", ctypes.c_double), ("ms", ctypes.c_float)]
+
+
 _vp = ctypes.c_void_p
 _pp = ctypes.POINTER(ctypes.c_void_p)
 _i32 = ctypes.c_int32
@@ -62,6 +67,8 @@ PROTOTYPES = {
     "zjai_set_stop": [_vp, _i32],
     "zjai_get_stats": [_vp, ctypes.POINTER(ZjaiStats)],
     "zjai_release_buffers": [_vp],
+    "zjai_profile_begin": [_vp],
+    "zjai_profile_end": [_vp, ctypes.POINTER(ZjaiProfRecord), _i32, _i32p],
     "zjai_tensor_create": [_vp, _i32, _i32, _i32, _i32, _pp],
     "zjai_tensor_from_planar": [_vp, _f32p, _i32, _i32, _i32, _i32, _pp],
     "zjai_tensor_to_planar": [_vp, _vp, _f32p, ctypes.c_size_t],

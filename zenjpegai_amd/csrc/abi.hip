@@ -62,8 +62,10 @@ TensorP planar_upload(Context& c, const float* data, int ch, int h, int w, int d
     float* stage = (float*)c.pool.alloc(n * 4);
     std::shared_ptr<void> keep(stage, [&c](void* q) { c.pool.release(q); });
     ZJAI_HIP(hipMemcpyAsync(stage, data, n * 4, hipMemcpyHostToDevice, c.stream));
-    ZJAI_HIP(launch_planar_to_nhwc(stage, ch, h, w, 0, 0, h, w, t->v, dtype, c.stream));
-    ++c.launches;
+    {
+        LaunchScope sc(c, "k_planar_to_nhwc", 0.0, (4.0 + dtype_size(dtype)) * n);
+        ZJAI_HIP(launch_planar_to_nhwc(stage, ch, h, w, 0, 0, h, w, t->v, dtype, c.stream));
+    }
     ZJAI_HIP(hipStreamSynchronize(c.stream));
     return t;
 }
@@ -146,6 +148,36 @@ extern "C" int32_t zjai_get_stats(zjai_ctx* ctx, zjai_stats* out) {
     return ZJAI_OK;
 }
 
+extern "C" int32_t zjai_profile_begin(zjai_ctx* ctx) {
+    if (!ctx) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
+        ctx->c.prof.clear();
+        ctx->c.ev_used = 0;
+        ctx->c.profiling = true;
+    });
+}
+
+extern "C" int32_t zjai_profile_end(zjai_ctx* ctx, zjai_prof_record* out, int32_t cap, int32_t* n) {
+    if (!ctx || !n || cap < 0 || (cap && !out)) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        ctx->c.profiling = false;
+        ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
+        *n = (int32_t)ctx->c.prof.size();
+        for (int32_t i = 0; i < std::min(cap, *n); ++i) {
+            const ProfRec& r = ctx->c.prof[i];
+            zjai_prof_record& o = out[i];
+            std::memset(o.name, 0, sizeof o.name);
+            std::strncpy(o.name, r.name.c_str(), sizeof o.name - 1);
+            o.flops = r.flops;
+            o.bytes = r.bytes;
+            ZJAI_HIP(hipEventElapsedTime(&o.ms, r.a, r.b));
+        }
+        ctx->c.prof.clear();
+        ctx->c.ev_used = 0;
+    });
+}
+
 extern "C" int32_t zjai_release_buffers(zjai_ctx* ctx) {
     if (!ctx) return ZJAI_E_INVALID_ARGUMENT;
     return guard(ctx, [&] {
@@ -182,8 +214,10 @@ extern "C" int32_t zjai_tensor_to_planar(zjai_ctx* ctx, const zjai_tensor* t, fl
         if (n == 0) return;
         float* stage = (float*)ctx->c.pool.alloc(n * 4);
         std::shared_ptr<void> keep(stage, [ctx](void* q) { ctx->c.pool.release(q); });
-        ZJAI_HIP(launch_nhwc_to_planar(x.v, x.dtype, x.c, x.h, x.w, stage, ctx->c.stream));
-        ++ctx->c.launches;
+        {
+            LaunchScope sc(ctx->c, "k_nhwc_to_planar", 0.0, (4.0 + dtype_size(x.dtype)) * n);
+            ZJAI_HIP(launch_nhwc_to_planar(x.v, x.dtype, x.c, x.h, x.w, stage, ctx->c.stream));
+        }
         ZJAI_HIP(hipMemcpyAsync(data, stage, n * 4, hipMemcpyDeviceToHost, ctx->c.stream));
         ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
     });
@@ -221,8 +255,8 @@ extern "C" int32_t zjai_tensor_cat(zjai_ctx* ctx, const zjai_tensor* const* part
         int c0 = 0;
         for (int i = 0; i < n; ++i) {
             const Tensor& p = *parts[i]->t;
+            LaunchScope sc(ctx->c, "k_copy", 0.0, 2.0 * dtype_size(p.dtype) * p.c * p.h * p.w);
             ZJAI_HIP(launch_copy(p.v, channel_view(y, c0, p.c)->v, p.dtype, p.c, p.h, p.w, ctx->c.stream));
-            ++ctx->c.launches;
             c0 += p.c;
         }
         *out = new zjai_tensor{y};
@@ -298,8 +332,8 @@ static int32_t eltwise(zjai_ctx* ctx, int op, zjai_tensor* x, const zjai_tensor*
             need(a.c == b.c && a.h == b.h && a.w == b.w && a.dtype == b.dtype, "shapes differ");
         }
         need(a.c % 4 == 0, "channel count must be a multiple of 4");
+        LaunchScope sc(ctx->c, "k_eltwise", 0.0, (op >= EL_ADD ? 3.0 : 2.0) * dtype_size(a.dtype) * a.c * a.h * a.w);
         ZJAI_HIP(launch_eltwise(op, a.v, s ? s->t->v : a.v, a.dtype, a.c, a.h, a.w, ctx->c.stream));
-        ++ctx->c.launches;
     });
 }
 
@@ -320,8 +354,8 @@ extern "C" int32_t zjai_pixel_shuffle(zjai_ctx* ctx, const zjai_tensor* x, int32
         const int co = a.c / (r * r);
         need(co % 4 == 0, "pixel_shuffle: output channels must be a multiple of 4");
         TensorP y = ctx->c.alloc(co, a.h * r, a.w * r, a.dtype);
+        LaunchScope sc(ctx->c, "k_pixel_shuffle", 0.0, 2.0 * dtype_size(a.dtype) * a.c * a.h * a.w);
         ZJAI_HIP(launch_pixel_shuffle(a.v, y->v, a.dtype, co, a.h, a.w, r, ctx->c.stream));
-        ++ctx->c.launches;
         *out = new zjai_tensor{y};
     });
 }
@@ -337,8 +371,10 @@ extern "C" int32_t zjai_layer_norm_channels(zjai_ctx* ctx, const zjai_tensor* x,
         ZJAI_HIP(hipMemcpyAsync(d, weight, sizeof(float) * a.c, hipMemcpyHostToDevice, ctx->c.stream));
         ZJAI_HIP(hipMemcpyAsync(d + a.c, bias, sizeof(float) * a.c, hipMemcpyHostToDevice, ctx->c.stream));
         TensorP y = ctx->c.alloc(a.c, a.h, a.w, a.dtype);
-        ZJAI_HIP(launch_layer_norm(a.v, y->v, a.dtype, a.c, a.h, a.w, d, d + a.c, ctx->c.stream));
-        ++ctx->c.launches;
+        {
+            LaunchScope sc(ctx->c, "k_layer_norm", 0.0, 2.0 * dtype_size(a.dtype) * a.c * a.h * a.w);
+            ZJAI_HIP(launch_layer_norm(a.v, y->v, a.dtype, a.c, a.h, a.w, d, d + a.c, ctx->c.stream));
+        }
         ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
         *out = new zjai_tensor{y};
     });
@@ -352,7 +388,7 @@ extern "C" int32_t zjai_channel_attention(zjai_ctx* ctx, const zjai_tensor* qkv,
         need(heads > 0 && a.c % (3 * heads) == 0, "attention: channel / head counts");
         const int dim = a.c / 3, c = dim / heads;
         need(dim % 8 == 0, "attention: dim must be a multiple of 8");
-        need(heads * (c * c + 2 * c) <= 256 * 20, "attention: head size too large");
+        need(c >= 1 && c <= 32, "attention: at most 32 channels per head");
         // attn . v as a 1x1 conv over v with the block-diagonal attention matrix as its weight
         // (identity projection folded in).
         std::vector<float> eye((size_t)dim * dim, 0.0f);
@@ -361,17 +397,7 @@ extern "C" int32_t zjai_channel_attention(zjai_ctx* ctx, const zjai_tensor* qkv,
         float* temp = (float*)ctx->c.pool.alloc(sizeof(float) * heads);
         std::shared_ptr<void> kt(temp, [ctx](void* q) { ctx->c.pool.release(q); });
         ZJAI_HIP(hipMemcpyAsync(temp, temperature, sizeof(float) * heads, hipMemcpyHostToDevice, ctx->c.stream));
-        const int nchunk = attention_gram_chunks(a.h, a.w);
-        const int total = heads * (c * c + 2 * c);
-        double* partial = (double*)ctx->c.pool.alloc(sizeof(double) * (size_t)std::max(nchunk, 1) * total);
-        std::shared_ptr<void> kp(partial, [ctx](void* q) { ctx->c.pool.release(q); });
-        float* scratch = (float*)ctx->c.pool.alloc(sizeof(float) * (size_t)(dim * c + dim * dim));
-        std::shared_ptr<void> ks(scratch, [ctx](void* q) { ctx->c.pool.release(q); });
-        ZJAI_HIP(launch_attention_gram(a.v, a.dtype, dim, heads, a.h, a.w, partial, ctx->c.stream));
-        ZJAI_HIP(launch_attention_softmax_fold(partial, nchunk, dim, heads, temp, L->w_f32, scratch,
-                                               scratch + dim * c, ctx->c.stream));
-        ctx->c.launches += 2;
-        pack_1x1_device(ctx->c, *L, scratch + dim * c);
+        attention_fold(ctx->c, qkv->t, heads, temp, *L);
         TensorP y = conv_forward(ctx->c, *L, channel_view(qkv->t, 2 * dim, dim), Epilogue{});
         ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
         *out = new zjai_tensor{y};
@@ -671,9 +697,11 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
         for (const zjai_tile& t : pic->tiles) {
             c.check_stop();
             TensorP by = c.alloc(160, t.latent_h, t.latent_w, dt);
-            ZJAI_HIP(launch_planar_to_nhwc(pic->y_hat, 160, pic->lh, pic->lw, t.latent_x, t.latent_y, t.latent_h,
-                                           t.latent_w, by->v, dt, c.stream));
-            ++c.launches;
+            {
+                LaunchScope sc(c, "k_planar_to_nhwc", 0.0, (4.0 + dtype_size(dt)) * 160 * t.latent_h * t.latent_w);
+                ZJAI_HIP(launch_planar_to_nhwc(pic->y_hat, 160, pic->lh, pic->lw, t.latent_x, t.latent_y,
+                                               t.latent_h, t.latent_w, by->v, dt, c.stream));
+            }
             // synthesize_luma_into (src/decoder/reconstruct.rs:379-411): core rows/cols that
             // fall inside the displayed picture.
             PlaneOut py;
@@ -689,9 +717,11 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
             primary_forward(c, *pic->net_y, by, t.image_h, t.image_w, py);
             if (pic->net_uv) {
                 TensorP buv = c.alloc(96, t.latent_h, t.latent_w, dt);
-                ZJAI_HIP(launch_planar_to_nhwc(pic->uv_hat, 96, pic->lh, pic->lw, t.latent_x, t.latent_y,
-                                               t.latent_h, t.latent_w, buv->v, dt, c.stream));
-                ++c.launches;
+                {
+                    LaunchScope sc(c, "k_planar_to_nhwc", 0.0, (4.0 + dtype_size(dt)) * 96 * t.latent_h * t.latent_w);
+                    ZJAI_HIP(launch_planar_to_nhwc(pic->uv_hat, 96, pic->lh, pic->lw, t.latent_x, t.latent_y,
+                                                   t.latent_h, t.latent_w, buv->v, dt, c.stream));
+                }
                 // synthesize_chroma_into (src/decoder/reconstruct.rs:416-464)
                 PlaneOut pu = py;
                 pu.plane = pic->out_uv;

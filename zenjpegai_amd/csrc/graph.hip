@@ -248,9 +248,9 @@ struct Fwd {
     }
     TensorP layer_norm(const std::string& pfx, const TensorP& x) {
         TensorP y = ctx.alloc(x->c, x->h, x->w, x->dtype);
+        LaunchScope sc(ctx, "k_layer_norm", 0.0, 2.0 * dtype_size(x->dtype) * x->c * x->h * x->w);
         ZJAI_HIP(launch_layer_norm(x->v, y->v, x->dtype, x->c, x->h, x->w, net.vec.at(pfx + ".weight"),
                                    net.vec.at(pfx + ".bias"), ctx.stream));
-        ++ctx.launches;
         return y;
     }
     // TransformerBlock::forward (src/model/attention.rs:328-372)
@@ -260,18 +260,8 @@ struct Fwd {
         t = conv(p + ".prep_data.conv1", t);
         t = conv(p + ".prep_data.conv2", t);  // depthwise 3x3
         // channel_attention + project_out: fold attn into the projection, run it on v.
-        const int nchunk = attention_gram_chunks(t->h, t->w);
-        const int c = dim / heads, total = heads * (c * c + 2 * c);
-        double* partial = (double*)ctx.pool.alloc(sizeof(double) * (size_t)nchunk * total);
-        std::shared_ptr<void> pk(partial, [this](void* q) { ctx.pool.release(q); });
-        ZJAI_HIP(launch_attention_gram(t->v, t->dtype, dim, heads, t->h, t->w, partial, ctx.stream));
-        float* scratch = (float*)ctx.pool.alloc(sizeof(float) * (size_t)(dim * c + dim * dim));
-        std::shared_ptr<void> sk(scratch, [this](void* q) { ctx.pool.release(q); });
         const Layer& proj = L(p + ".attn.project_out");
-        ZJAI_HIP(launch_attention_softmax_fold(partial, nchunk, dim, heads, net.vec.at(p + ".attn.temperature"),
-                                               proj.w_f32, scratch, scratch + dim * c, ctx.stream));
-        ctx.launches += 2;
-        pack_1x1_device(ctx, proj, scratch + dim * c);
+        attention_fold(ctx, t, heads, net.vec.at(p + ".attn.temperature"), proj);
         Epilogue ea;
         ea.res = RES_ADD;
         ea.r1 = x.get();
@@ -282,8 +272,12 @@ struct Fwd {
         u = conv(p + ".ffn.project_in", u);
         const Layer& dw = L(p + ".ffn.dwconv");
         TensorP f = ctx.alloc(hidden, u->h, u->w, u->dtype);
-        ZJAI_HIP(launch_depthwise3x3(u->v, f->v, u->dtype, 2 * hidden, u->h, u->w, dw.dw_w, dw.bias, hidden, ctx.stream));
-        ++ctx.launches;
+        {
+            LaunchScope sc(ctx, "k_depthwise3x3", 2.0 * 9 * 2 * hidden * u->h * u->w,
+                           (double)dtype_size(u->dtype) * 3 * hidden * u->h * u->w);
+            ZJAI_HIP(launch_depthwise3x3(u->v, f->v, u->dtype, 2 * hidden, u->h, u->w, dw.dw_w, dw.bias, hidden,
+                                         ctx.stream));
+        }
         u.reset();
         Epilogue ef;
         ef.res = RES_ADD;
@@ -392,13 +386,22 @@ void secondary_forward(Context& ctx, const Net& net, const TensorP& y_luma, cons
         throw Error(ZJAI_E_INVALID_ARGUMENT, "chroma latent larger than the luma latent");
     Fwd f{ctx, net};
     const int dt = net.dtype;
+    const double es = dtype_size(dt);
     TensorP cat = ctx.alloc(256, lh, lw, dt);
-    ZJAI_HIP(launch_copy(y_luma->v, cat->v, dt, 160, lh, lw, ctx.stream));
-    ZJAI_HIP(launch_copy(y_chroma->v, channel_view(cat, 160, 96)->v, dt, 96, lh, lw, ctx.stream));
+    {
+        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * 160 * lh * lw);
+        ZJAI_HIP(launch_copy(y_luma->v, cat->v, dt, 160, lh, lw, ctx.stream));
+    }
+    {
+        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * 96 * lh * lw);
+        ZJAI_HIP(launch_copy(y_chroma->v, channel_view(cat, 160, 96)->v, dt, 96, lh, lw, ctx.stream));
+    }
     TensorP x = ctx.alloc(144, lh, lw, dt);
     f.conv("first_stage.conv1", cat, Epilogue{}, channel_view(x, 0, 48));
-    ZJAI_HIP(launch_copy(y_chroma->v, channel_view(x, 48, 96)->v, dt, 96, lh, lw, ctx.stream));
-    ctx.launches += 3;
+    {
+        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * 96 * lh * lw);
+        ZJAI_HIP(launch_copy(y_chroma->v, channel_view(x, 48, 96)->v, dt, 96, lh, lw, ctx.stream));
+    }
     cat.reset();
     ctx.check_stop();
     const int h8 = ceil_div(h, 8), w8 = ceil_div(w, 8);

@@ -41,15 +41,17 @@ hipError_t launch_depthwise3x3(View src, View dst, int dtype, int C, int h, int 
 // Layer norm over channels per position (f64 sums), src -> dst.
 hipError_t launch_layer_norm(View src, View dst, int dtype, int C, int h, int w,
                              const float* weight, const float* bias, hipStream_t s);
-// Channel attention, phase 1: per-head Gram partial sums over position chunks.
-// qkv view holds 3*dim channels. Writes partial[nchunk][heads][c*c + 2c] f64.
+// Channel attention (src/nn/fast/math.rs:512-603), three phases:
+// 1. per-head Gram partial sums over chunks of positions (f32 MFMA): qkv view holds 3*dim
+//    channels; partial[nchunk][heads][c*c + 2c] f32 (c = dim / heads, 16 or 32);
+// 2. reduction (f64), normalisation, temperature and softmax -> attn [dim][c] f32;
+// 3. fold with the output projection proj [dim][dim] into a packed 1x1 conv weight.
 int attention_gram_chunks(int h, int w);
 hipError_t launch_attention_gram(View qkv, int dtype, int dim, int heads, int h, int w,
-                                 double* partial, hipStream_t s);
-// Phase 2: reduce partials, normalise, temperature, softmax -> attn [dim][c] f32, then fold the
-// output projection: wfold[o][head*c + j] = sum_i proj[o][head*c + i] * attn[head*c + i][j].
-hipError_t launch_attention_softmax_fold(const double* partial, int nchunk, int dim, int heads,
-                                         const float* temperature, const float* proj,
-                                         float* attn, float* wfold, hipStream_t s);
+                                 float* partial, hipStream_t s);
+hipError_t launch_attention_softmax(const float* partial, int nchunk, int dim, int heads,
+                                    const float* temperature, float* attn, hipStream_t s);
+hipError_t launch_attention_fold(const float* proj, const float* attn, int dim, int heads, int dtype,
+                                 int nblk, void* wpk, hipStream_t s);
 
 }  // namespace zjai

@@ -196,109 +196,129 @@ __global__ void k_layer_norm(View src, View dst, int C, int h, int w, const floa
 }
 
 // ------------------------------------------------------------------------ channel attention
-// Gram partial sums: per chunk of ATT_POS positions, entries per head are q_i.k_j (c*c),
-// |q_i|^2 (c) and |k_j|^2 (c). f32 products accumulated in f32 per chunk, stored as f64.
-constexpr int ATT_POS = 256, ATT_SUB = 32, ATT_MAXE = 20;
+// Per head h (c = dim / heads channels): S_ij = q_i . k_j, |q_i|^2 and |k_j|^2 summed over the
+// n = h*w positions. One wave per head per chunk of ATT_POS positions runs the sums on f32
+// MFMA (M = q channels, N = k channels, K = 4 positions per instruction); the chunk partials
+// are reduced in f64 by the softmax kernel.
+constexpr int ATT_POS = 256;
 
 int attention_gram_chunks(int h, int w) { return (h * w + ATT_POS - 1) / ATT_POS; }
 
 template <typename T>
-__global__ void __launch_bounds__(256) k_attention_gram(View qkv, int dim, int heads, int h, int w,
-                                                        double* partial) {
-    extern __shared__ float s_qk[];  // [ATT_SUB][2*dim]
-    const int c = dim / heads, E = c * c + 2 * c, total = heads * E;
-    const int n = h * w, tid = threadIdx.x;
-    float acc[ATT_MAXE];
-    int ea[ATT_MAXE], eb[ATT_MAXE];
+__global__ void __launch_bounds__(256) k_attention_gram(View qkv, int dim, int heads, int n, int w,
+                                                        float* partial) {
+    const int c = dim / heads, nb = (c + 15) / 16, E = c * c + 2 * c;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int m = lane & 15, kq = lane >> 4;
+    const int p0 = blockIdx.x * ATT_POS;
+    const int p1 = min(p0 + ATT_POS, n);
+    const T* base = (const T*)qkv.p + qkv.c_off;
+    for (int hd = wave; hd < heads; hd += 4) {
+        f32x4 g[2][2], dq[2], dk[2];
+        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int k = 0; k < ATT_MAXE; ++k) {
-        acc[k] = 0.0f;
-        const int e = tid + k * 256;
-        ea[k] = eb[k] = -1;
-        if (e < total) {
-            const int hd = e / E, r = e - hd * E;
-            if (r < c * c) { ea[k] = hd * c + r / c; eb[k] = dim + hd * c + r % c; }
-            else if (r < c * c + c) { ea[k] = eb[k] = hd * c + (r - c * c); }
-            else { ea[k] = eb[k] = dim + hd * c + (r - c * c - c); }
+        for (int a = 0; a < 2; ++a) {
+            dq[a] = dk[a] = z;
+            g[a][0] = g[a][1] = z;
         }
-    }
-    const int base = blockIdx.x * ATT_POS;
-    for (int sub = 0; sub < ATT_POS; sub += ATT_SUB) {
-        __syncthreads();
-        for (int u = tid; u < ATT_SUB * (2 * dim / 4); u += 256) {
-            const int pl = u / (2 * dim / 4), cq = u - pl * (2 * dim / 4);
-            const int p = base + sub + pl;
-            f32x4 v = {0, 0, 0, 0};
-            if (p < n) v = load4<T>(at<T>(qkv, p / w, p % w, cq * 4));
-            *(f32x4*)&s_qk[pl * 2 * dim + cq * 4] = v;
-        }
-        __syncthreads();
+        for (int p = p0; p < p1; p += 4) {
+            const int pos = p + kq;
+            float aq[2] = {0.0f, 0.0f}, ak[2] = {0.0f, 0.0f};
+            if (pos < p1) {
+                const int y = pos / w, x = pos - y * w;
+                const T* px = base + (long long)y * qkv.row + (long long)x * qkv.cs + hd * c + m;
 #pragma unroll
-        for (int k = 0; k < ATT_MAXE; ++k) {
-            if (ea[k] < 0) continue;
-            float a = acc[k];
-            for (int pl = 0; pl < ATT_SUB; ++pl) a = fmaf(s_qk[pl * 2 * dim + ea[k]], s_qk[pl * 2 * dim + eb[k]], a);
-            acc[k] = a;
-        }
-    }
+                for (int b = 0; b < 2; ++b)
+                    if (b * 16 + m < c) {
+                        aq[b] = to_f32(px[b * 16]);
+                        ak[b] = to_f32(px[dim + b * 16]);
+                    }
+            }
 #pragma unroll
-    for (int k = 0; k < ATT_MAXE; ++k) {
-        const int e = tid + k * 256;
-        if (e < total) partial[(long long)blockIdx.x * total + e] = (double)acc[k];
+            for (int bi = 0; bi < 2; ++bi) {
+                if (bi >= nb) continue;
+#pragma unroll
+                for (int bj = 0; bj < 2; ++bj)
+                    if (bj < nb) g[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[bi], ak[bj], g[bi][bj], 0, 0, 0);
+                dq[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[bi], aq[bi], dq[bi], 0, 0, 0);
+                dk[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(ak[bi], ak[bi], dk[bi], 0, 0, 0);
+            }
+        }
+        // Lane l holds D[4 * (l / 16) + i][l % 16] of each 16x16 tile.
+        float* out = partial + ((long long)blockIdx.x * heads + hd) * E;
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+            if (bi >= nb) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 4 * kq + i;
+                if (bi * 16 + r >= c) continue;
+#pragma unroll
+                for (int bj = 0; bj < 2; ++bj)
+                    if (bj < nb && bj * 16 + m < c) out[(bi * 16 + r) * c + bj * 16 + m] = g[bi][bj][i];
+                if (r == m) {
+                    out[c * c + bi * 16 + m] = dq[bi][i];
+                    out[c * c + c + bi * 16 + m] = dk[bi][i];
+                }
+            }
+        }
     }
 }
 
-// Reduce partials, normalise (F.normalize eps 1e-12), scale by temperature, softmax with the
-// Cephes exp and an f64 sum (src/nn/fast/math.rs:560-577), then fold the projection.
-__global__ void __launch_bounds__(256) k_attention_softmax_fold(const double* partial, int nchunk,
-                                                                int dim, int heads,
-                                                                const float* temperature,
-                                                                const float* proj, float* attn,
-                                                                float* wfold) {
-    extern __shared__ double s_red[];  // [heads * E]
-    const int c = dim / heads, E = c * c + 2 * c, total = heads * E, tid = threadIdx.x;
-    for (int e = tid; e < total; e += 256) {
-        double s = 0.0;
-        for (int k = 0; k < nchunk; ++k) s += partial[(long long)k * total + e];
-        s_red[e] = s;
+// One wave per attention row (head hd, query i): reduce the chunk partials in f64, normalise
+// (F.normalize, eps 1e-12), scale by the temperature, softmax with the Cephes exp and an f64 sum
+// in index order (src/nn/fast/math.rs:558-577).
+__global__ void __launch_bounds__(64) k_attention_softmax(const float* partial, int nchunk, int dim,
+                                                          int heads, const float* temperature,
+                                                          float* attn) {
+    __shared__ double s_qq;
+    __shared__ float s_e[64];
+    const int row = blockIdx.x, c = dim / heads, hd = row / c, i = row - hd * c;
+    const int E = c * c + 2 * c, lane = threadIdx.x;
+    double sqk = 0.0, skk = 0.0, sqq = 0.0;
+    if (lane < c) {
+        for (int k = 0; k < nchunk; ++k) {
+            const float* b = partial + ((long long)k * heads + hd) * E;
+            sqk += (double)b[i * c + lane];
+            skk += (double)b[c * c + c + lane];
+            if (lane == 0) sqq += (double)b[c * c + i];
+        }
     }
+    if (lane == 0) s_qq = sqq;
     __syncthreads();
-    // One thread per attention row (dim rows).
-    float* sm = (float*)(s_red + total);  // [dim][c] scratch rows
-    for (int row = tid; row < dim; row += 256) {
-        const int hd = row / c, i = row - hd * c;
-        const double* S = s_red + hd * E;
-        float nq = (float)sqrt(S[c * c + i]);
-        nq = nq > 1e-12f ? nq : 1e-12f;
-        float mx = -INFINITY;
-        for (int j = 0; j < c; ++j) {
-            float nk = (float)sqrt(S[c * c + c + j]);
-            nk = nk > 1e-12f ? nk : 1e-12f;
-            const float a = (float)(S[i * c + j] / ((double)nq * (double)nk)) * temperature[hd];
-            sm[row * c + j] = a;
-            mx = fmaxf(mx, a);
-        }
-        double sum = 0.0;
-        for (int j = 0; j < c; ++j) {
-            const float e = cephes_exp(sm[row * c + j] - mx);
-            sm[row * c + j] = e;
-            sum += (double)e;
-        }
-        const float s32 = (float)sum;
-        for (int j = 0; j < c; ++j) {
-            const float a = sm[row * c + j] / s32;
-            sm[row * c + j] = a;
-            attn[row * c + j] = a;
-        }
+    float nq = (float)sqrt(s_qq);
+    nq = nq > 1e-12f ? nq : 1e-12f;
+    float a = -INFINITY;
+    if (lane < c) {
+        float nk = (float)sqrt(skk);
+        nk = nk > 1e-12f ? nk : 1e-12f;
+        a = (float)(sqk / ((double)nq * (double)nk)) * temperature[hd];
     }
+    s_e[lane] = a;
     __syncthreads();
-    // wfold[o][hd*c + j] = sum_i proj[o][hd*c + i] * attn[hd*c + i][j]  (f64 accumulate)
-    for (int e = tid; e < dim * dim; e += 256) {
-        const int o = e / dim, col = e - o * dim, hd = col / c, j = col - hd * c;
-        double s = 0.0;
-        for (int i = 0; i < c; ++i) s += (double)proj[o * dim + hd * c + i] * (double)sm[(hd * c + i) * c + j];
-        wfold[e] = (float)s;
-    }
+    float mx = -INFINITY;
+    for (int j = 0; j < c; ++j) mx = fmaxf(mx, s_e[j]);
+    __syncthreads();
+    if (lane < c) s_e[lane] = cephes_exp(a - mx);
+    __syncthreads();
+    double sum = 0.0;
+    for (int j = 0; j < c; ++j) sum += (double)s_e[j];
+    if (lane < c) attn[row * c + lane] = s_e[lane] / (float)sum;
+}
+
+// Folds the output projection into the attention: wfold[o][hd*c + j] =
+// sum_i proj[o][hd*c + i] * attn[hd*c + i][j] (f64 accumulate), stored straight into the packed
+// 1x1 conv layout [chunk][nblk][16][CK] of the storage type.
+template <typename T>
+__global__ void k_attention_fold(const float* proj, const float* attn, int dim, int heads, int nblk,
+                                 int CK, T* wpk) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= dim * dim) return;
+    const int c = dim / heads, o = e / dim, col = e - o * dim, hd = col / c, j = col - hd * c;
+    double s = 0.0;
+    for (int i = 0; i < c; ++i) s += (double)proj[o * dim + hd * c + i] * (double)attn[(hd * c + i) * c + j];
+    const int ch = col / CK, kk = col - ch * CK;
+    wpk[(((long long)ch * nblk + o / 16) * 16 + o % 16) * CK + kk] = from_f32<T>((float)s);
 }
 
 // ------------------------------------------------------------------------------- launchers
@@ -369,23 +389,32 @@ hipError_t launch_layer_norm(View src, View dst, int dtype, int C, int h, int w,
 }
 
 hipError_t launch_attention_gram(View qkv, int dtype, int dim, int heads, int h, int w,
-                                 double* partial, hipStream_t s) {
+                                 float* partial, hipStream_t s) {
     const int c = dim / heads;
-    if (heads * (c * c + 2 * c) > 256 * ATT_MAXE) return hipErrorInvalidValue;
+    if (heads <= 0 || dim % heads || c < 1 || c > 32) return hipErrorInvalidValue;
     const int nchunk = attention_gram_chunks(h, w);
     if (nchunk == 0) return hipSuccess;
-    const size_t lds = sizeof(float) * ATT_SUB * 2 * dim;
-    ZJAI_DISPATCH(dtype, k_attention_gram, <<<dim3(nchunk), 256, lds, s>>>(qkv, dim, heads, h, w, partial))
+    ZJAI_DISPATCH(dtype, k_attention_gram, <<<dim3(nchunk), 256, 0, s>>>(qkv, dim, heads, h * w, w, partial))
     return hipGetLastError();
 }
 
-hipError_t launch_attention_softmax_fold(const double* partial, int nchunk, int dim, int heads,
-                                         const float* temperature, const float* proj,
-                                         float* attn, float* wfold, hipStream_t s) {
-    const int c = dim / heads, total = heads * (c * c + 2 * c);
-    const size_t lds = sizeof(double) * total + sizeof(float) * dim * c;
-    k_attention_softmax_fold<<<1, 256, lds, s>>>(partial, nchunk, dim, heads, temperature, proj,
-                                                 attn, wfold);
+hipError_t launch_attention_softmax(const float* partial, int nchunk, int dim, int heads,
+                                    const float* temperature, float* attn, hipStream_t s) {
+    if (dim / heads > 64) return hipErrorInvalidValue;
+    k_attention_softmax<<<dim, 64, 0, s>>>(partial, nchunk, dim, heads, temperature, attn);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_fold(const float* proj, const float* attn, int dim, int heads, int dtype,
+                                 int nblk, void* wpk, hipStream_t s) {
+    const int CK = dtype == DT_F32 ? 16 : 32;
+    const dim3 g((dim * dim + 255) / 256);
+    switch (dtype) {
+        case DT_F32: k_attention_fold<float><<<g, 256, 0, s>>>(proj, attn, dim, heads, nblk, CK, (float*)wpk); break;
+        case DT_F16: k_attention_fold<_Float16><<<g, 256, 0, s>>>(proj, attn, dim, heads, nblk, CK, (_Float16*)wpk); break;
+        case DT_BF16: k_attention_fold<__bf16><<<g, 256, 0, s>>>(proj, attn, dim, heads, nblk, CK, (__bf16*)wpk); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -69,6 +69,13 @@ struct Tensor {
 };
 using TensorP = std::shared_ptr<Tensor>;
 
+// One profiled launch: kernel name, algorithmic FLOPs and HBM bytes, HIP events around it.
+struct ProfRec {
+    std::string name;
+    double flops = 0.0, bytes = 0.0;
+    hipEvent_t a = nullptr, b = nullptr;
+};
+
 struct Context {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -78,9 +85,29 @@ struct Context {
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     float last_ms = 0.0f;
     long long launches = 0;
+    // Per-launch profiling (zjai_profile_begin / zjai_profile_end).
+    bool profiling = false;
+    std::vector<ProfRec> prof;
+    std::vector<hipEvent_t> ev_pool;
+    size_t ev_used = 0;
 
     TensorP alloc(int c, int h, int w, int dtype);
     void check_stop();
+    hipEvent_t take_event();
+    ~Context();
+};
+
+// Brackets one kernel launch: counts it and, while profiling, records events around it.
+class LaunchScope {
+public:
+    LaunchScope(Context& c, const std::string& name, double flops, double bytes);
+    ~LaunchScope();
+    LaunchScope(const LaunchScope&) = delete;
+    LaunchScope& operator=(const LaunchScope&) = delete;
+
+private:
+    Context& c_;
+    long idx_ = -1;
 };
 
 // View of the top-left h x w corner (`BTensor::crop_par`, src/nn/fast/tensor.rs:349-367).
@@ -138,8 +165,14 @@ struct PlaneOut {
 TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilogue& e,
                      const TensorP& dst = nullptr, const PlaneOut* plane = nullptr);
 
-// Device pack of an f32 [O][I] 1x1 weight into a layer's packed layout (attention fold).
-void pack_1x1_device(Context& ctx, const Layer& L, const float* w_dev);
+std::string conv_kernel_name(int kind, int dtype, TileCfg c);
+
+// Channel attention of qkv (3*dim channels, `heads` heads, device temperature) folded with the
+// projection layer `proj` (a dense 1x1 dim -> dim layer holding its f32 weight): afterwards
+// proj's packed weight is proj . blockdiag(attn), so proj applied to the v channels of qkv
+// yields project_out(channel_attention(qkv)).
+void attention_fold(Context& ctx, const TensorP& qkv, int heads, const float* temperature,
+                    const Layer& proj);
 
 // ---------------------------------------------------------------------------- synthesis nets
 enum Op : int { OP_SOP = 0, OP_BOP = 1, OP_HOP = 2 };

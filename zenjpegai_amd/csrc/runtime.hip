@@ -90,6 +90,37 @@ void Context::check_stop() {
     if (stop) throw Error(ZJAI_E_CANCELLED, "cancelled");
 }
 
+hipEvent_t Context::take_event() {
+    if (ev_used == ev_pool.size()) {
+        hipEvent_t e;
+        ZJAI_HIP(hipEventCreate(&e));
+        ev_pool.push_back(e);
+    }
+    return ev_pool[ev_used++];
+}
+
+Context::~Context() {
+    for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
+}
+
+LaunchScope::LaunchScope(Context& c, const std::string& name, double flops, double bytes) : c_(c) {
+    ++c_.launches;
+    if (!c_.profiling) return;
+    ProfRec r;
+    r.name = name;
+    r.flops = flops;
+    r.bytes = bytes;
+    r.a = c_.take_event();
+    r.b = c_.take_event();
+    ZJAI_HIP(hipEventRecord(r.a, c_.stream));
+    idx_ = (long)c_.prof.size();
+    c_.prof.push_back(r);
+}
+
+LaunchScope::~LaunchScope() {
+    if (idx_ >= 0) (void)hipEventRecord(c_.prof[idx_].b, c_.stream);
+}
+
 TensorP crop_view(const TensorP& t, int h, int w) {
     if (h > t->h || w > t->w || h < 0 || w < 0)
         throw Error(ZJAI_E_INVALID_ARGUMENT, "crop larger than tensor");
@@ -324,6 +355,15 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
 }
 
 // ------------------------------------------------------------------------------ conv launch
+// The kernel's name as profilers print it: conv_igemm<T, KH, KW, S, TR, WC, WP, CF, PF>.
+std::string conv_kernel_name(int kind, int dtype, TileCfg c) {
+    static const char* geo[] = {"1, 1, 1, false", "2, 2, 1, false", "3, 3, 1, false", "3, 3, 2, false",
+                                "3, 3, 1, true"};
+    static const char* ty[] = {"float", "_Float16", "__bf16"};
+    char buf[128];
+    snprintf(buf, sizeof buf, "conv_igemm<%s, %s, %d, %d, %d, %d>", ty[dtype], geo[kind], c.wc, c.wp, c.cf, c.pf);
+    return buf;
+}
 static View view_of(const Tensor* t) { return t ? t->v : View{nullptr, 0, 0, 0}; }
 
 TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilogue& e,
@@ -355,8 +395,9 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
     if (L.depthwise) {
         if (e.act || e.res || ps != 1 || e.relu6_in || plane)
             throw Error(ZJAI_E_UNSUPPORTED, "depthwise: fused epilogue");
+        const double es = dtype_size(L.dtype);
+        LaunchScope sc(ctx, "k_depthwise3x3", 2.0 * 9 * L.cin * x->h * x->w, 2.0 * es * L.cin * x->h * x->w);
         ZJAI_HIP(launch_depthwise3x3(x->v, y->v, L.dtype, L.cin, x->h, x->w, L.dw_w, L.bias, 0, ctx.stream));
-        ++ctx.launches;
         return y;
     }
     ConvParams p{};
@@ -408,33 +449,51 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
             p.tap_dx[ph][t] = L.tap_dx[ph][t];
         }
     }
+    // Algorithmic work: every tap of every output (padding taps included); compulsory bytes:
+    // input, output, weights and residual reads once each.
+    double macs;
+    if (L.transposed) {
+        double taps = 0.0;
+        for (int ph = 0; ph < 4; ++ph)
+            taps += (double)((OH - (ph >> 1) + 1) / 2) * ((OW - (ph & 1) + 1) / 2) * L.ntaps[ph];
+        macs = taps * L.cout * L.cin;
+    } else {
+        macs = (double)OH * OW * L.cout * (L.cin / L.groups) * L.kh * L.kw;
+    }
+    const double es = dtype_size(L.dtype);
+    double bytes = es * ((double)L.cin * x->h * x->w + (double)L.cout * OH * OW) + (double)L.wpk_bytes;
+    if (e.r1) bytes += es * (double)L.cout * OH * OW;
+    if (e.r2) bytes += es * (double)L.cout * OH * OW;
+    LaunchScope sc(ctx, conv_kernel_name(L.kind, L.dtype, L.cfg), 2.0 * macs, bytes);
     ZJAI_HIP(launch_conv(L.kind, L.dtype, L.cfg, p, ctx.stream));
-    ++ctx.launches;
     return y;
 }
 
-// ----------------------------------------------------------------------- device 1x1 packing
-template <typename T>
-__global__ void k_pack_1x1(const float* w, int O, int I, int nblk, int CK, T* dst) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= O * I) return;
-    const int o = i / I, ic = i - o * I;
-    const int ch = ic / CK, kk = ic - ch * CK;
-    dst[(((long long)ch * nblk + o / 16) * 16 + o % 16) * CK + kk] = from_f32<T>(w[i]);
-}
-
-void pack_1x1_device(Context& ctx, const Layer& L, const float* w_dev) {
-    if (L.kind != CK_1x1 || L.groups != 1 || L.depthwise || L.transposed)
-        throw Error(ZJAI_E_INVALID_ARGUMENT, "pack_1x1: not a dense 1x1 layer");
-    const int n = L.cout * L.cin, CK = 64 / dtype_size(L.dtype);
-    const dim3 g((n + 255) / 256);
-    switch (L.dtype) {
-        case DT_F32: k_pack_1x1<float><<<g, 256, 0, ctx.stream>>>(w_dev, L.cout, L.cin, L.nblk_g, CK, (float*)L.wpk); break;
-        case DT_F16: k_pack_1x1<_Float16><<<g, 256, 0, ctx.stream>>>(w_dev, L.cout, L.cin, L.nblk_g, CK, (_Float16*)L.wpk); break;
-        default: k_pack_1x1<__bf16><<<g, 256, 0, ctx.stream>>>(w_dev, L.cout, L.cin, L.nblk_g, CK, (__bf16*)L.wpk); break;
+// -------------------------------------------------------------------- attention + projection
+void attention_fold(Context& ctx, const TensorP& qkv, int heads, const float* temperature,
+                    const Layer& proj) {
+    const int dim = qkv->c / 3, c = dim / heads;
+    if (proj.kind != CK_1x1 || proj.groups != 1 || proj.depthwise || proj.transposed || !proj.w_f32 ||
+        proj.cin != dim || proj.cout != dim || proj.dtype != qkv->dtype)
+        throw Error(ZJAI_E_INVALID_ARGUMENT, "attention: projection is not a dense dim x dim 1x1 layer");
+    const int n = qkv->h * qkv->w, nchunk = attention_gram_chunks(qkv->h, qkv->w);
+    const int total = heads * (c * c + 2 * c);
+    const double es = dtype_size(qkv->dtype);
+    float* partial = (float*)ctx.pool.alloc(sizeof(float) * ((size_t)std::max(nchunk, 1) * total + (size_t)dim * c));
+    std::shared_ptr<void> keep(partial, [&ctx](void* q) { ctx.pool.release(q); });
+    float* attn = partial + (size_t)std::max(nchunk, 1) * total;
+    {
+        LaunchScope sc(ctx, "k_attention_gram", 2.0 * total * n, es * 2 * dim * n + 4.0 * nchunk * total);
+        ZJAI_HIP(launch_attention_gram(qkv->v, qkv->dtype, dim, heads, qkv->h, qkv->w, partial, ctx.stream));
     }
-    ZJAI_HIP(hipGetLastError());
-    ++ctx.launches;
+    {
+        LaunchScope sc(ctx, "k_attention_softmax", 0.0, 4.0 * nchunk * total);
+        ZJAI_HIP(launch_attention_softmax(partial, nchunk, dim, heads, temperature, attn, ctx.stream));
+    }
+    {
+        LaunchScope sc(ctx, "k_attention_fold", 2.0 * dim * dim * c, 4.0 * dim * dim + es * dim * dim);
+        ZJAI_HIP(launch_attention_fold(proj.w_f32, attn, dim, heads, proj.dtype, proj.nblk_g, proj.wpk, ctx.stream));
+    }
 }
 
 }  // namespace zjai

@@ -105,6 +105,17 @@ class Engine:
         check(lib().zjai_get_stats(self._h, ctypes.byref(s)), self._h)
         return {k: getattr(s, k) for k, _ in s._fields_}
 
+    def profile_begin(self):
+        """Start bracketing every launch with HIP events (see ``zjai_profile_begin``)."""
+        check(lib().zjai_profile_begin(self._h), self._h)
+
+    def profile_end(self, cap: int = 1 << 16) -> list:
+        """Stop profiling; returns ``[(kernel name, flops, bytes, ms)]`` per launch."""
+        recs = (_lib.ZjaiProfRecord * cap)()
+        n = ctypes.c_int32()
+        check(lib().zjai_profile_end(self._h, recs, cap, ctypes.byref(n)), self._h)
+        return [(r.name.decode(), r.flops, r.bytes, r.ms) for r in recs[:min(n.value, cap)]]
+
     def release_buffers(self):
         check(lib().zjai_release_buffers(self._h), self._h)
 
