@@ -57,14 +57,14 @@ TensorP planar_upload(Context& c, const float* data, int ch, int h, int w, int d
     need(ch > 0 && h > 0 && w > 0, "bad shape");
     need(ch % 4 == 0, "channel count must be a multiple of 4");
     need(dtype >= DT_F32 && dtype <= DT_BF16, "precision");
-    TensorP t = c.alloc(ch, h, w, dtype);
+    TensorP t = c.alloc(1, ch, h, w, dtype);
     const size_t n = (size_t)ch * h * w;
     float* stage = (float*)c.pool.alloc(n * 4);
     std::shared_ptr<void> keep(stage, [&c](void* q) { c.pool.release(q); });
     ZJAI_HIP(hipMemcpyAsync(stage, data, n * 4, hipMemcpyHostToDevice, c.stream));
     {
         LaunchScope sc(c, "k_planar_to_nhwc", 0.0, (4.0 + dtype_size(dtype)) * n);
-        ZJAI_HIP(launch_planar_to_nhwc(stage, ch, h, w, 0, 0, h, w, t->v, dtype, c.stream));
+        ZJAI_HIP(launch_planar_to_nhwc(stage, ch, h, w, Windows{}, 1, h, w, t->v, dtype, c.stream));
     }
     ZJAI_HIP(hipStreamSynchronize(c.stream));
     return t;
@@ -193,8 +193,8 @@ extern "C" int32_t zjai_tensor_create(zjai_ctx* ctx, int32_t c, int32_t h, int32
     return guard(ctx, [&] {
         need(precision >= DT_F32 && precision <= DT_BF16, "precision");
         need(c > 0 && h > 0 && w > 0, "bad shape");
-        TensorP t = ctx->c.alloc(c, h, w, precision);
-        ZJAI_HIP(hipMemsetAsync(t->v.p, 0, (size_t)h * t->v.row * dtype_size(precision), ctx->c.stream));
+        TensorP t = ctx->c.alloc(1, c, h, w, precision);
+        ZJAI_HIP(hipMemsetAsync(t->v.p, 0, (size_t)t->v.bstride * dtype_size(precision), ctx->c.stream));
         *out = new zjai_tensor{t};
     });
 }
@@ -209,14 +209,14 @@ extern "C" int32_t zjai_tensor_to_planar(zjai_ctx* ctx, const zjai_tensor* t, fl
     if (!ctx || !t || !data) return ZJAI_E_INVALID_ARGUMENT;
     return guard(ctx, [&] {
         const Tensor& x = *t->t;
-        const size_t n = (size_t)x.c * x.h * x.w;
+        const size_t n = (size_t)x.n * x.c * x.h * x.w;
         need(len >= n, "output buffer too small");
         if (n == 0) return;
         float* stage = (float*)ctx->c.pool.alloc(n * 4);
         std::shared_ptr<void> keep(stage, [ctx](void* q) { ctx->c.pool.release(q); });
         {
             LaunchScope sc(ctx->c, "k_nhwc_to_planar", 0.0, (4.0 + dtype_size(x.dtype)) * n);
-            ZJAI_HIP(launch_nhwc_to_planar(x.v, x.dtype, x.c, x.h, x.w, stage, ctx->c.stream));
+            ZJAI_HIP(launch_nhwc_to_planar(x.v, x.dtype, x.n, x.c, x.h, x.w, stage, ctx->c.stream));
         }
         ZJAI_HIP(hipMemcpyAsync(data, stage, n * 4, hipMemcpyDeviceToHost, ctx->c.stream));
         ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
@@ -247,16 +247,16 @@ extern "C" int32_t zjai_tensor_cat(zjai_ctx* ctx, const zjai_tensor* const* part
         const Tensor& f = *parts[0]->t;
         for (int i = 0; i < n; ++i) {
             const Tensor& p = *parts[i]->t;
-            need(p.h == f.h && p.w == f.w && p.dtype == f.dtype, "cat: shapes differ");
+            need(p.n == f.n && p.h == f.h && p.w == f.w && p.dtype == f.dtype, "cat: shapes differ");
             need(p.c % 4 == 0, "cat: channel counts must be multiples of 4");
             c += p.c;
         }
-        TensorP y = ctx->c.alloc(c, f.h, f.w, f.dtype);
+        TensorP y = ctx->c.alloc(f.n, c, f.h, f.w, f.dtype);
         int c0 = 0;
         for (int i = 0; i < n; ++i) {
             const Tensor& p = *parts[i]->t;
-            LaunchScope sc(ctx->c, "k_copy", 0.0, 2.0 * dtype_size(p.dtype) * p.c * p.h * p.w);
-            ZJAI_HIP(launch_copy(p.v, channel_view(y, c0, p.c)->v, p.dtype, p.c, p.h, p.w, ctx->c.stream));
+            LaunchScope sc(ctx->c, "k_copy", 0.0, 2.0 * dtype_size(p.dtype) * p.n * p.c * p.h * p.w);
+            ZJAI_HIP(launch_copy(p.v, channel_view(y, c0, p.c)->v, p.dtype, p.n, p.c, p.h, p.w, ctx->c.stream));
             c0 += p.c;
         }
         *out = new zjai_tensor{y};
@@ -329,11 +329,11 @@ static int32_t eltwise(zjai_ctx* ctx, int op, zjai_tensor* x, const zjai_tensor*
         if (op >= EL_ADD) {
             need(s != nullptr, "second operand missing");
             const Tensor& b = *s->t;
-            need(a.c == b.c && a.h == b.h && a.w == b.w && a.dtype == b.dtype, "shapes differ");
+            need(a.n == b.n && a.c == b.c && a.h == b.h && a.w == b.w && a.dtype == b.dtype, "shapes differ");
         }
         need(a.c % 4 == 0, "channel count must be a multiple of 4");
         LaunchScope sc(ctx->c, "k_eltwise", 0.0, (op >= EL_ADD ? 3.0 : 2.0) * dtype_size(a.dtype) * a.c * a.h * a.w);
-        ZJAI_HIP(launch_eltwise(op, a.v, s ? s->t->v : a.v, a.dtype, a.c, a.h, a.w, ctx->c.stream));
+        ZJAI_HIP(launch_eltwise(op, a.v, s ? s->t->v : a.v, a.dtype, a.n, a.c, a.h, a.w, ctx->c.stream));
     });
 }
 
@@ -353,9 +353,9 @@ extern "C" int32_t zjai_pixel_shuffle(zjai_ctx* ctx, const zjai_tensor* x, int32
         need(r > 0 && a.c % (r * r) == 0, "pixel_shuffle: channels not divisible by r^2");
         const int co = a.c / (r * r);
         need(co % 4 == 0, "pixel_shuffle: output channels must be a multiple of 4");
-        TensorP y = ctx->c.alloc(co, a.h * r, a.w * r, a.dtype);
+        TensorP y = ctx->c.alloc(a.n, co, a.h * r, a.w * r, a.dtype);
         LaunchScope sc(ctx->c, "k_pixel_shuffle", 0.0, 2.0 * dtype_size(a.dtype) * a.c * a.h * a.w);
-        ZJAI_HIP(launch_pixel_shuffle(a.v, y->v, a.dtype, co, a.h, a.w, r, ctx->c.stream));
+        ZJAI_HIP(launch_pixel_shuffle(a.v, y->v, a.dtype, a.n, co, a.h, a.w, r, ctx->c.stream));
         *out = new zjai_tensor{y};
     });
 }
@@ -370,10 +370,10 @@ extern "C" int32_t zjai_layer_norm_channels(zjai_ctx* ctx, const zjai_tensor* x,
         std::shared_ptr<void> keep(d, [ctx](void* q) { ctx->c.pool.release(q); });
         ZJAI_HIP(hipMemcpyAsync(d, weight, sizeof(float) * a.c, hipMemcpyHostToDevice, ctx->c.stream));
         ZJAI_HIP(hipMemcpyAsync(d + a.c, bias, sizeof(float) * a.c, hipMemcpyHostToDevice, ctx->c.stream));
-        TensorP y = ctx->c.alloc(a.c, a.h, a.w, a.dtype);
+        TensorP y = ctx->c.alloc(a.n, a.c, a.h, a.w, a.dtype);
         {
             LaunchScope sc(ctx->c, "k_layer_norm", 0.0, 2.0 * dtype_size(a.dtype) * a.c * a.h * a.w);
-            ZJAI_HIP(launch_layer_norm(a.v, y->v, a.dtype, a.c, a.h, a.w, d, d + a.c, ctx->c.stream));
+            ZJAI_HIP(launch_layer_norm(a.v, y->v, a.dtype, a.n, a.c, a.h, a.w, d, d + a.c, ctx->c.stream));
         }
         ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
         *out = new zjai_tensor{y};
@@ -397,8 +397,10 @@ extern "C" int32_t zjai_channel_attention(zjai_ctx* ctx, const zjai_tensor* qkv,
         float* temp = (float*)ctx->c.pool.alloc(sizeof(float) * heads);
         std::shared_ptr<void> kt(temp, [ctx](void* q) { ctx->c.pool.release(q); });
         ZJAI_HIP(hipMemcpyAsync(temp, temperature, sizeof(float) * heads, hipMemcpyHostToDevice, ctx->c.stream));
-        attention_fold(ctx->c, qkv->t, heads, temp, *L);
-        TensorP y = conv_forward(ctx->c, *L, channel_view(qkv->t, 2 * dim, dim), Epilogue{});
+        Epilogue e;
+        std::shared_ptr<void> wfold = attention_fold(ctx->c, qkv->t, heads, temp, *L, &e.w_bstride);
+        e.w_batch = wfold.get();
+        TensorP y = conv_forward(ctx->c, *L, channel_view(qkv->t, 2 * dim, dim), e);
         ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
         *out = new zjai_tensor{y};
     });
@@ -454,8 +456,8 @@ static void run_to_host(zjai_ctx* ctx, const zjai_net* net, const TensorP& a, co
     po.plane = dev;
     po.row = ow;
     po.cstride = (long long)oh * ow;
-    po.win_h = oh;
-    po.win_w = ow;
+    po.win_h[0] = oh;
+    po.win_w[0] = ow;
     if (primary) primary_forward(ctx->c, *net->n, a, h, w, po);
     else secondary_forward(ctx->c, *net->n, a, b, h, w, po);
     ZJAI_HIP(hipMemcpyAsync(out, dev, n * 4, hipMemcpyDeviceToHost, ctx->c.stream));
@@ -608,6 +610,7 @@ struct zjai_picture {
     NetP net_y, net_uv;
     int lh = 0, lw = 0, height = 0, width = 0, sv = 1, sh = 1, out_h = 0, out_w = 0, bit_depth = 0;
     std::vector<zjai_tile> tiles;
+    std::vector<std::vector<int>> batches;  // tile indices of equal image size, at most MAXB each
     float* y_hat = nullptr;   // device planar [160][lh][lw]
     float* uv_hat = nullptr;  // device planar [96][lh][lw]
     void* out_y = nullptr;    // device planes
@@ -656,6 +659,12 @@ extern "C" int32_t zjai_picture_create(zjai_ctx* ctx, const zjai_net* net_y, con
                  "synthesis tile smaller than its core");
             need(t.core_x >= 0 && t.core_y >= 0, "tile core position");
         }
+        std::map<std::pair<int, int>, std::vector<int>> by_size;
+        for (int i = 0; i < n_tiles; ++i) by_size[{p->tiles[i].image_h, p->tiles[i].image_w}].push_back(i);
+        for (auto& kv : by_size)
+            for (size_t i = 0; i < kv.second.size(); i += MAXB)
+                p->batches.emplace_back(kv.second.begin() + i,
+                                        kv.second.begin() + std::min(kv.second.size(), i + MAXB));
         ZJAI_HIP(hipMalloc(&p->y_hat, sizeof(float) * 160 * (size_t)lh * lw));
         if (p->net_uv) ZJAI_HIP(hipMalloc(&p->uv_hat, sizeof(float) * 96 * (size_t)lh * lw));
         ZJAI_HIP(hipMalloc(&p->out_y, p->sample_bytes() * (size_t)out_h * out_w));
@@ -694,33 +703,43 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
         Context& c = ctx->c;
         const int dt = pic->net_y->dtype;
         ZJAI_HIP(hipEventRecord(c.ev0, c.stream));
-        for (const zjai_tile& t : pic->tiles) {
+        // Tiles of one image size share every layer shape: run them as one batch of up to MAXB
+        // (each launch then covers all of them).
+        for (const std::vector<int>& group : pic->batches) {
             c.check_stop();
-            TensorP by = c.alloc(160, t.latent_h, t.latent_w, dt);
-            {
-                LaunchScope sc(c, "k_planar_to_nhwc", 0.0, (4.0 + dtype_size(dt)) * 160 * t.latent_h * t.latent_w);
-                ZJAI_HIP(launch_planar_to_nhwc(pic->y_hat, 160, pic->lh, pic->lw, t.latent_x, t.latent_y,
-                                               t.latent_h, t.latent_w, by->v, dt, c.stream));
-            }
-            // synthesize_luma_into (src/decoder/reconstruct.rs:379-411): core rows/cols that
-            // fall inside the displayed picture.
+            const zjai_tile& t0 = pic->tiles[group[0]];
+            const int N = (int)group.size();
+            Windows win{};
             PlaneOut py;
             py.plane = pic->out_y;
             py.row = pic->out_w;
-            py.win_y0 = t.core_off_y;
-            py.win_x0 = t.core_off_x;
-            py.win_h = std::min(t.core_h, std::max(pic->out_h - t.core_y, 0));
-            py.win_w = std::min(t.core_w, std::max(pic->out_w - t.core_x, 0));
-            py.dst_y0 = t.core_y;
-            py.dst_x0 = t.core_x;
             py.bit_depth = pic->bit_depth;
-            primary_forward(c, *pic->net_y, by, t.image_h, t.image_w, py);
+            for (int b = 0; b < N; ++b) {
+                const zjai_tile& t = pic->tiles[group[b]];
+                win.x0[b] = t.latent_x;
+                win.y0[b] = t.latent_y;
+                // synthesize_luma_into (src/decoder/reconstruct.rs:379-411): core rows/cols that
+                // fall inside the displayed picture.
+                py.win_y0[b] = t.core_off_y;
+                py.win_x0[b] = t.core_off_x;
+                py.win_h[b] = std::min(t.core_h, std::max(pic->out_h - t.core_y, 0));
+                py.win_w[b] = std::min(t.core_w, std::max(pic->out_w - t.core_x, 0));
+                py.dst_y0[b] = t.core_y;
+                py.dst_x0[b] = t.core_x;
+            }
+            TensorP by = c.alloc(N, 160, t0.latent_h, t0.latent_w, dt);
+            {
+                LaunchScope sc(c, "k_planar_to_nhwc", 0.0, (4.0 + dtype_size(dt)) * N * 160 * t0.latent_h * t0.latent_w);
+                ZJAI_HIP(launch_planar_to_nhwc(pic->y_hat, 160, pic->lh, pic->lw, win, N, t0.latent_h, t0.latent_w,
+                                               by->v, dt, c.stream));
+            }
+            primary_forward(c, *pic->net_y, by, t0.image_h, t0.image_w, py);
             if (pic->net_uv) {
-                TensorP buv = c.alloc(96, t.latent_h, t.latent_w, dt);
+                TensorP buv = c.alloc(N, 96, t0.latent_h, t0.latent_w, dt);
                 {
-                    LaunchScope sc(c, "k_planar_to_nhwc", 0.0, (4.0 + dtype_size(dt)) * 96 * t.latent_h * t.latent_w);
-                    ZJAI_HIP(launch_planar_to_nhwc(pic->uv_hat, 96, pic->lh, pic->lw, t.latent_x, t.latent_y,
-                                                   t.latent_h, t.latent_w, buv->v, dt, c.stream));
+                    LaunchScope sc(c, "k_planar_to_nhwc", 0.0, (4.0 + dtype_size(dt)) * N * 96 * t0.latent_h * t0.latent_w);
+                    ZJAI_HIP(launch_planar_to_nhwc(pic->uv_hat, 96, pic->lh, pic->lw, win, N, t0.latent_h,
+                                                   t0.latent_w, buv->v, dt, c.stream));
                 }
                 // synthesize_chroma_into (src/decoder/reconstruct.rs:416-464)
                 PlaneOut pu = py;
@@ -729,7 +748,7 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
                 pu.cstride = (long long)pic->ch() * pic->cw();
                 pu.sv = pic->sv;
                 pu.sh = pic->sh;
-                secondary_forward(c, *pic->net_uv, by, buv, t.image_h, t.image_w, pu);
+                secondary_forward(c, *pic->net_uv, by, buv, t0.image_h, t0.image_w, pu);
             }
         }
         ZJAI_HIP(hipEventRecord(c.ev1, c.stream));

@@ -25,13 +25,16 @@ struct ConvParams {
     // Input view and its valid extent (reads outside [0,H) x [0,W) are zero padding).
     View x;
     int H, W;
+    int N;  // batch items (tiles)
     // Output extent in conv-output coordinates (before pixel shuffle).
     int OH, OW;
     View y;  // OUT_NHWC destination (after pixel shuffle)
     // Packed weights: [phase][group][chunk][nblk][tap][16][CK] in the storage type; bias f32.
+    // w_bstride > 0: one packed weight per batch item (the folded attention projection).
     const void* w;
+    long long w_bstride;
     const float* bias;
-    int cin_g, cout_g, groups, nchunks, nblk_g;
+    int cin_g, cout_g, groups, nchunks, nblk_g, ntiles;
     long long phase_stride;  // elements between phases (transposed conv)
     int pad_t, pad_l;
     int relu6_in;  // clamp(x, 0, 6) on load (ResAU's relu6)
@@ -40,14 +43,15 @@ struct ConvParams {
     View r1, r2;
     int ps;  // pixel shuffle factor (1 = none)
     int out_mode;
-    // OUT_PLANE: planar destination. Channel c of the (shuffled) output goes to
-    // plane + c * pl_cstride; the kept window [win_y0, win_y0 + win_h) x [win_x0, ...) of the
-    // output lands at (dst_y0, dst_x0), keeping rows/cols that are multiples of sv / sh.
+    // OUT_PLANE: planar destination. Channel c of the (shuffled) output of batch item b goes to
+    // plane + c * pl_cstride; the kept window [win_y0[b], +win_h[b]) x [win_x0[b], +win_w[b]) of
+    // the output lands at (dst_y0[b], dst_x0[b]), keeping rows/cols that are multiples of sv / sh.
     void* plane;
     long long pl_row, pl_cstride;
-    int win_y0, win_x0, win_h, win_w, dst_y0, dst_x0, sv, sh;
+    int sv, sh;
     int denorm;     // x * 128 + 127.5 clamped to [0, 255]
     int bit_depth;  // 0: store f32; else quantise to u16 at this depth
+    int win_y0[MAXB], win_x0[MAXB], win_h[MAXB], win_w[MAXB], dst_y0[MAXB], dst_x0[MAXB];
     // Transposed conv (stride 2): tap tables per output phase (py * 2 + px).
     int ntaps[4];
     int tap_dy[4][4], tap_dx[4][4];

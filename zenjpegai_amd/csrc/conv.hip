@@ -90,13 +90,14 @@ __device__ __forceinline__ float apply_act(int act, float v) {
 }
 
 template <typename T>
-__device__ __forceinline__ void epilogue_store(const ConvParams& p, int oy, int ox, int oc0,
+__device__ __forceinline__ void epilogue_store(const ConvParams& p, int b, int oy, int ox, int oc0,
                                                int nvalid, f32x4 v) {
     // Activation, then the residual operation, each as separate IEEE operations.
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = apply_act(p.act, v[i]);
     if (p.res != RES_NONE) {
-        const long long o1 = (long long)oy * p.r1.row + (long long)ox * p.r1.cs + p.r1.c_off + oc0;
+        const long long o1 = (long long)b * p.r1.bstride + (long long)oy * p.r1.row +
+                             (long long)ox * p.r1.cs + p.r1.c_off + oc0;
         f32x4 r1;
         if (nvalid == 4) {
             r1 = load4<T>((const T*)p.r1.p + o1);
@@ -113,7 +114,8 @@ __device__ __forceinline__ void epilogue_store(const ConvParams& p, int oy, int 
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[i] = r1[i] * v[i];
         } else if (p.res == RES_CAB) {
-            const long long o2 = (long long)oy * p.r2.row + (long long)ox * p.r2.cs + p.r2.c_off + oc0;
+            const long long o2 = (long long)b * p.r2.bstride + (long long)oy * p.r2.row +
+                                 (long long)ox * p.r2.cs + p.r2.c_off + oc0;
             f32x4 r2;
             if (nvalid == 4) {
                 r2 = load4<T>((const T*)p.r2.p + o2);
@@ -129,7 +131,7 @@ __device__ __forceinline__ void epilogue_store(const ConvParams& p, int oy, int 
         }
     }
     if (p.out_mode == OUT_NHWC) {
-        T* y = (T*)p.y.p;
+        T* y = (T*)p.y.p + (long long)b * p.y.bstride;
         if (p.ps == 1) {
             const long long o = (long long)oy * p.y.row + (long long)ox * p.y.cs + p.y.c_off + oc0;
             if (nvalid == 4) {
@@ -153,9 +155,9 @@ __device__ __forceinline__ void epilogue_store(const ConvParams& p, int oy, int 
     for (int i = 0; i < nvalid; ++i) {
         const int oc = oc0 + i, c = oc / rr, sub = oc - c * rr;
         const int Y = oy * r + sub / r, X = ox * r + sub % r;
-        const int wy = Y - p.win_y0, wx = X - p.win_x0;
-        if (wy < 0 || wy >= p.win_h || wx < 0 || wx >= p.win_w) continue;
-        const int py = p.dst_y0 + wy, px = p.dst_x0 + wx;
+        const int wy = Y - p.win_y0[b], wx = X - p.win_x0[b];
+        if (wy < 0 || wy >= p.win_h[b] || wx < 0 || wx >= p.win_w[b]) continue;
+        const int py = p.dst_y0[b] + wy, px = p.dst_x0[b] + wx;
         if (py % p.sv || px % p.sh) continue;
         float s = v[i];
         if (p.denorm) {
@@ -202,8 +204,9 @@ conv_igemm(const ConvParams p) {
     const int wc = wave % WC, wp = wave / WC;
     const int col = lane & 15, grp = lane >> 4;
 
-    const int nt = TR ? (int)(blockIdx.z >> 2) : (int)blockIdx.z;
+    const int zz = TR ? (int)(blockIdx.z >> 2) : (int)blockIdx.z;
     const int phase = TR ? (int)(blockIdx.z & 3) : 0;
+    const int bi = zz / p.ntiles, nt = zz - bi * p.ntiles;
     const int gb = nt * NB;
     const int g = gb / p.nblk_g, nb0 = gb - g * p.nblk_g;
     const int ox0 = blockIdx.x * 16, oy0 = blockIdx.y * TY;
@@ -236,8 +239,8 @@ conv_igemm(const ConvParams p) {
 
     const int iy0 = TR ? oy0 - 1 : oy0 * S - p.pad_t;
     const int ix0 = TR ? ox0 - 1 : ox0 * S - p.pad_l;
-    const T* xg = (const T*)p.x.p;
-    const T* wg = (const T*)p.w + phase * p.phase_stride;
+    const T* xg = (const T*)p.x.p + (long long)bi * p.x.bstride;
+    const T* wg = (const T*)p.w + phase * p.phase_stride + (long long)bi * p.w_bstride;
     const long long xbase = (long long)p.x.c_off + (long long)g * p.cin_g;
 
     for (int chunk = 0; chunk < p.nchunks; ++chunk) {
@@ -293,7 +296,7 @@ conv_igemm(const ConvParams p) {
                 ox = ox0 + col;
             }
             if (oy >= p.OH || ox >= p.OW) continue;
-            epilogue_store<T>(p, oy, ox, g * p.cout_g + ocl, nvalid, acc[cf][pf]);
+            epilogue_store<T>(p, bi, oy, ox, g * p.cout_g + ocl, nvalid, acc[cf][pf]);
         }
     }
 }
@@ -306,8 +309,8 @@ static hipError_t go(const ConvParams& p, hipStream_t s) {
     constexpr int TY = WP * PF;
     const int gh = TR ? (p.OH + 1) / 2 : p.OH;
     const int gw = TR ? (p.OW + 1) / 2 : p.OW;
-    const int ntiles = p.groups * p.nblk_g / (WC * CF);
-    dim3 grid((gw + 15) / 16, (gh + TY - 1) / TY, ntiles * (TR ? 4 : 1));
+    if (p.ntiles != p.groups * p.nblk_g / (WC * CF) || p.N < 1 || p.N > MAXB) return hipErrorInvalidValue;
+    dim3 grid((gw + 15) / 16, (gh + TY - 1) / TY, p.N * p.ntiles * (TR ? 4 : 1));
     hipLaunchKernelGGL((conv_igemm<T, KH, KW, S, TR, WC, WP, CF, PF>), grid, dim3(WC * WP * 64), 0, s, p);
     return hipGetLastError();
 }

@@ -15,13 +15,27 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
-// An NHWC activation view: element (y, x, c) lives at p[y * row + x * cs + c_off + c].
+// A batched NHWC activation view: element (b, y, x, c) lives at
+// p[b * bstride + y * row + x * cs + c_off + c]. Batch items are synthesis tiles of one shape.
 struct View {
     void* p;
     long long row;
+    long long bstride;
     int cs;
     int c_off;
 };
+
+template <typename T>
+__device__ __forceinline__ const T* at(const View& v, int b, int y, int x, int c) {
+    return (const T*)v.p + (long long)b * v.bstride + (long long)y * v.row + (long long)x * v.cs + v.c_off + c;
+}
+template <typename T>
+__device__ __forceinline__ T* at_mut(const View& v, int b, int y, int x, int c) {
+    return (T*)v.p + (long long)b * v.bstride + (long long)y * v.row + (long long)x * v.cs + v.c_off + c;
+}
+
+// Largest number of tiles one launch batches.
+constexpr int MAXB = 8;
 
 template <typename T> struct Elem;
 template <> struct Elem<float> { static constexpr int dt = DT_F32; };

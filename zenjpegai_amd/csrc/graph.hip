@@ -247,9 +247,9 @@ struct Fwd {
         return conv(pfx + ".upscale", m, e);
     }
     TensorP layer_norm(const std::string& pfx, const TensorP& x) {
-        TensorP y = ctx.alloc(x->c, x->h, x->w, x->dtype);
-        LaunchScope sc(ctx, "k_layer_norm", 0.0, 2.0 * dtype_size(x->dtype) * x->c * x->h * x->w);
-        ZJAI_HIP(launch_layer_norm(x->v, y->v, x->dtype, x->c, x->h, x->w, net.vec.at(pfx + ".weight"),
+        TensorP y = ctx.alloc(x->n, x->c, x->h, x->w, x->dtype);
+        LaunchScope sc(ctx, "k_layer_norm", 0.0, 2.0 * dtype_size(x->dtype) * x->n * x->c * x->h * x->w);
+        ZJAI_HIP(launch_layer_norm(x->v, y->v, x->dtype, x->n, x->c, x->h, x->w, net.vec.at(pfx + ".weight"),
                                    net.vec.at(pfx + ".bias"), ctx.stream));
         return y;
     }
@@ -260,9 +260,11 @@ struct Fwd {
         t = conv(p + ".prep_data.conv1", t);
         t = conv(p + ".prep_data.conv2", t);  // depthwise 3x3
         // channel_attention + project_out: fold attn into the projection, run it on v.
-        const Layer& proj = L(p + ".attn.project_out");
-        attention_fold(ctx, t, heads, net.vec.at(p + ".attn.temperature"), proj);
         Epilogue ea;
+        std::shared_ptr<void> wfold =
+            attention_fold(ctx, t, heads, net.vec.at(p + ".attn.temperature"), L(p + ".attn.project_out"),
+                           &ea.w_bstride);
+        ea.w_batch = wfold.get();
         ea.res = RES_ADD;
         ea.r1 = x.get();
         conv(p + ".attn.project_out", channel_view(t, 2 * dim, dim), ea, x);
@@ -271,12 +273,12 @@ struct Fwd {
         TensorP u = layer_norm(p + ".ffn.norm1", x);
         u = conv(p + ".ffn.project_in", u);
         const Layer& dw = L(p + ".ffn.dwconv");
-        TensorP f = ctx.alloc(hidden, u->h, u->w, u->dtype);
+        TensorP f = ctx.alloc(u->n, hidden, u->h, u->w, u->dtype);
         {
-            LaunchScope sc(ctx, "k_depthwise3x3", 2.0 * 9 * 2 * hidden * u->h * u->w,
-                           (double)dtype_size(u->dtype) * 3 * hidden * u->h * u->w);
-            ZJAI_HIP(launch_depthwise3x3(u->v, f->v, u->dtype, 2 * hidden, u->h, u->w, dw.dw_w, dw.bias, hidden,
-                                         ctx.stream));
+            LaunchScope sc(ctx, "k_depthwise3x3", 2.0 * 9 * 2 * hidden * u->n * u->h * u->w,
+                           (double)dtype_size(u->dtype) * 3 * hidden * u->n * u->h * u->w);
+            ZJAI_HIP(launch_depthwise3x3(u->v, f->v, u->dtype, u->n, 2 * hidden, u->h, u->w, dw.dw_w, dw.bias,
+                                         hidden, ctx.stream));
         }
         u.reset();
         Epilogue ef;
@@ -384,23 +386,24 @@ void secondary_forward(Context& ctx, const Net& net, const TensorP& y_luma, cons
     const int lh = std::min(y_luma->h, y_chroma->h), lw = std::min(y_luma->w, y_chroma->w);
     if (y_chroma->h != lh || y_chroma->w != lw)
         throw Error(ZJAI_E_INVALID_ARGUMENT, "chroma latent larger than the luma latent");
+    if (y_luma->n != y_chroma->n) throw Error(ZJAI_E_INVALID_ARGUMENT, "secondary: latent batch sizes differ");
     Fwd f{ctx, net};
-    const int dt = net.dtype;
+    const int dt = net.dtype, N = y_luma->n;
     const double es = dtype_size(dt);
-    TensorP cat = ctx.alloc(256, lh, lw, dt);
+    TensorP cat = ctx.alloc(N, 256, lh, lw, dt);
     {
-        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * 160 * lh * lw);
-        ZJAI_HIP(launch_copy(y_luma->v, cat->v, dt, 160, lh, lw, ctx.stream));
+        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * N * 160 * lh * lw);
+        ZJAI_HIP(launch_copy(y_luma->v, cat->v, dt, N, 160, lh, lw, ctx.stream));
     }
     {
-        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * 96 * lh * lw);
-        ZJAI_HIP(launch_copy(y_chroma->v, channel_view(cat, 160, 96)->v, dt, 96, lh, lw, ctx.stream));
+        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * N * 96 * lh * lw);
+        ZJAI_HIP(launch_copy(y_chroma->v, channel_view(cat, 160, 96)->v, dt, N, 96, lh, lw, ctx.stream));
     }
-    TensorP x = ctx.alloc(144, lh, lw, dt);
+    TensorP x = ctx.alloc(N, 144, lh, lw, dt);
     f.conv("first_stage.conv1", cat, Epilogue{}, channel_view(x, 0, 48));
     {
-        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * 96 * lh * lw);
-        ZJAI_HIP(launch_copy(y_chroma->v, channel_view(x, 48, 96)->v, dt, 96, lh, lw, ctx.stream));
+        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * N * 96 * lh * lw);
+        ZJAI_HIP(launch_copy(y_chroma->v, channel_view(x, 48, 96)->v, dt, N, 96, lh, lw, ctx.stream));
     }
     cat.reset();
     ctx.check_stop();

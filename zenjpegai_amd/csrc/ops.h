@@ -1,5 +1,5 @@
 // Bandwidth-bound kernels of the synthesis path (layout, elementwise, depthwise, layer norm,
-// channel attention). Host-callable launchers.
+// channel attention). Host-callable launchers; every one runs over N batch items (tiles).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -20,38 +20,46 @@ enum EltOp : int {
     EL_ELU_GATE = 7, // x = elu(x) * s
 };
 
-// Planar f32 [C][LH][LW] window (x0, y0, w, h) -> NHWC view of dtype.
-hipError_t launch_planar_to_nhwc(const float* src, int C, int LH, int LW, int x0, int y0, int h,
-                                 int w, View dst, int dtype, hipStream_t s);
-// NHWC view -> planar f32 [C][h][w].
-hipError_t launch_nhwc_to_planar(View src, int dtype, int C, int h, int w, float* dst,
+// Per batch item origin of a latent window.
+struct Windows {
+    int x0[MAXB], y0[MAXB];
+};
+
+// Planar f32 [C][LH][LW] windows (x0[b], y0[b], w, h) -> NHWC view of dtype, N items.
+hipError_t launch_planar_to_nhwc(const float* src, int C, int LH, int LW, const Windows& win, int N,
+                                 int h, int w, View dst, int dtype, hipStream_t s);
+// NHWC view -> planar f32 [N][C][h][w].
+hipError_t launch_nhwc_to_planar(View src, int dtype, int N, int C, int h, int w, float* dst,
                                  hipStream_t s);
-// x = op(x[, s]) over an h x w x C region.
-hipError_t launch_eltwise(int op, View x, View src, int dtype, int C, int h, int w, hipStream_t s);
-// NHWC copy of C channels over h x w (channel offsets / crops / concatenation).
-hipError_t launch_copy(View src, View dst, int dtype, int C, int h, int w, hipStream_t s);
+// x = op(x[, s]) over N x h x w x C.
+hipError_t launch_eltwise(int op, View x, View src, int dtype, int N, int C, int h, int w,
+                          hipStream_t s);
+// NHWC copy of C channels over N x h x w (channel offsets / crops / concatenation).
+hipError_t launch_copy(View src, View dst, int dtype, int N, int C, int h, int w, hipStream_t s);
 // Pixel shuffle NHWC -> NHWC: out channel c at (y*r+dy, x*r+dx) = in channel c*r*r+dy*r+dx.
-hipError_t launch_pixel_shuffle(View src, View dst, int dtype, int C_out, int h, int w, int r,
-                                hipStream_t s);
-// Depthwise 3x3, stride 1, pad 1, weights [C][9] f32, optional bias. With elu_half > 0 the
+hipError_t launch_pixel_shuffle(View src, View dst, int dtype, int N, int C_out, int h, int w,
+                                int r, hipStream_t s);
+// Depthwise 3x3, stride 1, pad 1, weights [9][C] f32, optional bias. With elu_half > 0 the
 // output keeps channels [0, elu_half) = elu(dw(c)) * dw(c + elu_half) (the FFN gate).
-hipError_t launch_depthwise3x3(View src, View dst, int dtype, int C, int h, int w,
+hipError_t launch_depthwise3x3(View src, View dst, int dtype, int N, int C, int h, int w,
                                const float* weight, const float* bias, int elu_half,
                                hipStream_t s);
 // Layer norm over channels per position (f64 sums), src -> dst.
-hipError_t launch_layer_norm(View src, View dst, int dtype, int C, int h, int w,
+hipError_t launch_layer_norm(View src, View dst, int dtype, int N, int C, int h, int w,
                              const float* weight, const float* bias, hipStream_t s);
-// Channel attention (src/nn/fast/math.rs:512-603), three phases:
+// Channel attention (src/nn/fast/math.rs:512-603), three phases per batch item:
 // 1. per-head Gram partial sums over chunks of positions (f32 MFMA): qkv view holds 3*dim
-//    channels; partial[nchunk][heads][c*c + 2c] f32 (c = dim / heads, 16 or 32);
-// 2. reduction (f64), normalisation, temperature and softmax -> attn [dim][c] f32;
-// 3. fold with the output projection proj [dim][dim] into a packed 1x1 conv weight.
+//    channels; partial[N][nchunk][heads][c*c + 2c] f32 (c = dim / heads <= 32);
+// 2. reduction (f64), normalisation, temperature and softmax -> attn [N][dim][c] f32;
+// 3. fold with the output projection proj [dim][dim] into a packed 1x1 conv weight per item
+//    (wpk + b * w_bstride).
 int attention_gram_chunks(int h, int w);
-hipError_t launch_attention_gram(View qkv, int dtype, int dim, int heads, int h, int w,
+hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads, int h, int w,
                                  float* partial, hipStream_t s);
-hipError_t launch_attention_softmax(const float* partial, int nchunk, int dim, int heads,
+hipError_t launch_attention_softmax(const float* partial, int N, int nchunk, int dim, int heads,
                                     const float* temperature, float* attn, hipStream_t s);
-hipError_t launch_attention_fold(const float* proj, const float* attn, int dim, int heads, int dtype,
-                                 int nblk, void* wpk, hipStream_t s);
+hipError_t launch_attention_fold(const float* proj, const float* attn, int N, int dim, int heads,
+                                 int dtype, int nblk, void* wpk, long long w_bstride,
+                                 hipStream_t s);
 
 }  // namespace zjai

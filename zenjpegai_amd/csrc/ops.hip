@@ -1,91 +1,92 @@
 // Bandwidth-bound kernels: layout changes, elementwise ops, depthwise 3x3, layer norm and the
 // reductions of channel attention. Element order and rounding follow the reference's
 // `nn::fast::{layers, depthwise, math}` (each op a separate IEEE operation, FMA only where the
-// reference's contract has one).
+// reference's contract has one). Every kernel covers N batch items (tiles of one shape).
 
 #include "ops.h"
 
 namespace zjai {
 
-template <typename T>
-__device__ __forceinline__ const T* at(const View& v, int y, int x, int c) {
-    return (const T*)v.p + (long long)y * v.row + (long long)x * v.cs + v.c_off + c;
-}
-template <typename T>
-__device__ __forceinline__ T* at_mut(const View& v, int y, int x, int c) {
-    return (T*)v.p + (long long)y * v.row + (long long)x * v.cs + v.c_off + c;
+// Decomposes a flat index over [N][h][w][q] (q = channel quads, fastest).
+struct Idx4 {
+    int b, y, x, cq;
+};
+__device__ __forceinline__ Idx4 split(long long i, int h, int w, int q) {
+    Idx4 r;
+    r.cq = (int)(i % q);
+    long long t = i / q;
+    r.x = (int)(t % w);
+    t /= w;
+    r.y = (int)(t % h);
+    r.b = (int)(t / h);
+    return r;
 }
 
 // ------------------------------------------------------------------------------ layout moves
 template <typename T>
-__global__ void k_planar_to_nhwc(const float* src, int C, int LH, int LW, int x0, int y0, int h,
+__global__ void k_planar_to_nhwc(const float* src, int C, int LH, int LW, Windows win, int N, int h,
                                  int w, View dst) {
     const int q = C / 4;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)h * w * q) return;
-    const int cq = (int)(i % q);
-    const long long pos = i / q;
-    const int x = (int)(pos % w), y = (int)(pos / w);
+    if (i >= (long long)N * h * w * q) return;
+    const Idx4 d = split(i, h, w, q);
     f32x4 v;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-        v[k] = src[((long long)(cq * 4 + k) * LH + (y0 + y)) * LW + (x0 + x)];
-    store4<T>(at_mut<T>(dst, y, x, cq * 4), v);
+        v[k] = src[((long long)(d.cq * 4 + k) * LH + (win.y0[d.b] + d.y)) * LW + (win.x0[d.b] + d.x)];
+    store4<T>(at_mut<T>(dst, d.b, d.y, d.x, d.cq * 4), v);
 }
 
 template <typename T>
-__global__ void k_nhwc_to_planar(View src, int C, int h, int w, float* dst) {
+__global__ void k_nhwc_to_planar(View src, int N, int C, int h, int w, float* dst) {
     const int q = (C + 3) / 4;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)h * w * q) return;
+    if (i >= (long long)N * h * w * q) return;
+    // x fastest so the planar writes coalesce.
     const int x = (int)(i % w);
-    const long long r = i / w;
-    const int y = (int)(r % h), cq = (int)(r / h);
+    long long r = i / w;
+    const int y = (int)(r % h);
+    r /= h;
+    const int cq = (int)(r % q), b = (int)(r / q);
     for (int k = 0; k < 4; ++k) {
         const int c = cq * 4 + k;
-        if (c < C) dst[((long long)c * h + y) * w + x] = to_f32(*at<T>(src, y, x, c));
+        if (c < C) dst[(((long long)b * C + c) * h + y) * w + x] = to_f32(*at<T>(src, b, y, x, c));
     }
 }
 
 template <typename T>
-__global__ void k_copy(View src, View dst, int C, int h, int w) {
+__global__ void k_copy(View src, View dst, int N, int C, int h, int w) {
     const int q = C / 4;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)h * w * q) return;
-    const int cq = (int)(i % q);
-    const long long pos = i / q;
-    const int x = (int)(pos % w), y = (int)(pos / w);
-    store4<T>(at_mut<T>(dst, y, x, cq * 4), load4<T>(at<T>(src, y, x, cq * 4)));
+    if (i >= (long long)N * h * w * q) return;
+    const Idx4 d = split(i, h, w, q);
+    store4<T>(at_mut<T>(dst, d.b, d.y, d.x, d.cq * 4), load4<T>(at<T>(src, d.b, d.y, d.x, d.cq * 4)));
 }
 
 template <typename T>
-__global__ void k_pixel_shuffle(View src, View dst, int C, int h, int w, int r) {
+__global__ void k_pixel_shuffle(View src, View dst, int N, int C, int h, int w, int r) {
     const int q = C / 4, oh = h * r, ow = w * r;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)oh * ow * q) return;
-    const int cq = (int)(i % q);
-    const long long pos = i / q;
-    const int X = (int)(pos % ow), Y = (int)(pos / ow);
-    const int y = Y / r, dy = Y - y * r, x = X / r, dx = X - x * r;
+    if (i >= (long long)N * oh * ow * q) return;
+    const Idx4 d = split(i, oh, ow, q);
+    const int y = d.y / r, dy = d.y - y * r, x = d.x / r, dx = d.x - x * r;
     f32x4 v;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) v[k] = to_f32(*at<T>(src, y, x, (cq * 4 + k) * r * r + dy * r + dx));
-    store4<T>(at_mut<T>(dst, Y, X, cq * 4), v);
+    for (int k = 0; k < 4; ++k) v[k] = to_f32(*at<T>(src, d.b, y, x, (d.cq * 4 + k) * r * r + dy * r + dx));
+    store4<T>(at_mut<T>(dst, d.b, d.y, d.x, d.cq * 4), v);
 }
 
 // ---------------------------------------------------------------------------------- eltwise
 template <typename T>
-__global__ void k_eltwise(int op, View xv, View sv, int C, int h, int w) {
+__global__ void k_eltwise(int op, View xv, View sv, int N, int C, int h, int w) {
     const int q = C / 4;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)h * w * q) return;
-    const int cq = (int)(i % q);
-    const long long pos = i / q;
-    const int x = (int)(pos % w), y = (int)(pos / w);
-    T* px = at_mut<T>(xv, y, x, cq * 4);
+    if (i >= (long long)N * h * w * q) return;
+    const Idx4 d = split(i, h, w, q);
+    T* px = at_mut<T>(xv, d.b, d.y, d.x, d.cq * 4);
     f32x4 v = load4<T>(px);
     f32x4 s = {0, 0, 0, 0};
-    if (op >= EL_ADD) s = load4<T>(at<T>(sv, y, x, cq * 4));
+    if (op >= EL_ADD) s = load4<T>(at<T>(sv, d.b, d.y, d.x, d.cq * 4));
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         float e = v[k];
@@ -112,30 +113,28 @@ __global__ void k_eltwise(int op, View xv, View sv, int C, int h, int w) {
 // Per output element: acc = bias; for ky, kx ascending: acc = fma(w, x, acc), padding taps
 // included (src/nn/fast/depthwise.rs:40-73). Weights are stored transposed, [9][C].
 template <typename T>
-__global__ void k_depthwise3x3(View src, View dst, int C, int h, int w, const float* wt,
+__global__ void k_depthwise3x3(View src, View dst, int N, int C, int h, int w, const float* wt,
                                const float* bias, int elu_half) {
     const int cout = elu_half > 0 ? elu_half : C;
     const int q = cout / 4;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)h * w * q) return;
-    const int cq = (int)(i % q);
-    const long long pos = i / q;
-    const int x = (int)(pos % w), y = (int)(pos / w);
+    if (i >= (long long)N * h * w * q) return;
+    const Idx4 d = split(i, h, w, q);
     const int npass = elu_half > 0 ? 2 : 1;
     f32x4 res[2];
     for (int pass = 0; pass < npass; ++pass) {
-        const int c0 = cq * 4 + pass * elu_half;
+        const int c0 = d.cq * 4 + pass * elu_half;
         f32x4 acc;
 #pragma unroll
         for (int k = 0; k < 4; ++k) acc[k] = bias ? bias[c0 + k] : 0.0f;
 #pragma unroll
         for (int ky = 0; ky < 3; ++ky) {
-            const int yy = y + ky - 1;
+            const int yy = d.y + ky - 1;
 #pragma unroll
             for (int kx = 0; kx < 3; ++kx) {
-                const int xx = x + kx - 1;
+                const int xx = d.x + kx - 1;
                 f32x4 xv = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (yy >= 0 && yy < h && xx >= 0 && xx < w) xv = load4<T>(at<T>(src, yy, xx, c0));
+                if (yy >= 0 && yy < h && xx >= 0 && xx < w) xv = load4<T>(at<T>(src, d.b, yy, xx, c0));
                 const f32x4 wv = *(const f32x4*)(wt + (ky * 3 + kx) * C + c0);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) acc[k] = fmaf(wv[k], xv[k], acc[k]);
@@ -153,19 +152,19 @@ __global__ void k_depthwise3x3(View src, View dst, int C, int h, int w, const fl
             out[k] = elu * res[1][k];
         }
     }
-    store4<T>(at_mut<T>(dst, y, x, cq * 4), out);
+    store4<T>(at_mut<T>(dst, d.b, d.y, d.x, d.cq * 4), out);
 }
 
 // ------------------------------------------------------------------------------ layer norm
 // `layer_norm_channels` (src/nn/fast/math.rs:423-448): f64 sums over channels in order,
 // (x - mean) / sqrt(var + 1e-5) * w + b with f32 operations.
 template <typename T>
-__global__ void k_layer_norm(View src, View dst, int C, int h, int w, const float* wt,
+__global__ void k_layer_norm(View src, View dst, int N, int C, int h, int w, const float* wt,
                              const float* bs) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)h * w) return;
-    const int x = (int)(i % w), y = (int)(i / w);
-    const T* p = at<T>(src, y, x, 0);
+    if (i >= (long long)N * h * w) return;
+    const Idx4 d = split(i, h, w, 1);
+    const T* p = at<T>(src, d.b, d.y, d.x, 0);
     double mean = 0.0;
     for (int c = 0; c < C; c += 4) {
         const f32x4 v = load4<T>(p + c);
@@ -176,11 +175,11 @@ __global__ void k_layer_norm(View src, View dst, int C, int h, int w, const floa
     for (int c = 0; c < C; c += 4) {
         const f32x4 v = load4<T>(p + c);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) { const double d = (double)v[k] - mean; var = var + d * d; }
+        for (int k = 0; k < 4; ++k) { const double e = (double)v[k] - mean; var = var + e * e; }
     }
     const float m32 = (float)mean;
     const float den = sqrtf((float)(var / (double)C) + 1e-5f);
-    T* o = at_mut<T>(dst, y, x, 0);
+    T* o = at_mut<T>(dst, d.b, d.y, d.x, 0);
     for (int c = 0; c < C; c += 4) {
         const f32x4 v = load4<T>(p + c);
         f32x4 r;
@@ -210,9 +209,10 @@ __global__ void __launch_bounds__(256) k_attention_gram(View qkv, int dim, int h
     const int c = dim / heads, nb = (c + 15) / 16, E = c * c + 2 * c;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m = lane & 15, kq = lane >> 4;
+    const int b = blockIdx.y, nchunk = gridDim.x;
     const int p0 = blockIdx.x * ATT_POS;
     const int p1 = min(p0 + ATT_POS, n);
-    const T* base = (const T*)qkv.p + qkv.c_off;
+    const T* base = (const T*)qkv.p + (long long)b * qkv.bstride + qkv.c_off;
     for (int hd = wave; hd < heads; hd += 4) {
         f32x4 g[2][2], dq[2], dk[2];
         const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -228,10 +228,10 @@ __global__ void __launch_bounds__(256) k_attention_gram(View qkv, int dim, int h
                 const int y = pos / w, x = pos - y * w;
                 const T* px = base + (long long)y * qkv.row + (long long)x * qkv.cs + hd * c + m;
 #pragma unroll
-                for (int b = 0; b < 2; ++b)
-                    if (b * 16 + m < c) {
-                        aq[b] = to_f32(px[b * 16]);
-                        ak[b] = to_f32(px[dim + b * 16]);
+                for (int bb = 0; bb < 2; ++bb)
+                    if (bb * 16 + m < c) {
+                        aq[bb] = to_f32(px[bb * 16]);
+                        ak[bb] = to_f32(px[dim + bb * 16]);
                     }
             }
 #pragma unroll
@@ -245,7 +245,7 @@ __global__ void __launch_bounds__(256) k_attention_gram(View qkv, int dim, int h
             }
         }
         // Lane l holds D[4 * (l / 16) + i][l % 16] of each 16x16 tile.
-        float* out = partial + ((long long)blockIdx.x * heads + hd) * E;
+        float* out = partial + (((long long)b * nchunk + blockIdx.x) * heads + hd) * E;
 #pragma unroll
         for (int bi = 0; bi < 2; ++bi) {
             if (bi >= nb) continue;
@@ -265,23 +265,23 @@ __global__ void __launch_bounds__(256) k_attention_gram(View qkv, int dim, int h
     }
 }
 
-// One wave per attention row (head hd, query i): reduce the chunk partials in f64, normalise
-// (F.normalize, eps 1e-12), scale by the temperature, softmax with the Cephes exp and an f64 sum
-// in index order (src/nn/fast/math.rs:558-577).
+// One wave per attention row (item b, head hd, query i): reduce the chunk partials in f64,
+// normalise (F.normalize, eps 1e-12), scale by the temperature, softmax with the Cephes exp and
+// an f64 sum in index order (src/nn/fast/math.rs:558-577).
 __global__ void __launch_bounds__(64) k_attention_softmax(const float* partial, int nchunk, int dim,
                                                           int heads, const float* temperature,
                                                           float* attn) {
     __shared__ double s_qq;
     __shared__ float s_e[64];
-    const int row = blockIdx.x, c = dim / heads, hd = row / c, i = row - hd * c;
+    const int row = blockIdx.x, b = blockIdx.y, c = dim / heads, hd = row / c, i = row - hd * c;
     const int E = c * c + 2 * c, lane = threadIdx.x;
     double sqk = 0.0, skk = 0.0, sqq = 0.0;
     if (lane < c) {
         for (int k = 0; k < nchunk; ++k) {
-            const float* b = partial + ((long long)k * heads + hd) * E;
-            sqk += (double)b[i * c + lane];
-            skk += (double)b[c * c + c + lane];
-            if (lane == 0) sqq += (double)b[c * c + i];
+            const float* pb = partial + (((long long)b * nchunk + k) * heads + hd) * E;
+            sqk += (double)pb[i * c + lane];
+            skk += (double)pb[c * c + c + lane];
+            if (lane == 0) sqq += (double)pb[c * c + i];
         }
     }
     if (lane == 0) s_qq = sqq;
@@ -303,22 +303,23 @@ __global__ void __launch_bounds__(64) k_attention_softmax(const float* partial, 
     __syncthreads();
     double sum = 0.0;
     for (int j = 0; j < c; ++j) sum += (double)s_e[j];
-    if (lane < c) attn[row * c + lane] = s_e[lane] / (float)sum;
+    if (lane < c) attn[((long long)b * dim + row) * c + lane] = s_e[lane] / (float)sum;
 }
 
 // Folds the output projection into the attention: wfold[o][hd*c + j] =
 // sum_i proj[o][hd*c + i] * attn[hd*c + i][j] (f64 accumulate), stored straight into the packed
-// 1x1 conv layout [chunk][nblk][16][CK] of the storage type.
+// 1x1 conv layout [chunk][nblk][16][CK] of the storage type, one weight per batch item.
 template <typename T>
 __global__ void k_attention_fold(const float* proj, const float* attn, int dim, int heads, int nblk,
-                                 int CK, T* wpk) {
-    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+                                 int CK, T* wpk, long long w_bstride) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x, b = blockIdx.y;
     if (e >= dim * dim) return;
     const int c = dim / heads, o = e / dim, col = e - o * dim, hd = col / c, j = col - hd * c;
+    const float* at_b = attn + (long long)b * dim * c;
     double s = 0.0;
-    for (int i = 0; i < c; ++i) s += (double)proj[o * dim + hd * c + i] * (double)attn[(hd * c + i) * c + j];
+    for (int i = 0; i < c; ++i) s += (double)proj[o * dim + hd * c + i] * (double)at_b[(hd * c + i) * c + j];
     const int ch = col / CK, kk = col - ch * CK;
-    wpk[(((long long)ch * nblk + o / 16) * 16 + o % 16) * CK + kk] = from_f32<T>((float)s);
+    wpk[(long long)b * w_bstride + (((long long)ch * nblk + o / 16) * 16 + o % 16) * CK + kk] = from_f32<T>((float)s);
 }
 
 // ------------------------------------------------------------------------------- launchers
@@ -332,87 +333,90 @@ static inline dim3 grid_for(long long n) { return dim3((unsigned)((n + 255) / 25
         default: return hipErrorInvalidValue;                                                \
     }
 
-hipError_t launch_planar_to_nhwc(const float* src, int C, int LH, int LW, int x0, int y0, int h,
-                                 int w, View dst, int dtype, hipStream_t s) {
-    const long long n = (long long)h * w * (C / 4);
+hipError_t launch_planar_to_nhwc(const float* src, int C, int LH, int LW, const Windows& win, int N,
+                                 int h, int w, View dst, int dtype, hipStream_t s) {
+    if (N < 1 || N > MAXB) return hipErrorInvalidValue;
+    const long long n = (long long)N * h * w * (C / 4);
     if (n == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_planar_to_nhwc, <<<grid_for(n), 256, 0, s>>>(src, C, LH, LW, x0, y0, h, w, dst))
+    ZJAI_DISPATCH(dtype, k_planar_to_nhwc, <<<grid_for(n), 256, 0, s>>>(src, C, LH, LW, win, N, h, w, dst))
     return hipGetLastError();
 }
 
-hipError_t launch_nhwc_to_planar(View src, int dtype, int C, int h, int w, float* dst,
+hipError_t launch_nhwc_to_planar(View src, int dtype, int N, int C, int h, int w, float* dst,
                                  hipStream_t s) {
-    const long long n = (long long)h * w * ((C + 3) / 4);
+    const long long n = (long long)N * h * w * ((C + 3) / 4);
     if (n == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_nhwc_to_planar, <<<grid_for(n), 256, 0, s>>>(src, C, h, w, dst))
+    ZJAI_DISPATCH(dtype, k_nhwc_to_planar, <<<grid_for(n), 256, 0, s>>>(src, N, C, h, w, dst))
     return hipGetLastError();
 }
 
-hipError_t launch_eltwise(int op, View x, View src, int dtype, int C, int h, int w, hipStream_t s) {
-    const long long n = (long long)h * w * (C / 4);
+hipError_t launch_eltwise(int op, View x, View src, int dtype, int N, int C, int h, int w,
+                          hipStream_t s) {
+    const long long n = (long long)N * h * w * (C / 4);
     if (n == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_eltwise, <<<grid_for(n), 256, 0, s>>>(op, x, src, C, h, w))
+    ZJAI_DISPATCH(dtype, k_eltwise, <<<grid_for(n), 256, 0, s>>>(op, x, src, N, C, h, w))
     return hipGetLastError();
 }
 
-hipError_t launch_copy(View src, View dst, int dtype, int C, int h, int w, hipStream_t s) {
-    const long long n = (long long)h * w * (C / 4);
+hipError_t launch_copy(View src, View dst, int dtype, int N, int C, int h, int w, hipStream_t s) {
+    const long long n = (long long)N * h * w * (C / 4);
     if (n == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_copy, <<<grid_for(n), 256, 0, s>>>(src, dst, C, h, w))
+    ZJAI_DISPATCH(dtype, k_copy, <<<grid_for(n), 256, 0, s>>>(src, dst, N, C, h, w))
     return hipGetLastError();
 }
 
-hipError_t launch_pixel_shuffle(View src, View dst, int dtype, int C_out, int h, int w, int r,
-                                hipStream_t s) {
-    const long long n = (long long)h * r * w * r * (C_out / 4);
+hipError_t launch_pixel_shuffle(View src, View dst, int dtype, int N, int C_out, int h, int w,
+                                int r, hipStream_t s) {
+    const long long n = (long long)N * h * r * w * r * (C_out / 4);
     if (n == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_pixel_shuffle, <<<grid_for(n), 256, 0, s>>>(src, dst, C_out, h, w, r))
+    ZJAI_DISPATCH(dtype, k_pixel_shuffle, <<<grid_for(n), 256, 0, s>>>(src, dst, N, C_out, h, w, r))
     return hipGetLastError();
 }
 
-hipError_t launch_depthwise3x3(View src, View dst, int dtype, int C, int h, int w,
+hipError_t launch_depthwise3x3(View src, View dst, int dtype, int N, int C, int h, int w,
                                const float* weight, const float* bias, int elu_half,
                                hipStream_t s) {
     const int cout = elu_half > 0 ? elu_half : C;
-    const long long n = (long long)h * w * (cout / 4);
+    const long long n = (long long)N * h * w * (cout / 4);
     if (n == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_depthwise3x3, <<<grid_for(n), 256, 0, s>>>(src, dst, C, h, w, weight, bias, elu_half))
+    ZJAI_DISPATCH(dtype, k_depthwise3x3, <<<grid_for(n), 256, 0, s>>>(src, dst, N, C, h, w, weight, bias, elu_half))
     return hipGetLastError();
 }
 
-hipError_t launch_layer_norm(View src, View dst, int dtype, int C, int h, int w,
+hipError_t launch_layer_norm(View src, View dst, int dtype, int N, int C, int h, int w,
                              const float* weight, const float* bias, hipStream_t s) {
-    const long long n = (long long)h * w;
+    const long long n = (long long)N * h * w;
     if (n == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_layer_norm, <<<grid_for(n), 256, 0, s>>>(src, dst, C, h, w, weight, bias))
+    ZJAI_DISPATCH(dtype, k_layer_norm, <<<grid_for(n), 256, 0, s>>>(src, dst, N, C, h, w, weight, bias))
     return hipGetLastError();
 }
 
-hipError_t launch_attention_gram(View qkv, int dtype, int dim, int heads, int h, int w,
+hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads, int h, int w,
                                  float* partial, hipStream_t s) {
-    const int c = dim / heads;
+    const int c = heads > 0 ? dim / heads : 0;
     if (heads <= 0 || dim % heads || c < 1 || c > 32) return hipErrorInvalidValue;
     const int nchunk = attention_gram_chunks(h, w);
-    if (nchunk == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_attention_gram, <<<dim3(nchunk), 256, 0, s>>>(qkv, dim, heads, h * w, w, partial))
+    if (nchunk == 0 || N == 0) return hipSuccess;
+    ZJAI_DISPATCH(dtype, k_attention_gram, <<<dim3(nchunk, N), 256, 0, s>>>(qkv, dim, heads, h * w, w, partial))
     return hipGetLastError();
 }
 
-hipError_t launch_attention_softmax(const float* partial, int nchunk, int dim, int heads,
+hipError_t launch_attention_softmax(const float* partial, int N, int nchunk, int dim, int heads,
                                     const float* temperature, float* attn, hipStream_t s) {
     if (dim / heads > 64) return hipErrorInvalidValue;
-    k_attention_softmax<<<dim, 64, 0, s>>>(partial, nchunk, dim, heads, temperature, attn);
+    k_attention_softmax<<<dim3(dim, N), 64, 0, s>>>(partial, nchunk, dim, heads, temperature, attn);
     return hipGetLastError();
 }
 
-hipError_t launch_attention_fold(const float* proj, const float* attn, int dim, int heads, int dtype,
-                                 int nblk, void* wpk, hipStream_t s) {
+hipError_t launch_attention_fold(const float* proj, const float* attn, int N, int dim, int heads,
+                                 int dtype, int nblk, void* wpk, long long w_bstride,
+                                 hipStream_t s) {
     const int CK = dtype == DT_F32 ? 16 : 32;
-    const dim3 g((dim * dim + 255) / 256);
+    const dim3 g((dim * dim + 255) / 256, N);
     switch (dtype) {
-        case DT_F32: k_attention_fold<float><<<g, 256, 0, s>>>(proj, attn, dim, heads, nblk, CK, (float*)wpk); break;
-        case DT_F16: k_attention_fold<_Float16><<<g, 256, 0, s>>>(proj, attn, dim, heads, nblk, CK, (_Float16*)wpk); break;
-        case DT_BF16: k_attention_fold<__bf16><<<g, 256, 0, s>>>(proj, attn, dim, heads, nblk, CK, (__bf16*)wpk); break;
+        case DT_F32: k_attention_fold<float><<<g, 256, 0, s>>>(proj, attn, dim, heads, nblk, CK, (float*)wpk, w_bstride); break;
+        case DT_F16: k_attention_fold<_Float16><<<g, 256, 0, s>>>(proj, attn, dim, heads, nblk, CK, (_Float16*)wpk, w_bstride); break;
+        case DT_BF16: k_attention_fold<__bf16><<<g, 256, 0, s>>>(proj, attn, dim, heads, nblk, CK, (__bf16*)wpk, w_bstride); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -58,12 +58,13 @@ private:
 
 struct Context;
 
-// Device activation (NHWC view). `owner` blocks return to the pool when the tensor dies.
+// Device activation: n batch items (tiles of one shape) of [h][w][c], NHWC. The pool block
+// returns to the pool when the last tensor or view of it dies.
 struct Tensor {
     Context* ctx = nullptr;
-    void* base = nullptr;  // pool block (owner) or nullptr for views
+    void* base = nullptr;
     View v{};
-    int dtype = DT_F32, c = 0, h = 0, w = 0;
+    int dtype = DT_F32, n = 1, c = 0, h = 0, w = 0;
     std::shared_ptr<void> keep;  // keeps the underlying block alive for views
     int cs() const { return v.cs; }
 };
@@ -91,7 +92,7 @@ struct Context {
     std::vector<hipEvent_t> ev_pool;
     size_t ev_used = 0;
 
-    TensorP alloc(int c, int h, int w, int dtype);
+    TensorP alloc(int n, int c, int h, int w, int dtype);
     void check_stop();
     hipEvent_t take_event();
     ~Context();
@@ -145,19 +146,23 @@ LayerP make_conv(Context& ctx, int cin, int cout, int kh, int kw, int stride, in
 LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, int pad,
                            int out_pad, const float* weight, const float* bias, int dtype);
 
-// Fused epilogue description for one conv launch.
+// Fused epilogue description for one conv launch. `w_batch` (with `w_bstride` elements between
+// items) replaces the layer's packed weight with one weight per batch item.
 struct Epilogue {
     int act = ACT_NONE, res = RES_NONE, ps = 1, relu6_in = 0;
     const Tensor* r1 = nullptr;
     const Tensor* r2 = nullptr;
+    const void* w_batch = nullptr;
+    long long w_bstride = 0;
 };
 
-// Planar picture destination of a last layer.
+// Planar picture destination of a last layer; windows per batch item.
 struct PlaneOut {
     void* plane = nullptr;
     long long row = 0, cstride = 0;
-    int win_y0 = 0, win_x0 = 0, win_h = 0, win_w = 0, dst_y0 = 0, dst_x0 = 0, sv = 1, sh = 1;
-    int denorm = 1, bit_depth = 0;
+    int sv = 1, sh = 1, denorm = 1, bit_depth = 0;
+    int win_y0[MAXB] = {}, win_x0[MAXB] = {}, win_h[MAXB] = {}, win_w[MAXB] = {};
+    int dst_y0[MAXB] = {}, dst_x0[MAXB] = {};
 };
 
 // Runs a layer on x. With `dst` null a new tensor is allocated; with `plane` set the output
@@ -168,11 +173,13 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
 std::string conv_kernel_name(int kind, int dtype, TileCfg c);
 
 // Channel attention of qkv (3*dim channels, `heads` heads, device temperature) folded with the
-// projection layer `proj` (a dense 1x1 dim -> dim layer holding its f32 weight): afterwards
-// proj's packed weight is proj . blockdiag(attn), so proj applied to the v channels of qkv
-// yields project_out(channel_attention(qkv)).
-void attention_fold(Context& ctx, const TensorP& qkv, int heads, const float* temperature,
-                    const Layer& proj);
+// projection layer `proj` (a dense 1x1 dim -> dim layer holding its f32 weight): returns, per
+// batch item, proj . blockdiag(attn) packed like proj's weight (`*w_bstride` elements apart), so
+// proj run with these weights on the v channels of qkv yields
+// project_out(channel_attention(qkv)).
+std::shared_ptr<void> attention_fold(Context& ctx, const TensorP& qkv, int heads,
+                                     const float* temperature, const Layer& proj,
+                                     long long* w_bstride);
 
 // ---------------------------------------------------------------------------- synthesis nets
 enum Op : int { OP_SOP = 0, OP_BOP = 1, OP_HOP = 2 };

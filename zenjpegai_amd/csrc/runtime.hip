@@ -66,18 +66,20 @@ Pool::~Pool() {
 }
 
 // --------------------------------------------------------------------------------- tensors
-TensorP Context::alloc(int c, int h, int w, int dtype) {
-    if (c <= 0 || h < 0 || w < 0) throw Error(ZJAI_E_INVALID_ARGUMENT, "tensor: bad shape");
+TensorP Context::alloc(int n, int c, int h, int w, int dtype) {
+    if (n <= 0 || n > MAXB || c <= 0 || h < 0 || w < 0) throw Error(ZJAI_E_INVALID_ARGUMENT, "tensor: bad shape");
     auto t = std::make_shared<Tensor>();
     t->ctx = this;
     t->dtype = dtype;
+    t->n = n;
     t->c = c;
     t->h = h;
     t->w = w;
     t->v.cs = round_up(c, 8);
     t->v.row = (long long)w * t->v.cs;
+    t->v.bstride = (long long)h * t->v.row;
     t->v.c_off = 0;
-    const size_t bytes = (size_t)h * (size_t)t->v.row * dtype_size(dtype);
+    const size_t bytes = (size_t)n * (size_t)t->v.bstride * dtype_size(dtype);
     void* p = pool.alloc(bytes);
     Context* self = this;
     t->keep = std::shared_ptr<void>(p, [self](void* q) { self->pool.release(q); });
@@ -364,12 +366,13 @@ std::string conv_kernel_name(int kind, int dtype, TileCfg c) {
     snprintf(buf, sizeof buf, "conv_igemm<%s, %s, %d, %d, %d, %d>", ty[dtype], geo[kind], c.wc, c.wp, c.cf, c.pf);
     return buf;
 }
-static View view_of(const Tensor* t) { return t ? t->v : View{nullptr, 0, 0, 0}; }
+static View view_of(const Tensor* t) { return t ? t->v : View{nullptr, 0, 0, 0, 0}; }
 
 TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilogue& e,
                      const TensorP& dst, const PlaneOut* plane) {
     if (x->c != L.cin) throw Error(ZJAI_E_INVALID_ARGUMENT, "conv: input channel count mismatch");
     if (x->dtype != L.dtype) throw Error(ZJAI_E_INVALID_ARGUMENT, "conv: input precision mismatch");
+    const int N = x->n;
     int OH, OW;
     L.out_size(x->h, x->w, &OH, &OW);
     if (OH <= 0 || OW <= 0) throw Error(ZJAI_E_INVALID_ARGUMENT, "conv: input smaller than the kernel");
@@ -377,7 +380,7 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
     if (L.cout % (ps * ps)) throw Error(ZJAI_E_INVALID_ARGUMENT, "pixel_shuffle: channels not divisible by r^2");
     for (const Tensor* r : {e.r1, e.r2}) {
         if (!r) continue;
-        if (r->c != L.cout || r->h != OH || r->w != OW || r->dtype != L.dtype)
+        if (r->n != N || r->c != L.cout || r->h != OH || r->w != OW || r->dtype != L.dtype)
             throw Error(ZJAI_E_INVALID_ARGUMENT, "conv epilogue: residual shape differs");
     }
     if ((e.res != RES_NONE && !e.r1) || (e.res == RES_CAB && !e.r2))
@@ -385,35 +388,39 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
     TensorP y;
     if (!plane) {
         if (dst) {
-            if (dst->c != L.cout / (ps * ps) || dst->h != OH * ps || dst->w != OW * ps || dst->dtype != L.dtype)
+            if (dst->n != N || dst->c != L.cout / (ps * ps) || dst->h != OH * ps || dst->w != OW * ps ||
+                dst->dtype != L.dtype)
                 throw Error(ZJAI_E_INVALID_ARGUMENT, "conv: destination shape differs");
             y = dst;
         } else {
-            y = ctx.alloc(L.cout / (ps * ps), OH * ps, OW * ps, L.dtype);
+            y = ctx.alloc(N, L.cout / (ps * ps), OH * ps, OW * ps, L.dtype);
         }
     }
+    const double es = dtype_size(L.dtype);
     if (L.depthwise) {
-        if (e.act || e.res || ps != 1 || e.relu6_in || plane)
+        if (e.act || e.res || ps != 1 || e.relu6_in || plane || e.w_batch)
             throw Error(ZJAI_E_UNSUPPORTED, "depthwise: fused epilogue");
-        const double es = dtype_size(L.dtype);
-        LaunchScope sc(ctx, "k_depthwise3x3", 2.0 * 9 * L.cin * x->h * x->w, 2.0 * es * L.cin * x->h * x->w);
-        ZJAI_HIP(launch_depthwise3x3(x->v, y->v, L.dtype, L.cin, x->h, x->w, L.dw_w, L.bias, 0, ctx.stream));
+        LaunchScope sc(ctx, "k_depthwise3x3", 2.0 * 9 * N * L.cin * x->h * x->w, 2.0 * es * N * L.cin * x->h * x->w);
+        ZJAI_HIP(launch_depthwise3x3(x->v, y->v, L.dtype, N, L.cin, x->h, x->w, L.dw_w, L.bias, 0, ctx.stream));
         return y;
     }
     ConvParams p{};
     p.x = x->v;
     p.H = x->h;
     p.W = x->w;
+    p.N = N;
     p.OH = OH;
     p.OW = OW;
-    p.y = y ? y->v : View{nullptr, 0, 0, 0};
-    p.w = L.wpk;
+    p.y = y ? y->v : View{nullptr, 0, 0, 0, 0};
+    p.w = e.w_batch ? e.w_batch : L.wpk;
+    p.w_bstride = e.w_batch ? e.w_bstride : 0;
     p.bias = L.bias;
     p.cin_g = L.cin / L.groups;
     p.cout_g = L.cout / L.groups;
     p.groups = L.groups;
     p.nchunks = L.nchunks;
     p.nblk_g = L.nblk_g;
+    p.ntiles = L.groups * L.nblk_g / (L.cfg.wc * L.cfg.cf);
     p.phase_stride = L.phase_stride;
     p.pad_t = L.pad_h + L.extra[0];
     p.pad_l = L.pad_w + L.extra[1];
@@ -428,16 +435,18 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
         p.plane = plane->plane;
         p.pl_row = plane->row;
         p.pl_cstride = plane->cstride;
-        p.win_y0 = plane->win_y0;
-        p.win_x0 = plane->win_x0;
-        p.win_h = plane->win_h;
-        p.win_w = plane->win_w;
-        p.dst_y0 = plane->dst_y0;
-        p.dst_x0 = plane->dst_x0;
         p.sv = plane->sv;
         p.sh = plane->sh;
         p.denorm = plane->denorm;
         p.bit_depth = plane->bit_depth;
+        for (int b = 0; b < MAXB; ++b) {
+            p.win_y0[b] = plane->win_y0[b];
+            p.win_x0[b] = plane->win_x0[b];
+            p.win_h[b] = plane->win_h[b];
+            p.win_w[b] = plane->win_w[b];
+            p.dst_y0[b] = plane->dst_y0[b];
+            p.dst_x0[b] = plane->dst_x0[b];
+        }
     } else {
         p.out_mode = OUT_NHWC;
         p.sv = p.sh = 1;
@@ -460,40 +469,49 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
     } else {
         macs = (double)OH * OW * L.cout * (L.cin / L.groups) * L.kh * L.kw;
     }
-    const double es = dtype_size(L.dtype);
-    double bytes = es * ((double)L.cin * x->h * x->w + (double)L.cout * OH * OW) + (double)L.wpk_bytes;
-    if (e.r1) bytes += es * (double)L.cout * OH * OW;
-    if (e.r2) bytes += es * (double)L.cout * OH * OW;
+    macs *= N;
+    double bytes = es * N * ((double)L.cin * x->h * x->w + (double)L.cout * OH * OW) +
+                   (double)L.wpk_bytes * (e.w_batch ? N : 1);
+    if (e.r1) bytes += es * N * (double)L.cout * OH * OW;
+    if (e.r2) bytes += es * N * (double)L.cout * OH * OW;
     LaunchScope sc(ctx, conv_kernel_name(L.kind, L.dtype, L.cfg), 2.0 * macs, bytes);
     ZJAI_HIP(launch_conv(L.kind, L.dtype, L.cfg, p, ctx.stream));
     return y;
 }
 
 // -------------------------------------------------------------------- attention + projection
-void attention_fold(Context& ctx, const TensorP& qkv, int heads, const float* temperature,
-                    const Layer& proj) {
-    const int dim = qkv->c / 3, c = dim / heads;
+std::shared_ptr<void> attention_fold(Context& ctx, const TensorP& qkv, int heads, const float* temperature,
+                                     const Layer& proj, long long* w_bstride) {
+    const int dim = qkv->c / 3, c = dim / heads, N = qkv->n;
     if (proj.kind != CK_1x1 || proj.groups != 1 || proj.depthwise || proj.transposed || !proj.w_f32 ||
         proj.cin != dim || proj.cout != dim || proj.dtype != qkv->dtype)
         throw Error(ZJAI_E_INVALID_ARGUMENT, "attention: projection is not a dense dim x dim 1x1 layer");
-    const int n = qkv->h * qkv->w, nchunk = attention_gram_chunks(qkv->h, qkv->w);
+    const int n = qkv->h * qkv->w, nchunk = std::max(attention_gram_chunks(qkv->h, qkv->w), 1);
     const int total = heads * (c * c + 2 * c);
     const double es = dtype_size(qkv->dtype);
-    float* partial = (float*)ctx.pool.alloc(sizeof(float) * ((size_t)std::max(nchunk, 1) * total + (size_t)dim * c));
+    float* partial = (float*)ctx.pool.alloc(sizeof(float) * N * ((size_t)nchunk * total + (size_t)dim * c));
     std::shared_ptr<void> keep(partial, [&ctx](void* q) { ctx.pool.release(q); });
-    float* attn = partial + (size_t)std::max(nchunk, 1) * total;
+    float* attn = partial + (size_t)N * nchunk * total;
+    void* wfold = ctx.pool.alloc(proj.wpk_bytes * N);
+    std::shared_ptr<void> out(wfold, [&ctx](void* q) { ctx.pool.release(q); });
+    *w_bstride = (long long)(proj.wpk_bytes / dtype_size(proj.dtype));
+    const int CK = 64 / dtype_size(proj.dtype);
+    if (proj.nblk_g * 16 != dim || proj.nchunks * CK != dim)  // padded rows / columns stay zero
+        ZJAI_HIP(hipMemsetAsync(wfold, 0, proj.wpk_bytes * N, ctx.stream));
     {
-        LaunchScope sc(ctx, "k_attention_gram", 2.0 * total * n, es * 2 * dim * n + 4.0 * nchunk * total);
-        ZJAI_HIP(launch_attention_gram(qkv->v, qkv->dtype, dim, heads, qkv->h, qkv->w, partial, ctx.stream));
+        LaunchScope sc(ctx, "k_attention_gram", 2.0 * N * total * n, es * N * 2 * dim * n + 4.0 * N * nchunk * total);
+        ZJAI_HIP(launch_attention_gram(qkv->v, qkv->dtype, N, dim, heads, qkv->h, qkv->w, partial, ctx.stream));
     }
     {
-        LaunchScope sc(ctx, "k_attention_softmax", 0.0, 4.0 * nchunk * total);
-        ZJAI_HIP(launch_attention_softmax(partial, nchunk, dim, heads, temperature, attn, ctx.stream));
+        LaunchScope sc(ctx, "k_attention_softmax", 0.0, 4.0 * N * nchunk * total);
+        ZJAI_HIP(launch_attention_softmax(partial, N, nchunk, dim, heads, temperature, attn, ctx.stream));
     }
     {
-        LaunchScope sc(ctx, "k_attention_fold", 2.0 * dim * dim * c, 4.0 * dim * dim + es * dim * dim);
-        ZJAI_HIP(launch_attention_fold(proj.w_f32, attn, dim, heads, proj.dtype, proj.nblk_g, proj.wpk, ctx.stream));
+        LaunchScope sc(ctx, "k_attention_fold", 2.0 * N * dim * dim * c, 4.0 * dim * dim + es * N * dim * dim);
+        ZJAI_HIP(launch_attention_fold(proj.w_f32, attn, N, dim, heads, proj.dtype, proj.nblk_g, wfold,
+                                       *w_bstride, ctx.stream));
     }
+    return out;
 }
 
 }  // namespace zjai
