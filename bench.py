@@ -93,16 +93,21 @@ def profile_step(eng, pic):
     return by
 
 
-def read_traffic(kernel, workload):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
+def read_traffic(kernel, workload, precision):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (``profiles/traffic_<workload>_<precision>.md``, lines
+    ``TRAFFIC <workload> <precision> <bytes> <kernel>``), or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}_{precision}.md")
     try:
         with open(path) as f:
-            t = json.load(f)
-        e = t.get(workload, {}).get(kernel)
-        return None if e is None else float(e["bytes_per_launch"])
-    except (OSError, ValueError, KeyError):
-        return None
+            for line in f:
+                parts = line.split(None, 4)
+                if len(parts) == 5 and parts[0] == "TRAFFIC" and parts[1] == workload \
+                        and parts[2] == precision and parts[4].strip() == kernel:
+                    return float(parts[3])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(info, seconds_cap=60.0):
@@ -135,7 +140,23 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the extra precision / cfg4 runs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--profile-out", default=None, help="write the per-kernel profile (JSON)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (k_copy) 5 times: the known-size "
+                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    if args.copy_probe:
+        import numpy as np
+        from zenjpegai_amd import nn
+        eng = nn.Engine(0, "f32")
+        c, w = 64, 1024
+        h = args.copy_probe * (1 << 20) // (c * w * 4)
+        t = nn.BTensor.zeros(eng, c, h, w)
+        for _ in range(5):
+            nn.BTensor.cat([t])
+        eng.sync()
+        print(json.dumps({"copy_probe_bytes_read": c * h * w * 4, "copy_probe_bytes_written": c * h * w * 4,
+                          "kernel": "k_copy", "dispatches": 5}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only; the synthesis tiles would shard "
               "across GPUs with no collective (see DESIGN.md), but no multi-GPU figure is "
@@ -167,7 +188,7 @@ def main():
         peak = PEAK_HBM_GBS
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": peak, "unit": "GB/s"}
     roof["frac"] = round(ach / peak, 4)
-    roof["traffic"] = read_traffic(dom_name, args.workload)
+    roof["traffic"] = read_traffic(dom_name, args.workload, args.precision)
     roof["kernel"] = dom_name
     roof["launches"] = dom["count"]
     roof["avg_launch_us"] = round(dom["ms"] * 1e3 / dom["count"], 2)
