@@ -63,7 +63,7 @@ TensorP planar_upload(Context& c, const float* data, int ch, int h, int w, int d
     std::shared_ptr<void> keep(stage, [&c](void* q) { c.pool.release(q); });
     ZJAI_HIP(hipMemcpyAsync(stage, data, n * 4, hipMemcpyHostToDevice, c.stream));
     {
-        LaunchScope sc(c, "k_planar_to_nhwc", 0.0, (4.0 + dtype_size(dtype)) * n);
+        LaunchScope sc(c, kname("k_planar_to_nhwc", dtype), 0.0, (4.0 + dtype_size(dtype)) * n);
         ZJAI_HIP(launch_planar_to_nhwc(stage, ch, h, w, Windows{}, 1, h, w, t->v, dtype, c.stream));
     }
     ZJAI_HIP(hipStreamSynchronize(c.stream));
@@ -215,7 +215,7 @@ extern "C" int32_t zjai_tensor_to_planar(zjai_ctx* ctx, const zjai_tensor* t, fl
         float* stage = (float*)ctx->c.pool.alloc(n * 4);
         std::shared_ptr<void> keep(stage, [ctx](void* q) { ctx->c.pool.release(q); });
         {
-            LaunchScope sc(ctx->c, "k_nhwc_to_planar", 0.0, (4.0 + dtype_size(x.dtype)) * n);
+            LaunchScope sc(ctx->c, kname("k_nhwc_to_planar", x.dtype), 0.0, (4.0 + dtype_size(x.dtype)) * n);
             ZJAI_HIP(launch_nhwc_to_planar(x.v, x.dtype, x.n, x.c, x.h, x.w, stage, ctx->c.stream));
         }
         ZJAI_HIP(hipMemcpyAsync(data, stage, n * 4, hipMemcpyDeviceToHost, ctx->c.stream));
@@ -255,7 +255,7 @@ extern "C" int32_t zjai_tensor_cat(zjai_ctx* ctx, const zjai_tensor* const* part
         int c0 = 0;
         for (int i = 0; i < n; ++i) {
             const Tensor& p = *parts[i]->t;
-            LaunchScope sc(ctx->c, "k_copy", 0.0, 2.0 * dtype_size(p.dtype) * p.n * p.c * p.h * p.w);
+            LaunchScope sc(ctx->c, kname("k_copy", p.dtype), 0.0, 2.0 * dtype_size(p.dtype) * p.n * p.c * p.h * p.w);
             ZJAI_HIP(launch_copy(p.v, channel_view(y, c0, p.c)->v, p.dtype, p.n, p.c, p.h, p.w, ctx->c.stream));
             c0 += p.c;
         }
@@ -332,7 +332,7 @@ static int32_t eltwise(zjai_ctx* ctx, int op, zjai_tensor* x, const zjai_tensor*
             need(a.n == b.n && a.c == b.c && a.h == b.h && a.w == b.w && a.dtype == b.dtype, "shapes differ");
         }
         need(a.c % 4 == 0, "channel count must be a multiple of 4");
-        LaunchScope sc(ctx->c, "k_eltwise", 0.0, (op >= EL_ADD ? 3.0 : 2.0) * dtype_size(a.dtype) * a.c * a.h * a.w);
+        LaunchScope sc(ctx->c, kname("k_eltwise", a.dtype), 0.0, (op >= EL_ADD ? 3.0 : 2.0) * dtype_size(a.dtype) * a.c * a.h * a.w);
         ZJAI_HIP(launch_eltwise(op, a.v, s ? s->t->v : a.v, a.dtype, a.n, a.c, a.h, a.w, ctx->c.stream));
     });
 }
@@ -354,7 +354,7 @@ extern "C" int32_t zjai_pixel_shuffle(zjai_ctx* ctx, const zjai_tensor* x, int32
         const int co = a.c / (r * r);
         need(co % 4 == 0, "pixel_shuffle: output channels must be a multiple of 4");
         TensorP y = ctx->c.alloc(a.n, co, a.h * r, a.w * r, a.dtype);
-        LaunchScope sc(ctx->c, "k_pixel_shuffle", 0.0, 2.0 * dtype_size(a.dtype) * a.c * a.h * a.w);
+        LaunchScope sc(ctx->c, kname("k_pixel_shuffle", a.dtype), 0.0, 2.0 * dtype_size(a.dtype) * a.c * a.h * a.w);
         ZJAI_HIP(launch_pixel_shuffle(a.v, y->v, a.dtype, a.n, co, a.h, a.w, r, ctx->c.stream));
         *out = new zjai_tensor{y};
     });
@@ -372,7 +372,7 @@ extern "C" int32_t zjai_layer_norm_channels(zjai_ctx* ctx, const zjai_tensor* x,
         ZJAI_HIP(hipMemcpyAsync(d + a.c, bias, sizeof(float) * a.c, hipMemcpyHostToDevice, ctx->c.stream));
         TensorP y = ctx->c.alloc(a.n, a.c, a.h, a.w, a.dtype);
         {
-            LaunchScope sc(ctx->c, "k_layer_norm", 0.0, 2.0 * dtype_size(a.dtype) * a.c * a.h * a.w);
+            LaunchScope sc(ctx->c, kname("k_layer_norm", a.dtype), 0.0, 2.0 * dtype_size(a.dtype) * a.c * a.h * a.w);
             ZJAI_HIP(launch_layer_norm(a.v, y->v, a.dtype, a.n, a.c, a.h, a.w, d, d + a.c, ctx->c.stream));
         }
         ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
@@ -729,7 +729,7 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
             }
             TensorP by = c.alloc(N, 160, t0.latent_h, t0.latent_w, dt);
             {
-                LaunchScope sc(c, "k_planar_to_nhwc", 0.0, (4.0 + dtype_size(dt)) * N * 160 * t0.latent_h * t0.latent_w);
+                LaunchScope sc(c, kname("k_planar_to_nhwc", dt), 0.0, (4.0 + dtype_size(dt)) * N * 160 * t0.latent_h * t0.latent_w);
                 ZJAI_HIP(launch_planar_to_nhwc(pic->y_hat, 160, pic->lh, pic->lw, win, N, t0.latent_h, t0.latent_w,
                                                by->v, dt, c.stream));
             }
@@ -737,7 +737,7 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
             if (pic->net_uv) {
                 TensorP buv = c.alloc(N, 96, t0.latent_h, t0.latent_w, dt);
                 {
-                    LaunchScope sc(c, "k_planar_to_nhwc", 0.0, (4.0 + dtype_size(dt)) * N * 96 * t0.latent_h * t0.latent_w);
+                    LaunchScope sc(c, kname("k_planar_to_nhwc", dt), 0.0, (4.0 + dtype_size(dt)) * N * 96 * t0.latent_h * t0.latent_w);
                     ZJAI_HIP(launch_planar_to_nhwc(pic->uv_hat, 96, pic->lh, pic->lw, win, N, t0.latent_h,
                                                    t0.latent_w, buv->v, dt, c.stream));
                 }

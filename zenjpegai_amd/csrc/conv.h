@@ -35,6 +35,7 @@ struct ConvParams {
     long long w_bstride;
     const float* bias;
     int cin_g, cout_g, groups, nchunks, nblk_g, ntiles;
+    int gx, gy;  // spatial tile grid (set by the launcher)
     long long phase_stride;  // elements between phases (transposed conv)
     int pad_t, pad_l;
     int relu6_in;  // clamp(x, 0, 6) on load (ResAU's relu6)

@@ -197,19 +197,39 @@ conv_igemm(const ConvParams p) {
     constexpr int CK = 4 * VEC;
     constexpr int HALO_U = HY * HX * 4;
     constexpr int W_U = NB * NTAP * 64;
-    __shared__ u32x4 s_halo[HALO_U];
-    __shared__ u32x4 s_w[W_U];
+    // The output tile [TY * 16 positions][NB * 16 + 4 channels] (f32) reuses the same LDS after
+    // the K loop (the +4 pads rows against bank conflicts).
+    constexpr int OUT_LD = NB * 16 + 4;
+    constexpr int OUT_U = (TY * 16 * OUT_LD + 3) / 4;
+    constexpr int LDS_U = (HALO_U + W_U) > OUT_U ? (HALO_U + W_U) : OUT_U;
+    __shared__ u32x4 s_lds[LDS_U];
+    u32x4* s_halo = s_lds;
+    u32x4* s_w = s_lds + HALO_U;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wc = wave % WC, wp = wave / WC;
     const int col = lane & 15, grp = lane >> 4;
 
-    const int zz = TR ? (int)(blockIdx.z >> 2) : (int)blockIdx.z;
-    const int phase = TR ? (int)(blockIdx.z & 3) : 0;
-    const int bi = zz / p.ntiles, nt = zz - bi * p.ntiles;
+    // XCD-aware order. Workgroup ids are dealt round-robin to the 8 XCDs (id % 8), each with its
+    // own L2; id -> (xcd j, k-th block of that XCD) -> logical id j * share + k, so every XCD
+    // walks a contiguous logical range. Logical order is (batch, tile row, tile col, channel
+    // tile, phase) with the channel tiles and phases of one spatial tile consecutive: they read
+    // the same input halo, which then comes from L2 rather than HBM.
+    const int nz = p.ntiles * (TR ? 4 : 1);
+    const int total = p.gx * p.gy * p.N * nz;
+    const int bid = (int)blockIdx.x, xj = bid & 7, xk = bid >> 3;
+    const int q8 = total >> 3, r8 = total & 7;
+    const int lid = xj < r8 ? xj * (q8 + 1) + xk : r8 * (q8 + 1) + (xj - r8) * q8 + xk;
+    int rest = lid / nz;
+    const int zl = lid - rest * nz;
+    const int tx = rest % p.gx;
+    rest /= p.gx;
+    const int ty = rest % p.gy, bi = rest / p.gy;
+    const int phase = TR ? (zl & 3) : 0;
+    const int nt = TR ? (zl >> 2) : zl;
     const int gb = nt * NB;
     const int g = gb / p.nblk_g, nb0 = gb - g * p.nblk_g;
-    const int ox0 = blockIdx.x * 16, oy0 = blockIdx.y * TY;
+    const int ox0 = tx * 16, oy0 = ty * TY;
 
     int ntap = NTAP;
     int tdy[NTAP], tdx[NTAP];
@@ -279,6 +299,35 @@ conv_igemm(const ConvParams p) {
         }
     }
 
+    if (p.out_mode == OUT_NHWC && p.ps == 1) {
+        // Transpose the tile through LDS so that consecutive threads store consecutive channel
+        // quads of one position: every position's NB * 16 channels leave as one contiguous run
+        // (a lane's accumulator holds 4 channels of one position, 16 lanes apart per position).
+        __syncthreads();
+        float* so = reinterpret_cast<float*>(s_lds);
+#pragma unroll
+        for (int cf = 0; cf < CF; ++cf)
+#pragma unroll
+            for (int pf = 0; pf < PF; ++pf) {
+                float* d = so + ((wp * PF + pf) * 16 + col) * OUT_LD + (wc * CF + cf) * 16 + grp * 4;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) d[i] = acc[cf][pf][i];
+            }
+        __syncthreads();
+        constexpr int QP = NB * 4;
+        for (int u = tid; u < TY * 16 * QP; u += NT) {
+            const int pos = u / QP, cq = u - pos * QP;
+            const int r = pos >> 4, cx = pos & 15;
+            const int oy = TR ? 2 * (oy0 + r) + (phase >> 1) : oy0 + r;
+            const int ox = TR ? 2 * (ox0 + cx) + (phase & 1) : ox0 + cx;
+            const int ocl = nb0 * 16 + cq * 4;
+            if (oy >= p.OH || ox >= p.OW || ocl >= p.cout_g) continue;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + cq * 4);
+            epilogue_store<T>(p, bi, oy, ox, g * p.cout_g + ocl, min(4, p.cout_g - ocl), v);
+        }
+        return;
+    }
+
 #pragma unroll
     for (int cf = 0; cf < CF; ++cf) {
         const int ocl = (nb0 + wc * CF + cf) * 16 + grp * 4;
@@ -305,13 +354,18 @@ conv_igemm(const ConvParams p) {
 // Launch dispatch.
 // ---------------------------------------------------------------------------------------------
 template <typename T, int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF>
-static hipError_t go(const ConvParams& p, hipStream_t s) {
+static hipError_t go(const ConvParams& p0, hipStream_t s) {
     constexpr int TY = WP * PF;
+    ConvParams p = p0;
     const int gh = TR ? (p.OH + 1) / 2 : p.OH;
     const int gw = TR ? (p.OW + 1) / 2 : p.OW;
     if (p.ntiles != p.groups * p.nblk_g / (WC * CF) || p.N < 1 || p.N > MAXB) return hipErrorInvalidValue;
-    dim3 grid((gw + 15) / 16, (gh + TY - 1) / TY, p.N * p.ntiles * (TR ? 4 : 1));
-    hipLaunchKernelGGL((conv_igemm<T, KH, KW, S, TR, WC, WP, CF, PF>), grid, dim3(WC * WP * 64), 0, s, p);
+    p.gx = (gw + 15) / 16;
+    p.gy = (gh + TY - 1) / TY;
+    const long long total = (long long)p.gx * p.gy * p.N * p.ntiles * (TR ? 4 : 1);
+    if (total <= 0 || total > (1ll << 30)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((conv_igemm<T, KH, KW, S, TR, WC, WP, CF, PF>), dim3((unsigned)total),
+                       dim3(WC * WP * 64), 0, s, p);
     return hipGetLastError();
 }
 

@@ -248,7 +248,7 @@ struct Fwd {
     }
     TensorP layer_norm(const std::string& pfx, const TensorP& x) {
         TensorP y = ctx.alloc(x->n, x->c, x->h, x->w, x->dtype);
-        LaunchScope sc(ctx, "k_layer_norm", 0.0, 2.0 * dtype_size(x->dtype) * x->n * x->c * x->h * x->w);
+        LaunchScope sc(ctx, kname("k_layer_norm", x->dtype), 0.0, 2.0 * dtype_size(x->dtype) * x->n * x->c * x->h * x->w);
         ZJAI_HIP(launch_layer_norm(x->v, y->v, x->dtype, x->n, x->c, x->h, x->w, net.vec.at(pfx + ".weight"),
                                    net.vec.at(pfx + ".bias"), ctx.stream));
         return y;
@@ -275,7 +275,7 @@ struct Fwd {
         const Layer& dw = L(p + ".ffn.dwconv");
         TensorP f = ctx.alloc(u->n, hidden, u->h, u->w, u->dtype);
         {
-            LaunchScope sc(ctx, "k_depthwise3x3", 2.0 * 9 * 2 * hidden * u->n * u->h * u->w,
+            LaunchScope sc(ctx, kname("k_depthwise3x3", u->dtype), 2.0 * 9 * 2 * hidden * u->n * u->h * u->w,
                            (double)dtype_size(u->dtype) * 3 * hidden * u->n * u->h * u->w);
             ZJAI_HIP(launch_depthwise3x3(u->v, f->v, u->dtype, u->n, 2 * hidden, u->h, u->w, dw.dw_w, dw.bias,
                                          hidden, ctx.stream));
@@ -392,17 +392,17 @@ void secondary_forward(Context& ctx, const Net& net, const TensorP& y_luma, cons
     const double es = dtype_size(dt);
     TensorP cat = ctx.alloc(N, 256, lh, lw, dt);
     {
-        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * N * 160 * lh * lw);
+        LaunchScope sc(ctx, kname("k_copy", dt), 0.0, 2.0 * es * N * 160 * lh * lw);
         ZJAI_HIP(launch_copy(y_luma->v, cat->v, dt, N, 160, lh, lw, ctx.stream));
     }
     {
-        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * N * 96 * lh * lw);
+        LaunchScope sc(ctx, kname("k_copy", dt), 0.0, 2.0 * es * N * 96 * lh * lw);
         ZJAI_HIP(launch_copy(y_chroma->v, channel_view(cat, 160, 96)->v, dt, N, 96, lh, lw, ctx.stream));
     }
     TensorP x = ctx.alloc(N, 144, lh, lw, dt);
     f.conv("first_stage.conv1", cat, Epilogue{}, channel_view(x, 0, 48));
     {
-        LaunchScope sc(ctx, "k_copy", 0.0, 2.0 * es * N * 96 * lh * lw);
+        LaunchScope sc(ctx, kname("k_copy", dt), 0.0, 2.0 * es * N * 96 * lh * lw);
         ZJAI_HIP(launch_copy(y_chroma->v, channel_view(x, 48, 96)->v, dt, N, 96, lh, lw, ctx.stream));
     }
     cat.reset();

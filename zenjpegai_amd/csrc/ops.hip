@@ -5,6 +5,8 @@
 
 #include "ops.h"
 
+#include <algorithm>
+
 namespace zjai {
 
 // Decomposes a flat index over [N][h][w][q] (q = channel quads, fastest).
@@ -112,85 +114,122 @@ __global__ void k_eltwise(int op, View xv, View sv, int N, int C, int h, int w) 
 // ------------------------------------------------------------------------- depthwise 3x3
 // Per output element: acc = bias; for ky, kx ascending: acc = fma(w, x, acc), padding taps
 // included (src/nn/fast/depthwise.rs:40-73). Weights are stored transposed, [9][C].
+// One thread: 4 channels x DW_X consecutive output columns of one row, with a sliding 3-row x
+// (DW_X + 2)-column window of input vectors (lanes run over channels, so every load instruction
+// of a wave reads contiguous channel runs).
+constexpr int DW_X = 4;
+
 template <typename T>
-__global__ void k_depthwise3x3(View src, View dst, int N, int C, int h, int w, const float* wt,
-                               const float* bias, int elu_half) {
+__device__ __forceinline__ void dw_strip(const View& src, int b, int y, int x0, int h, int w,
+                                         int c0, const float* wt, int C, const float* bias,
+                                         f32x4 (&acc)[DW_X]) {
+    f32x4 wv[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) wv[t] = *(const f32x4*)(wt + t * C + c0);
+#pragma unroll
+    for (int j = 0; j < DW_X; ++j)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[j][k] = bias ? bias[c0 + k] : 0.0f;
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky) {
+        const int yy = y + ky - 1;
+        const bool row_ok = yy >= 0 && yy < h;
+        f32x4 win[DW_X + 2];
+#pragma unroll
+        for (int j = 0; j < DW_X + 2; ++j) {
+            const int xx = x0 + j - 1;
+            win[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (row_ok && xx >= 0 && xx < w) win[j] = load4<T>(at<T>(src, b, yy, xx, c0));
+        }
+        // Taps in (ky, kx) ascending order per output: acc = fma(w, x, acc).
+#pragma unroll
+        for (int j = 0; j < DW_X; ++j)
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[j][k] = fmaf(wv[ky * 3 + kx][k], win[j + kx][k], acc[j][k]);
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) k_depthwise3x3(View src, View dst, int N, int C, int h, int w,
+                                                      const float* wt, const float* bias, int elu_half) {
     const int cout = elu_half > 0 ? elu_half : C;
-    const int q = cout / 4;
+    const int q = cout / 4, wx = (w + DW_X - 1) / DW_X;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)N * h * w * q) return;
-    const Idx4 d = split(i, h, w, q);
-    const int npass = elu_half > 0 ? 2 : 1;
-    f32x4 res[2];
-    for (int pass = 0; pass < npass; ++pass) {
-        const int c0 = d.cq * 4 + pass * elu_half;
-        f32x4 acc;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) acc[k] = bias ? bias[c0 + k] : 0.0f;
-#pragma unroll
-        for (int ky = 0; ky < 3; ++ky) {
-            const int yy = d.y + ky - 1;
-#pragma unroll
-            for (int kx = 0; kx < 3; ++kx) {
-                const int xx = d.x + kx - 1;
-                f32x4 xv = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (yy >= 0 && yy < h && xx >= 0 && xx < w) xv = load4<T>(at<T>(src, d.b, yy, xx, c0));
-                const f32x4 wv = *(const f32x4*)(wt + (ky * 3 + kx) * C + c0);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) acc[k] = fmaf(wv[k], xv[k], acc[k]);
-            }
-        }
-        res[pass] = acc;
-    }
-    f32x4 out = res[0];
+    if (i >= (long long)N * h * wx * q) return;
+    const Idx4 d = split(i, h, wx, q);
+    const int x0 = d.x * DW_X;
+    f32x4 a[DW_X];
+    dw_strip<T>(src, d.b, d.y, x0, h, w, d.cq * 4, wt, C, bias, a);
     if (elu_half > 0) {
+        f32x4 g[DW_X];
+        dw_strip<T>(src, d.b, d.y, x0, h, w, d.cq * 4 + elu_half, wt, C, bias, g);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float a = res[0][k];
-            const float e = cephes_exp(a) - 1.0f;
-            const float elu = a > 0.0f ? a : e;
-            out[k] = elu * res[1][k];
-        }
+        for (int j = 0; j < DW_X; ++j)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float v = a[j][k];
+                const float e = cephes_exp(v) - 1.0f;
+                const float elu = v > 0.0f ? v : e;
+                a[j][k] = elu * g[j][k];
+            }
     }
-    store4<T>(at_mut<T>(dst, d.b, d.y, d.x, d.cq * 4), out);
+#pragma unroll
+    for (int j = 0; j < DW_X; ++j)
+        if (x0 + j < w) store4<T>(at_mut<T>(dst, d.b, d.y, x0 + j, d.cq * 4), a[j]);
 }
 
 // ------------------------------------------------------------------------------ layer norm
 // `layer_norm_channels` (src/nn/fast/math.rs:423-448): f64 sums over channels in order,
 // (x - mean) / sqrt(var + 1e-5) * w + b with f32 operations.
+// A block stages LN_P positions x C channels in LDS with coalesced 16-byte loads (rows padded by
+// one float against bank conflicts); one thread per position then sums its row in channel
+// order, and all threads write the normalised values back coalesced.
 template <typename T>
-__global__ void k_layer_norm(View src, View dst, int N, int C, int h, int w, const float* wt,
-                             const float* bs) {
-    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)N * h * w) return;
-    const Idx4 d = split(i, h, w, 1);
-    const T* p = at<T>(src, d.b, d.y, d.x, 0);
-    double mean = 0.0;
-    for (int c = 0; c < C; c += 4) {
-        const f32x4 v = load4<T>(p + c);
-        mean += (double)v[0]; mean += (double)v[1]; mean += (double)v[2]; mean += (double)v[3];
+__global__ void __launch_bounds__(256) k_layer_norm(View src, View dst, int N, int C, int h, int w,
+                                                    const float* wt, const float* bs, int P) {
+    extern __shared__ float s_ln[];  // [P][C + 1], then mean[P], den[P]
+    const int ld = C + 1, q = C / 4;
+    float* s_m = s_ln + P * ld;
+    float* s_d = s_m + P;
+    const long long npos = (long long)N * h * w, p0 = (long long)blockIdx.x * P;
+    for (int u = threadIdx.x; u < P * q; u += blockDim.x) {
+        const int pl = u / q, cq = u - pl * q;
+        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (p0 + pl < npos) {
+            const Idx4 d = split(p0 + pl, h, w, 1);
+            v = load4<T>(at<T>(src, d.b, d.y, d.x, cq * 4));
+        }
+        float* r = s_ln + pl * ld + cq * 4;
+        r[0] = v[0]; r[1] = v[1]; r[2] = v[2]; r[3] = v[3];
     }
-    mean /= (double)C;
-    double var = 0.0;
-    for (int c = 0; c < C; c += 4) {
-        const f32x4 v = load4<T>(p + c);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) { const double e = (double)v[k] - mean; var = var + e * e; }
+    __syncthreads();
+    if ((int)threadIdx.x < P) {
+        const float* r = s_ln + threadIdx.x * ld;
+        double mean = 0.0;
+        for (int c = 0; c < C; ++c) mean += (double)r[c];
+        mean /= (double)C;
+        double var = 0.0;
+        for (int c = 0; c < C; ++c) { const double e = (double)r[c] - mean; var = var + e * e; }
+        s_m[threadIdx.x] = (float)mean;
+        s_d[threadIdx.x] = sqrtf((float)(var / (double)C) + 1e-5f);
     }
-    const float m32 = (float)mean;
-    const float den = sqrtf((float)(var / (double)C) + 1e-5f);
-    T* o = at_mut<T>(dst, d.b, d.y, d.x, 0);
-    for (int c = 0; c < C; c += 4) {
-        const f32x4 v = load4<T>(p + c);
-        f32x4 r;
+    __syncthreads();
+    for (int u = threadIdx.x; u < P * q; u += blockDim.x) {
+        const int pl = u / q, cq = u - pl * q;
+        if (p0 + pl >= npos) continue;
+        const Idx4 d = split(p0 + pl, h, w, 1);
+        const float* r = s_ln + pl * ld + cq * 4;
+        f32x4 o;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            float e = v[k] - m32;
-            e = e / den;
-            e = e * wt[c + k];
-            r[k] = e + bs[c + k];
+            float e = r[k] - s_m[pl];
+            e = e / s_d[pl];
+            e = e * wt[cq * 4 + k];
+            o[k] = e + bs[cq * 4 + k];
         }
-        store4<T>(o + c, r);
+        store4<T>(at_mut<T>(dst, d.b, d.y, d.x, cq * 4), o);
     }
 }
 
@@ -377,7 +416,7 @@ hipError_t launch_depthwise3x3(View src, View dst, int dtype, int N, int C, int 
                                const float* weight, const float* bias, int elu_half,
                                hipStream_t s) {
     const int cout = elu_half > 0 ? elu_half : C;
-    const long long n = (long long)N * h * w * (cout / 4);
+    const long long n = (long long)N * h * ((w + DW_X - 1) / DW_X) * (cout / 4);
     if (n == 0) return hipSuccess;
     ZJAI_DISPATCH(dtype, k_depthwise3x3, <<<grid_for(n), 256, 0, s>>>(src, dst, N, C, h, w, weight, bias, elu_half))
     return hipGetLastError();
@@ -387,7 +426,12 @@ hipError_t launch_layer_norm(View src, View dst, int dtype, int N, int C, int h,
                              const float* weight, const float* bias, hipStream_t s) {
     const long long n = (long long)N * h * w;
     if (n == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_layer_norm, <<<grid_for(n), 256, 0, s>>>(src, dst, N, C, h, w, weight, bias))
+    // Positions per block: as many as fit in 32 KiB of LDS, at most 64.
+    const int P = std::max(1, std::min(64, 8192 / (C + 1)));
+    const size_t lds = sizeof(float) * ((size_t)P * (C + 1) + 2 * P);
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    const dim3 g((unsigned)((n + P - 1) / P));
+    ZJAI_DISPATCH(dtype, k_layer_norm, <<<g, 256, lds, s>>>(src, dst, N, C, h, w, weight, bias, P))
     return hipGetLastError();
 }
 

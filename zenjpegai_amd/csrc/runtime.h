@@ -171,6 +171,11 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
                      const TensorP& dst = nullptr, const PlaneOut* plane = nullptr);
 
 std::string conv_kernel_name(int kind, int dtype, TileCfg c);
+// "<base><T>" as profilers print the templated kernels of ops.hip.
+inline std::string kname(const char* base, int dtype) {
+    static const char* ty[] = {"float", "_Float16", "__bf16"};
+    return std::string(base) + "<" + ty[dtype] + ">";
+}
 
 // Channel attention of qkv (3*dim channels, `heads` heads, device temperature) folded with the
 // projection layer `proj` (a dense 1x1 dim -> dim layer holding its f32 weight): returns, per

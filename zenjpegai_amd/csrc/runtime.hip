@@ -400,7 +400,7 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
     if (L.depthwise) {
         if (e.act || e.res || ps != 1 || e.relu6_in || plane || e.w_batch)
             throw Error(ZJAI_E_UNSUPPORTED, "depthwise: fused epilogue");
-        LaunchScope sc(ctx, "k_depthwise3x3", 2.0 * 9 * N * L.cin * x->h * x->w, 2.0 * es * N * L.cin * x->h * x->w);
+        LaunchScope sc(ctx, kname("k_depthwise3x3", L.dtype), 2.0 * 9 * N * L.cin * x->h * x->w, 2.0 * es * N * L.cin * x->h * x->w);
         ZJAI_HIP(launch_depthwise3x3(x->v, y->v, L.dtype, N, L.cin, x->h, x->w, L.dw_w, L.bias, 0, ctx.stream));
         return y;
     }
@@ -499,7 +499,7 @@ std::shared_ptr<void> attention_fold(Context& ctx, const TensorP& qkv, int heads
     if (proj.nblk_g * 16 != dim || proj.nchunks * CK != dim)  // padded rows / columns stay zero
         ZJAI_HIP(hipMemsetAsync(wfold, 0, proj.wpk_bytes * N, ctx.stream));
     {
-        LaunchScope sc(ctx, "k_attention_gram", 2.0 * N * total * n, es * N * 2 * dim * n + 4.0 * N * nchunk * total);
+        LaunchScope sc(ctx, kname("k_attention_gram", qkv->dtype), 2.0 * N * total * n, es * N * 2 * dim * n + 4.0 * N * nchunk * total);
         ZJAI_HIP(launch_attention_gram(qkv->v, qkv->dtype, N, dim, heads, qkv->h, qkv->w, partial, ctx.stream));
     }
     {
@@ -507,7 +507,7 @@ std::shared_ptr<void> attention_fold(Context& ctx, const TensorP& qkv, int heads
         ZJAI_HIP(launch_attention_softmax(partial, N, nchunk, dim, heads, temperature, attn, ctx.stream));
     }
     {
-        LaunchScope sc(ctx, "k_attention_fold", 2.0 * N * dim * dim * c, 4.0 * dim * dim + es * N * dim * dim);
+        LaunchScope sc(ctx, kname("k_attention_fold", proj.dtype), 2.0 * N * dim * dim * c, 4.0 * dim * dim + es * N * dim * dim);
         ZJAI_HIP(launch_attention_fold(proj.w_f32, attn, N, dim, heads, proj.dtype, proj.nblk_g, wfold,
                                        *w_bstride, ctx.stream));
     }
