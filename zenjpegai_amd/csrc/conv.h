@@ -69,4 +69,10 @@ enum ConvKind : int { CK_1x1 = 0, CK_2x2 = 1, CK_3x3 = 2, CK_3x3_S2 = 3, CK_T3 =
 hipError_t launch_conv(int kind, int dtype, TileCfg cfg, const ConvParams& p, hipStream_t s);
 bool conv_cfg_supported(int kind, int dtype, TileCfg cfg);
 
+// Stride-2 transposed conv with cout <= 8 on the vector ALUs (coutp = cout rounded up to 1, 2, 4
+// or 8); wn is [phase][tap][cin][coutp] f32. Uses p's input view, output geometry, tap tables,
+// bias and epilogue fields.
+hipError_t launch_convT_narrow(int dtype, int coutp, const ConvParams& p, const float* wn, int cin,
+                               hipStream_t s);
+
 }  // namespace zjai

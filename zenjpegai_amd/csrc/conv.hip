@@ -351,6 +351,133 @@ conv_igemm(const ConvParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Narrow transposed convolution (stride 2, at most 8 output channels): the last synthesis layers
+// (HOP luma 128 -> 1, chroma 64 -> 8). An MFMA tile would leave at least half of its 16 or 32
+// output rows idle, so these run on the vector ALUs: one thread per phase-grid position (y', x')
+// computes its 2x2 output phases for every output channel. Per output: acc = bias, then for each
+// input channel ascending and each reaching tap in (ky, kx) order acc = fma(w, x, acc) -- the
+// reference's convT order (src/nn/reference.rs:155-236), so in f32 the result equals the oracle
+// bit for bit. Per chunk of 16 input channels a workgroup stages its (TYN + 2) x (TXN + 2) input
+// halo in LDS channel-major, so consecutive threads read consecutive words.
+// wn: [phase][tap][cin][COUT] f32 (weights already rounded to the storage type).
+template <typename T, int COUT>
+__global__ void __launch_bounds__(256)
+k_convT_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
+    constexpr int TXN = 64, TYN = 4, HXN = TXN + 2, HYN = TYN + 2, CKN = 16;
+    constexpr int HP = HXN * HYN;
+    __shared__ float s_x[CKN * HP];
+    __shared__ float s_w[4 * 4 * CKN * COUT];
+    const int gw = (p.OW + 1) / 2, gh = (p.OH + 1) / 2;
+    const int gx = (gw + TXN - 1) / TXN, gy = (gh + TYN - 1) / TYN;
+    int bid = (int)blockIdx.x;
+    const int tx = bid % gx;
+    bid /= gx;
+    const int ty = bid % gy, bi = bid / gy;
+    const int tid = threadIdx.x, r = tid / TXN, c = tid % TXN;
+    const int y0 = ty * TYN, x0 = tx * TXN;
+    const T* xg = (const T*)p.x.p + (long long)bi * p.x.bstride;
+
+    int nt[4], tdy[4][4], tdx[4][4];
+#pragma unroll
+    for (int ph = 0; ph < 4; ++ph) {
+        nt[ph] = p.ntaps[ph];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            tdy[ph][t] = p.tap_dy[ph][t];
+            tdx[ph][t] = p.tap_dx[ph][t];
+        }
+    }
+    float acc[4][COUT];
+#pragma unroll
+    for (int ph = 0; ph < 4; ++ph)
+#pragma unroll
+        for (int oc = 0; oc < COUT; ++oc) acc[ph][oc] = (p.bias && oc < p.cout_g) ? p.bias[oc] : 0.0f;
+
+    for (int c0 = 0; c0 < cin; c0 += CKN) {
+        __syncthreads();
+        // Halo: pixel (hy, hx) <- input (y0 - 1 + hy, x0 - 1 + hx); 4 channels per thread step.
+        for (int u = tid; u < HP * (CKN / 4); u += 256) {
+            const int pix = u / (CKN / 4), q = u - pix * (CKN / 4);
+            const int hy = pix / HXN, hx = pix - hy * HXN;
+            const int iy = y0 - 1 + hy, ix = x0 - 1 + hx, ch = c0 + 4 * q;
+            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (iy >= 0 && iy < p.H && ix >= 0 && ix < p.W && ch < cin) {
+                v = load4<T>(xg + (long long)iy * p.x.row + (long long)ix * p.x.cs + p.x.c_off + ch);
+                if (p.relu6_in) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float e = v[i];
+                        e = e < 0.0f ? 0.0f : e;
+                        v[i] = e > 6.0f ? 6.0f : e;
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s_x[(4 * q + i) * HP + pix] = v[i];
+        }
+        for (int u = tid; u < 4 * 4 * CKN * COUT; u += 256) {
+            const int oc = u % COUT, k = (u / COUT) % CKN, pt = u / (COUT * CKN);
+            s_w[u] = c0 + k < cin ? wn[((long long)pt * cin + c0 + k) * COUT + oc] : 0.0f;
+        }
+        __syncthreads();
+        const int kn = min(CKN, cin - c0);
+        for (int k = 0; k < kn; ++k) {
+            const float* sx = s_x + k * HP;
+#pragma unroll
+            for (int ph = 0; ph < 4; ++ph)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    if (t >= nt[ph]) break;
+                    const float x = sx[(r + tdy[ph][t]) * HXN + c + tdx[ph][t]];
+                    const float* w = s_w + ((ph * 4 + t) * CKN + k) * COUT;
+#pragma unroll
+                    for (int oc = 0; oc < COUT; ++oc) acc[ph][oc] = fmaf(w[oc], x, acc[ph][oc]);
+                }
+        }
+    }
+    const int yq = y0 + r, xq = x0 + c;
+#pragma unroll
+    for (int ph = 0; ph < 4; ++ph) {
+        const int oy = 2 * yq + (ph >> 1), ox = 2 * xq + (ph & 1);
+        if (oy >= p.OH || ox >= p.OW) continue;
+#pragma unroll
+        for (int oc0 = 0; oc0 < COUT; oc0 += 4) {
+            if (oc0 >= p.cout_g) break;
+            f32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = oc0 + i < COUT ? acc[ph][min(oc0 + i, COUT - 1)] : 0.0f;
+            epilogue_store<T>(p, bi, oy, ox, oc0, min(4, p.cout_g - oc0), v);
+        }
+    }
+}
+
+template <typename T>
+static hipError_t go_narrow(int coutp, const ConvParams& p, const float* wn, int cin, hipStream_t s) {
+    const int gw = (p.OW + 1) / 2, gh = (p.OH + 1) / 2;
+    const long long blocks = (long long)((gw + 63) / 64) * ((gh + 3) / 4) * p.N;
+    if (blocks <= 0 || blocks > (1ll << 30) || p.N < 1 || p.N > MAXB) return hipErrorInvalidValue;
+    const dim3 g((unsigned)blocks);
+    switch (coutp) {
+        case 1: hipLaunchKernelGGL((k_convT_narrow<T, 1>), g, dim3(256), 0, s, p, wn, cin); break;
+        case 2: hipLaunchKernelGGL((k_convT_narrow<T, 2>), g, dim3(256), 0, s, p, wn, cin); break;
+        case 4: hipLaunchKernelGGL((k_convT_narrow<T, 4>), g, dim3(256), 0, s, p, wn, cin); break;
+        case 8: hipLaunchKernelGGL((k_convT_narrow<T, 8>), g, dim3(256), 0, s, p, wn, cin); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_convT_narrow(int dtype, int coutp, const ConvParams& p, const float* wn, int cin,
+                               hipStream_t s) {
+    switch (dtype) {
+        case DT_F32: return go_narrow<float>(coutp, p, wn, cin, s);
+        case DT_F16: return go_narrow<_Float16>(coutp, p, wn, cin, s);
+        case DT_BF16: return go_narrow<__bf16>(coutp, p, wn, cin, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------------------------
 // Launch dispatch.
 // ---------------------------------------------------------------------------------------------
 template <typename T, int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF>

@@ -133,6 +133,8 @@ struct Layer {
     float* bias = nullptr;     // f32 [cout] or null
     float* dw_w = nullptr;     // depthwise [9][C]
     float* w_f32 = nullptr;    // f32 [cout][cin] copy (1x1 only, for attention folding)
+    float* wn = nullptr;       // narrow transposed conv: [phase][tap][cin][coutp] f32
+    int coutp = 0;             // cout rounded up to 1, 2, 4 or 8 (narrow transposed conv)
     size_t wpk_bytes = 0;
     ~Layer();
 

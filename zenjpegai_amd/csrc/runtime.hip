@@ -181,6 +181,33 @@ static uint16_t f32_to_bf16_bits(float v) {
     return (uint16_t)(r >> 16);
 }
 
+// The f32 value of a storage-dtype weight (f16 / bf16 upcasts are exact).
+static float storage_value(float v, int dtype) {
+    if (dtype == DT_F32) return v;
+    uint32_t b;
+    if (dtype == DT_BF16) {
+        b = (uint32_t)f32_to_bf16_bits(v) << 16;
+    } else {
+        const uint32_t h = f32_to_f16_bits(v), sign = (h & 0x8000u) << 16;
+        const uint32_t e = (h >> 10) & 0x1f, m = h & 0x3ff;
+        if (e == 31) {
+            b = sign | 0x7f800000u | (m << 13);
+        } else if (e) {
+            b = sign | ((e + 112) << 23) | (m << 13);
+        } else if (!m) {
+            b = sign;
+        } else {  // subnormal half: normalise
+            int sh = 0;
+            uint32_t mm = m;
+            while (!(mm & 0x400)) { mm <<= 1; ++sh; }
+            b = sign | ((uint32_t)(113 - sh) << 23) | ((mm & 0x3ff) << 13);
+        }
+    }
+    float f;
+    std::memcpy(&f, &b, 4);
+    return f;
+}
+
 // Converts an f32 staging vector to the storage dtype and uploads it.
 static void* upload_as(Context& ctx, const std::vector<float>& host, int dtype, size_t* bytes_out) {
     const size_t n = host.size();
@@ -213,6 +240,7 @@ Layer::~Layer() {
     if (bias) (void)hipFree(bias);
     if (dw_w) (void)hipFree(dw_w);
     if (w_f32) (void)hipFree(w_f32);
+    if (wn) (void)hipFree(wn);
 }
 
 void Layer::out_size(int h, int w, int* oh, int* ow) const {
@@ -353,6 +381,25 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
     }
     L->wpk = upload_as(ctx, pk, dtype, &L->wpk_bytes);
     if (bias) L->bias = upload_f32(bias, cout);
+    if (cout <= 8) {
+        // Narrow layers run on the vector ALUs (launch_convT_narrow) from an f32 copy of the
+        // storage-rounded weights, [phase][tap][cin][coutp].
+        L->coutp = cout <= 1 ? 1 : cout <= 2 ? 2 : cout <= 4 ? 4 : 8;
+        std::vector<float> wn((size_t)16 * cin * L->coutp, 0.0f);
+        for (int ph = 0; ph < 4; ++ph) {
+            const int py = ph >> 1, px = ph & 1;
+            int t = 0;
+            for (int a = 0; a < nky[py]; ++a)
+                for (int b = 0; b < nky[px]; ++b, ++t) {
+                    const int ky = ky_list[py][a], kx = ky_list[px][b];
+                    for (int ic = 0; ic < cin; ++ic)
+                        for (int oc = 0; oc < cout; ++oc)
+                            wn[((size_t)(ph * 4 + t) * cin + ic) * L->coutp + oc] =
+                                storage_value(weight[(((size_t)ic * cout + oc) * k + ky) * k + kx], dtype);
+                }
+        }
+        L->wn = upload_f32(wn.data(), wn.size());
+    }
     return L;
 }
 
@@ -474,6 +521,14 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
                    (double)L.wpk_bytes * (e.w_batch ? N : 1);
     if (e.r1) bytes += es * N * (double)L.cout * OH * OW;
     if (e.r2) bytes += es * N * (double)L.cout * OH * OW;
+    if (L.wn && !e.w_batch) {
+        static const char* ty[] = {"float", "_Float16", "__bf16"};
+        char name[64];
+        snprintf(name, sizeof name, "k_convT_narrow<%s, %d>", ty[L.dtype], L.coutp);
+        LaunchScope sc(ctx, name, 2.0 * macs, bytes);
+        ZJAI_HIP(launch_convT_narrow(L.dtype, L.coutp, p, L.wn, L.cin, ctx.stream));
+        return y;
+    }
     LaunchScope sc(ctx, conv_kernel_name(L.kind, L.dtype, L.cfg), 2.0 * macs, bytes);
     ZJAI_HIP(launch_conv(L.kind, L.dtype, L.cfg, p, ctx.stream));
     return y;
