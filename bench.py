@@ -40,7 +40,7 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_workload(name, eng):
+def make_workload(name, eng, lanes=1):
     from zenjpegai_amd import model, synth
     if name == "cfg5":
         h, w, op, sv, sh, bits = 2160, 3840, "hop", 2, 2, 10
@@ -62,7 +62,7 @@ def make_workload(name, eng):
         puv = synth.random_params(op, "uv", seed=1)
         sec = model.SynthesisSecondary.load(puv, op, eng)
         uvl = synth.latent(1, f"{name}/uv", 96, lh, lw)
-    pic = model.Picture(eng, prim, sec, lh, lw, h, w, tiles, sv, sh, bit_depth=bits)
+    pic = model.Picture(eng, prim, sec, lh, lw, h, w, tiles, sv, sh, bit_depth=bits, lanes=lanes)
     pic.upload(y, uvl)
     return pic, dict(h=h, w=w, op=op, tiles=len(tiles), bits=bits, sv=sv, sh=sh,
                      latent=(lh, lw), py=py, y=y, uvl=uvl, puv=puv, tile_list=tiles)
@@ -80,9 +80,14 @@ def time_steps(eng, pic, steps, warmup):
 
 
 def profile_step(eng, pic):
+    """One step on a single stream with HIP events around every launch (concurrent lanes would
+    overlap kernels and inflate each one's event-measured duration)."""
+    lanes = pic.lanes
+    pic.set_lanes(1)
     eng.profile_begin()
     pic.run()
     recs = eng.profile_end()
+    pic.set_lanes(lanes)
     by = {}
     for name, flops, nbytes, ms in recs:
         d = by.setdefault(name, {"count": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
@@ -137,6 +142,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="cfg5", choices=["cfg5", "cfg4"])
     ap.add_argument("--precision", default="f32", choices=["f32", "f16", "bf16"])
+    ap.add_argument("--lanes", type=int, default=4,
+                    help="concurrent streams the picture's tile batches run on (1 = one stream)")
     ap.add_argument("--no-extra", action="store_true", help="skip the extra precision / cfg4 runs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--profile-out", default=None, help="write the per-kernel profile (JSON)")
@@ -167,7 +174,7 @@ def main():
 
     eng = nn.Engine(0, args.precision)
     log(f"[bench] building workload {args.workload} ({args.precision})")
-    pic, info = make_workload(args.workload, eng)
+    pic, info = make_workload(args.workload, eng, args.lanes)
     log(f"[bench] {info['tiles']} tiles; warmup {args.warmup}, timing {args.steps} steps")
     ms = time_steps(eng, pic, args.steps, args.warmup)
     pixels = info["h"] * info["w"]
@@ -211,7 +218,7 @@ def main():
             if prec == args.precision:
                 continue
             e2 = nn.Engine(0, prec)
-            p2, _ = make_workload(args.workload, e2)
+            p2, _ = make_workload(args.workload, e2, args.lanes)
             ms2 = time_steps(e2, p2, args.steps, args.warmup)
             pr2 = profile_step(e2, p2)
             cv = {k: d for k, d in pr2.items() if k.startswith("conv_igemm")}
@@ -222,7 +229,7 @@ def main():
             del p2, e2
         if args.workload != "cfg4":
             e3 = nn.Engine(0, args.precision)
-            p3, i3 = make_workload("cfg4", e3)
+            p3, i3 = make_workload("cfg4", e3, args.lanes)
             ms3 = time_steps(e3, p3, max(args.steps, 10), args.warmup)
             extra[f"cfg4_sop_1mp_{args.precision}_mpix_s"] = round(i3["h"] * i3["w"] / (ms3 / 1e3) / 1e6, 3)
             log(f"[bench] cfg4: {ms3:.3f} ms/step")

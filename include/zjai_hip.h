@@ -237,8 +237,14 @@ ZJAI_API int32_t zjai_picture_destroy(zjai_picture* pic);
 /* Uploads the decoded latents once (planar f32; uv_hat may be NULL without net_uv). */
 ZJAI_API int32_t zjai_picture_upload(zjai_ctx* ctx, zjai_picture* pic, const float* y_hat,
                             const float* uv_hat);
-/* Enqueues every tile on the context's stream (asynchronous; latents must be uploaded). */
+/* Runs every tile, on the context's stream or spread over lanes (see zjai_picture_set_lanes),
+ * and waits for the picture (latents must be uploaded). */
 ZJAI_API int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic);
+/* Runs the picture's tile batches on `lanes` (1..8) concurrent streams of the context, each with
+ * its own buffer pool; 1 (the default) keeps everything on the context's stream. Mirrors the
+ * reference's tile-parallel synthesis (rayon over tiles, src/decoder/reconstruct.rs:379-464):
+ * tiles are independent and write disjoint core rectangles. */
+ZJAI_API int32_t zjai_picture_set_lanes(zjai_ctx* ctx, zjai_picture* pic, int32_t lanes);
 /* Copies the planes out (synchronises): Y out_h*out_w, U/V ceil(out_h/sv)*ceil(out_w/sh)
  * samples each, as float (bit_depth 0) or uint16. u/v may be NULL without net_uv. */
 ZJAI_API int32_t zjai_picture_download(zjai_ctx* ctx, zjai_picture* pic, void* y, void* u, void* v);

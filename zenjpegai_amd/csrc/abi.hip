@@ -611,12 +611,15 @@ struct zjai_picture {
     int lh = 0, lw = 0, height = 0, width = 0, sv = 1, sh = 1, out_h = 0, out_w = 0, bit_depth = 0;
     std::vector<zjai_tile> tiles;
     std::vector<std::vector<int>> batches;  // tile indices of equal image size, at most MAXB each
+    int lanes = 1;            // tile batches run on this many concurrent streams
+    std::vector<hipEvent_t> lane_ev;  // join events, one per lane
     float* y_hat = nullptr;   // device planar [160][lh][lw]
     float* uv_hat = nullptr;  // device planar [96][lh][lw]
     void* out_y = nullptr;    // device planes
     void* out_uv = nullptr;   // [2][ch][cw]
     bool uploaded = false;
     ~zjai_picture() {
+        for (hipEvent_t e : lane_ev) (void)hipEventDestroy(e);
         if (y_hat) (void)hipFree(y_hat);
         if (uv_hat) (void)hipFree(uv_hat);
         if (out_y) (void)hipFree(out_y);
@@ -700,12 +703,25 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
     if (!ctx || !pic) return ZJAI_E_INVALID_ARGUMENT;
     return guard(ctx, [&] {
         need(pic->uploaded, "latents not uploaded");
-        Context& c = ctx->c;
+        Context& root = ctx->c;
         const int dt = pic->net_y->dtype;
-        ZJAI_HIP(hipEventRecord(c.ev0, c.stream));
+        ZJAI_HIP(hipEventRecord(root.ev0, root.stream));
         // Tiles of one image size share every layer shape: run them as one batch of up to MAXB
-        // (each launch then covers all of them).
-        for (const std::vector<int>& group : pic->batches) {
+        // (each launch then covers all of them). Batches are independent (disjoint core
+        // rectangles of the output planes, read-only latents), so with lanes > 1 batch i runs
+        // on lane i % lanes, concurrently with the others; the root stream waits for all lanes.
+        const int nl = std::min<int>(pic->lanes, (int)pic->batches.size());
+        while ((int)pic->lane_ev.size() < nl) {
+            hipEvent_t e;
+            ZJAI_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+            pic->lane_ev.push_back(e);
+        }
+        if (nl > 1) {
+            for (int i = 0; i < nl; ++i) ZJAI_HIP(hipStreamWaitEvent(root.lane(i).stream, root.ev0, 0));
+        }
+        for (size_t bidx = 0; bidx < pic->batches.size(); ++bidx) {
+            const std::vector<int>& group = pic->batches[bidx];
+            Context& c = nl > 1 ? root.lane((int)bidx % nl) : root;
             c.check_stop();
             const zjai_tile& t0 = pic->tiles[group[0]];
             const int N = (int)group.size();
@@ -751,10 +767,21 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
                 secondary_forward(c, *pic->net_uv, by, buv, t0.image_h, t0.image_w, pu);
             }
         }
-        ZJAI_HIP(hipEventRecord(c.ev1, c.stream));
-        ZJAI_HIP(hipEventSynchronize(c.ev1));
-        ZJAI_HIP(hipEventElapsedTime(&c.last_ms, c.ev0, c.ev1));
+        if (nl > 1) {
+            for (int i = 0; i < nl; ++i) {
+                ZJAI_HIP(hipEventRecord(pic->lane_ev[i], root.lane(i).stream));
+                ZJAI_HIP(hipStreamWaitEvent(root.stream, pic->lane_ev[i], 0));
+            }
+        }
+        ZJAI_HIP(hipEventRecord(root.ev1, root.stream));
+        ZJAI_HIP(hipEventSynchronize(root.ev1));
+        ZJAI_HIP(hipEventElapsedTime(&root.last_ms, root.ev0, root.ev1));
     });
+}
+
+extern "C" int32_t zjai_picture_set_lanes(zjai_ctx* ctx, zjai_picture* pic, int32_t lanes) {
+    if (!ctx || !pic || lanes < 1 || lanes > MAXB) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] { pic->lanes = lanes; });
 }
 
 extern "C" int32_t zjai_picture_download(zjai_ctx* ctx, zjai_picture* pic, void* y, void* u, void* v) {

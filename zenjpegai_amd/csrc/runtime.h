@@ -92,6 +92,16 @@ struct Context {
     std::vector<hipEvent_t> ev_pool;
     size_t ev_used = 0;
 
+    // Lanes: sub-contexts on the same device, each with its own stream and buffer pool (a pool
+    // block is only reused in the stream order of the lane that freed it). Independent work --
+    // the tile batches of a picture -- runs on several lanes at once so that one batch's kernels
+    // fill the tail of another's. Launch counts, profiling and the stop flag stay with the root.
+    Context* root = nullptr;
+    bool owns_stream = false;
+    std::vector<std::unique_ptr<Context>> lanes;
+    Context& lane(int i);
+    Context& top() { return root ? *root : *this; }
+
     TensorP alloc(int n, int c, int h, int w, int dtype);
     void check_stop();
     hipEvent_t take_event();

@@ -89,10 +89,25 @@ TensorP Context::alloc(int n, int c, int h, int w, int dtype) {
 }
 
 void Context::check_stop() {
-    if (stop) throw Error(ZJAI_E_CANCELLED, "cancelled");
+    if (top().stop) throw Error(ZJAI_E_CANCELLED, "cancelled");
+}
+
+Context& Context::lane(int i) {
+    if (root) return root->lane(i);
+    while ((int)lanes.size() <= i) {
+        auto l = std::make_unique<Context>();
+        l->root = this;
+        l->device = device;
+        ZJAI_HIP(hipSetDevice(device));
+        ZJAI_HIP(hipStreamCreateWithFlags(&l->stream, hipStreamNonBlocking));
+        l->owns_stream = true;
+        lanes.push_back(std::move(l));
+    }
+    return *lanes[i];
 }
 
 hipEvent_t Context::take_event() {
+    if (root) return root->take_event();
     if (ev_used == ev_pool.size()) {
         hipEvent_t e;
         ZJAI_HIP(hipEventCreate(&e));
@@ -102,25 +117,31 @@ hipEvent_t Context::take_event() {
 }
 
 Context::~Context() {
+    lanes.clear();
+    if (owns_stream && stream) {
+        (void)hipStreamSynchronize(stream);
+        (void)hipStreamDestroy(stream);
+    }
     for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
 }
 
 LaunchScope::LaunchScope(Context& c, const std::string& name, double flops, double bytes) : c_(c) {
-    ++c_.launches;
-    if (!c_.profiling) return;
+    Context& t = c_.top();
+    ++t.launches;
+    if (!t.profiling) return;
     ProfRec r;
     r.name = name;
     r.flops = flops;
     r.bytes = bytes;
-    r.a = c_.take_event();
-    r.b = c_.take_event();
+    r.a = t.take_event();
+    r.b = t.take_event();
     ZJAI_HIP(hipEventRecord(r.a, c_.stream));
-    idx_ = (long)c_.prof.size();
-    c_.prof.push_back(r);
+    idx_ = (long)t.prof.size();
+    t.prof.push_back(r);
 }
 
 LaunchScope::~LaunchScope() {
-    if (idx_ >= 0) (void)hipEventRecord(c_.prof[idx_].b, c_.stream);
+    if (idx_ >= 0) (void)hipEventRecord(c_.top().prof[idx_].b, c_.stream);
 }
 
 TensorP crop_view(const TensorP& t, int h, int w) {

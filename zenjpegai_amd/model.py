@@ -136,13 +136,14 @@ def _tile_array(tiles):
 
 
 class Picture:
-    """A planned whole-picture synthesis: latents uploaded once, every tile on one stream,
-    tile cores written (and quantised) straight into the output planes."""
+    """A planned whole-picture synthesis: latents uploaded once, tile batches on one stream or
+    on `lanes` concurrent streams (``zjai_picture_set_lanes``), tile cores written (and
+    quantised) straight into the output planes."""
 
     def __init__(self, eng: Engine, primary: SynthesisPrimary,
                  secondary: SynthesisSecondary | None, lh: int, lw: int, height: int,
                  width: int, tiles, sv: int = 1, sh: int = 1, out_h: int | None = None,
-                 out_w: int | None = None, bit_depth: int = 0):
+                 out_w: int | None = None, bit_depth: int = 0, lanes: int = 1):
         self.eng = eng
         self.primary, self.secondary = primary, secondary
         self.lh, self.lw, self.height, self.width = lh, lw, height, width
@@ -156,6 +157,11 @@ class Picture:
                                         lh, lw, height, width, self._tiles, len(self.tiles), sv,
                                         sh, self.out_h, self.out_w, bit_depth,
                                         ctypes.byref(self._h)), eng.handle)
+        self.set_lanes(lanes)
+
+    def set_lanes(self, lanes: int):
+        check(lib().zjai_picture_set_lanes(self.eng.handle, self._h, lanes), self.eng.handle)
+        self.lanes = lanes
 
     def upload(self, y_hat: np.ndarray, uv_hat: np.ndarray | None = None):
         self._y = _f32(y_hat)
@@ -189,12 +195,12 @@ class Picture:
 
 
 def synthesize(eng: Engine, primary, secondary, y_hat, uv_hat, height, width, tiles, sv=1, sh=1,
-               out_h=None, out_w=None, bit_depth=0):
+               out_h=None, out_w=None, bit_depth=0, lanes=1):
     """``reconstruct::synthesize_with`` (src/decoder/reconstruct.rs:285-331) followed by
     ``quantize_plane`` when ``bit_depth`` > 0: returns ``(rec_y, rec_u, rec_v)``."""
     lh, lw = y_hat.shape[1:]
     pic = Picture(eng, primary, secondary, lh, lw, height, width, tiles, sv, sh, out_h, out_w,
-                  bit_depth)
+                  bit_depth, lanes)
     pic.upload(y_hat, uv_hat)
     pic.run()
     return pic.download()
