@@ -67,6 +67,14 @@ def lib():
         L.or_f16_to_f32.restype = ctypes.c_float
         L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.or_f16_round_trip.argtypes = [_f32p, ctypes.c_long, _f32p]
+        L.fc_conv2d.restype = ctypes.c_int
+        L.fc_conv2d.argtypes = L.or_conv2d.argtypes
+        L.fc_conv_transpose2d.restype = ctypes.c_int
+        L.fc_conv_transpose2d.argtypes = L.or_conv_transpose2d.argtypes
+        L.fc_block_size.restype = ctypes.c_int
+        L.fc_threads.restype = ctypes.c_int
+        L.fc_force_tier.restype = ctypes.c_int
+        L.fc_force_tier.argtypes = [ctypes.c_int]
         _lib = L
     return _lib
 
@@ -84,9 +92,10 @@ class OracleError(ValueError):
     pass
 
 
-def conv2d(x, weight, bias, stride=1, pad=(0, 0), groups=1, extra_pad=(0, 0, 0, 0)):
+def conv2d(x, weight, bias, stride=1, pad=(0, 0), groups=1, extra_pad=(0, 0, 0, 0), fast=False):
     """``reference::conv2d`` (src/nn/reference.rs:103-133) with the optional
-    ``ConvLayer::with_extra_pad`` border (src/nn/fast/layers.rs:36)."""
+    ``ConvLayer::with_extra_pad`` border (src/nn/fast/layers.rs:36). ``fast=True`` runs the
+    restated ``nn::fast`` blocked engine (``fast_cpu.cpp``) instead: same result, bit for bit."""
     x, weight = _c(x), _c(weight)
     c, h, w = x.shape
     out_ch, _icg, kh, kw = weight.shape
@@ -96,15 +105,17 @@ def conv2d(x, weight, bias, stride=1, pad=(0, 0), groups=1, extra_pad=(0, 0, 0, 
     y = np.empty((out_ch, oh, ow), np.float32)
     b = _c(bias) if bias is not None else None
     ext = (ctypes.c_int * 4)(*extra_pad)
-    rc = lib().or_conv2d(_p(x), c, h, w, _p(weight), _p(b) if b is not None else None, out_ch,
-                         kh, kw, stride, pad[0], pad[1], groups, ext, _p(y))
+    fn = lib().fc_conv2d if fast else lib().or_conv2d
+    rc = fn(_p(x), c, h, w, _p(weight), _p(b) if b is not None else None, out_ch,
+            kh, kw, stride, pad[0], pad[1], groups, ext, _p(y))
     if rc:
         raise OracleError("conv2d: inconsistent geometry")
     return y
 
 
-def conv_transpose2d(x, weight, bias, stride, pad, out_pad):
-    """``reference::conv_transpose2d`` (src/nn/reference.rs:206-236); weight [in][out][k][k]."""
+def conv_transpose2d(x, weight, bias, stride, pad, out_pad, fast=False):
+    """``reference::conv_transpose2d`` (src/nn/reference.rs:206-236); weight [in][out][k][k].
+    ``fast=True``: the restated ``nn::fast`` phase driver (stride 2, k <= 4), same result."""
     x, weight = _c(x), _c(weight)
     c, h, w = x.shape
     _, out_ch, k, _ = weight.shape
@@ -112,8 +123,9 @@ def conv_transpose2d(x, weight, bias, stride, pad, out_pad):
     ow = (w - 1) * stride + k + out_pad - 2 * pad
     y = np.empty((out_ch, oh, ow), np.float32)
     b = _c(bias) if bias is not None else None
-    rc = lib().or_conv_transpose2d(_p(x), c, h, w, _p(weight), _p(b) if b is not None else None,
-                                   out_ch, k, stride, pad, out_pad, _p(y))
+    fn = lib().fc_conv_transpose2d if fast else lib().or_conv_transpose2d
+    rc = fn(_p(x), c, h, w, _p(weight), _p(b) if b is not None else None,
+            out_ch, k, stride, pad, out_pad, _p(y))
     if rc:
         raise OracleError("conv_transpose2d: unsupported geometry")
     return y
@@ -229,3 +241,9 @@ def f16_round_trip(x):
     y = np.empty_like(x)
     lib().or_f16_round_trip(_p(x), x.size, _p(y))
     return y
+
+
+def force_cpu_tier(v: int) -> None:
+    """Pins the ``nn::fast`` restatement to its AVX2 (8) or AVX-512 (16) tier; 0 = automatic."""
+    if lib().fc_force_tier(v):
+        raise OracleError(f"CPU tier {v} is not available on this host")

@@ -12,8 +12,34 @@ import math
 
 import numpy as np
 
-from . import (add, channel_attention, conv2d, conv_transpose2d, denormalize, elu_gate, gate,
+from . import (add, channel_attention, denormalize, elu_gate, gate,
                layer_norm_channels, mul, pixel_shuffle, quantize_plane, relu, relu6, sigmoid)
+from . import conv2d as _conv2d
+from . import conv_transpose2d as _conv_transpose2d
+
+# Which convolution engine the graphs run on: the nn::reference loops (default) or the restated
+# nn::fast blocked engine (the CPU baseline). Both give the same result bit for bit.
+_FAST = False
+
+
+class fast_convs:
+    """``with fast_convs(): ...`` runs the graphs' convolutions on the nn::fast restatement."""
+
+    def __enter__(self):
+        global _FAST
+        self._prev, _FAST = _FAST, True
+
+    def __exit__(self, *exc):
+        global _FAST
+        _FAST = self._prev
+
+
+def conv2d(*args, **kw):
+    return _conv2d(*args, fast=_FAST, **kw)
+
+
+def conv_transpose2d(*args, **kw):
+    return _conv_transpose2d(*args, fast=_FAST, **kw)
 
 
 def _ceil(a, b):

@@ -396,3 +396,80 @@ def test_4k_independent_region_tiling_is_24_tiles():
     assert sum(x.core.width * x.core.height for x in t) == 2160 * 3840
     shapes = sorted({(x.image.width, x.image.height) for x in t})
     assert (640, 640) in shapes or (704, 704) in shapes
+
+
+# ------------------------------------------------- nn::fast restatement (the CPU baseline)
+def _tiers():
+    tiers = [8]
+    try:
+        oracle.force_cpu_tier(16)
+        tiers.append(16)
+    except oracle.OracleError:
+        pass
+    finally:
+        oracle.force_cpu_tier(0)
+    return tiers
+
+
+@pytest.fixture(params=_tiers())
+def cpu_tier(request):
+    oracle.force_cpu_tier(request.param)
+    yield request.param
+    oracle.force_cpu_tier(0)
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+@pytest.mark.parametrize("c,oc,k,stride,pad,groups,extra,h,w", [
+    (128, 128, 3, 1, 1, 1, (0, 0, 0, 0), 13, 50),    # HOP residual conv, a tail block per row
+    (20, 36, 3, 1, 1, 1, (0, 0, 0, 0), 7, 29),       # partial input / output blocks
+    (128, 128, 3, 2, 1, 1, (0, 0, 0, 0), 17, 33),    # CAB / TAM stride-2 conv
+    (128, 128, 3, 1, 1, 4, (0, 0, 0, 0), 10, 27),    # ResAU grouped conv (32 per group)
+    (64, 64, 1, 1, 0, 1, (0, 0, 0, 0), 5, 60),       # 1x1
+    (144, 128, 2, 1, 0, 1, (0, 0, 1, 1), 6, 9),      # SOP upsampler 2x2 with extra pad
+    (64, 64, 3, 1, 1, 4, (0, 0, 0, 0), 6, 7),        # 16 per group: the oracle-loop fallback
+    (256, 48, 3, 1, 1, 1, (0, 0, 0, 0), 8, 8),       # combine layer
+])
+def test_fast_conv2d_equals_reference_loops_bit_for_bit(cpu_tier, c, oc, k, stride, pad, groups,
+                                                        extra, h, w):
+    """nn::fast is bit-identical to nn::reference by contract (src/nn/mod.rs:1-29,
+    tests/fast_vs_reference.rs); so is its restatement, in both SIMD tiers."""
+    x = rng.standard_normal((c, h, w)).astype(np.float32)
+    wt = (rng.standard_normal((oc, c // groups, k, k)) * 0.1).astype(np.float32)
+    b = rng.standard_normal(oc).astype(np.float32)
+    want = oracle.conv2d(x, wt, b, stride, (pad, pad), groups, extra)
+    got = oracle.conv2d(x, wt, b, stride, (pad, pad), groups, extra, fast=True)
+    assert got.shape == want.shape
+    assert np.array_equal(_bits(got), _bits(want))
+
+
+@pytest.mark.parametrize("c,oc,k,out_pad,h,w", [
+    (128, 128, 3, 1, 9, 13), (64, 8, 3, 1, 5, 31), (192, 128, 4, 0, 7, 11), (20, 3, 3, 1, 4, 5),
+    (128, 1, 3, 1, 6, 40),
+])
+def test_fast_conv_transpose2d_equals_reference_loops_bit_for_bit(cpu_tier, c, oc, k, out_pad, h, w):
+    x = rng.standard_normal((c, h, w)).astype(np.float32)
+    wt = (rng.standard_normal((c, oc, k, k)) * 0.1).astype(np.float32)
+    b = rng.standard_normal(oc).astype(np.float32)
+    want = oracle.conv_transpose2d(x, wt, b, 2, 1, out_pad)
+    got = oracle.conv_transpose2d(x, wt, b, 2, 1, out_pad, fast=True)
+    assert got.shape == want.shape
+    assert np.array_equal(_bits(got), _bits(want))
+
+
+def test_fast_graph_equals_reference_graph():
+    """The whole HOP luma + chroma graph on the nn::fast restatement equals the reference-loop
+    graph bit for bit (the CPU baseline computes the oracle's result)."""
+    import oracle.graphs as og
+    from zenjpegai_amd import synth
+    py = synth.random_params("hop", "y", seed=12, gain=0.5)
+    puv = synth.random_params("hop", "uv", seed=12, gain=0.5)
+    y = synth.latent(12, "fg/y", 160, 4, 6)
+    uv = synth.latent(12, "fg/uv", 96, 4, 6)
+    want = (og.primary(py, "hop", y, 64, 96), og.secondary(puv, "hop", y, uv, 64, 96))
+    with og.fast_convs():
+        got = (og.primary(py, "hop", y, 64, 96), og.secondary(puv, "hop", y, uv, 64, 96))
+    for g, wv in zip(got, want):
+        assert np.array_equal(_bits(g), _bits(wv))
