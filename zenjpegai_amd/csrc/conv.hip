@@ -184,7 +184,10 @@ __device__ __forceinline__ void epilogue_store(const ConvParams& p, int b, int o
     }
 }
 
-template <typename T, int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF>
+// SG: input-channel chunks staged per barrier. 1x1 layers do little matrix work per chunk, so
+// they stage several (SG = 4: the whole K of a 128-channel f16 layer) with every global load of
+// the stage issued before its LDS stores -- more bytes in flight per workgroup, fewer barriers.
+template <typename T, int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF, int SG>
 __global__ void __launch_bounds__(WC * WP * 64)
 conv_igemm(const ConvParams p) {
     constexpr int NT = WC * WP * 64;
@@ -201,10 +204,10 @@ conv_igemm(const ConvParams p) {
     // the K loop (the +4 pads rows against bank conflicts).
     constexpr int OUT_LD = NB * 16 + 4;
     constexpr int OUT_U = (TY * 16 * OUT_LD + 3) / 4;
-    constexpr int LDS_U = (HALO_U + W_U) > OUT_U ? (HALO_U + W_U) : OUT_U;
+    constexpr int STG_U = HALO_U + W_U;
+    constexpr int LDS_U = (SG * STG_U) > OUT_U ? (SG * STG_U) : OUT_U;
+    constexpr int HN = (HALO_U + NT - 1) / NT, WN = (W_U + NT - 1) / NT;
     __shared__ u32x4 s_lds[LDS_U];
-    u32x4* s_halo = s_lds;
-    u32x4* s_w = s_lds + HALO_U;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wc = wave % WC, wp = wave / WC;
@@ -263,25 +266,7 @@ conv_igemm(const ConvParams p) {
     const T* wg = (const T*)p.w + phase * p.phase_stride + (long long)bi * p.w_bstride;
     const long long xbase = (long long)p.x.c_off + (long long)g * p.cin_g;
 
-    for (int chunk = 0; chunk < p.nchunks; ++chunk) {
-        __syncthreads();
-        const int cl0 = chunk * CK;
-        for (int u = tid; u < HALO_U; u += NT) {
-            const int pix = u >> 2, q = u & 3;
-            const int hy = pix / HX, hx = pix - hy * HX;
-            const int iy = iy0 + hy, ix = ix0 + hx, cl = cl0 + q * VEC;
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (iy >= 0 && iy < p.H && ix >= 0 && ix < p.W && cl < p.cin_g) {
-                v = *(const u32x4*)(xg + (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + cl);
-                if (p.relu6_in) v = relu6_vec<T>(v);
-            }
-            s_halo[u] = v;
-        }
-        const u32x4* wsrc = (const u32x4*)(wg + ((long long)(g * p.nchunks + chunk) * p.nblk_g + nb0) *
-                                                     (long long)(NTAP * 16 * CK));
-        for (int u = tid; u < W_U; u += NT) s_w[u] = wsrc[u];
-        __syncthreads();
-
+    auto compute = [&](const u32x4* s_halo, const u32x4* s_w) {
         for (int t = 0; t < ntap; ++t) {
             const int ky = tdy[t], kx = tdx[t];
             u32x4 a[CF], b[PF];
@@ -296,6 +281,83 @@ conv_igemm(const ConvParams p) {
             for (int cf = 0; cf < CF; ++cf)
 #pragma unroll
                 for (int pf = 0; pf < PF; ++pf) Mma<T>::run(acc[cf][pf], a[cf], b[pf]);
+        }
+    };
+
+    if constexpr (SG == 1) {
+        for (int chunk = 0; chunk < p.nchunks; ++chunk) {
+            __syncthreads();
+            const int cl0 = chunk * CK;
+            for (int u = tid; u < HALO_U; u += NT) {
+                const int pix = u >> 2, q = u & 3;
+                const int hy = pix / HX, hx = pix - hy * HX;
+                const int iy = iy0 + hy, ix = ix0 + hx, cl = cl0 + q * VEC;
+                u32x4 v = {0u, 0u, 0u, 0u};
+                if (iy >= 0 && iy < p.H && ix >= 0 && ix < p.W && cl < p.cin_g) {
+                    v = *(const u32x4*)(xg + (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + cl);
+                    if (p.relu6_in) v = relu6_vec<T>(v);
+                }
+                s_lds[u] = v;
+            }
+            const u32x4* wsrc = (const u32x4*)(wg + ((long long)(g * p.nchunks + chunk) * p.nblk_g + nb0) *
+                                                         (long long)(NTAP * 16 * CK));
+            for (int u = tid; u < W_U; u += NT) s_lds[HALO_U + u] = wsrc[u];
+            __syncthreads();
+            compute(s_lds, s_lds + HALO_U);
+        }
+    } else {
+        // Halo element offsets of this thread's units (u = tid + i * NT), -1 in the padding.
+        long long hoff[HN];
+#pragma unroll
+        for (int i = 0; i < HN; ++i) {
+            const int u = tid + i * NT, pix = u >> 2, q = u & 3;
+            const int hy = pix / HX, hx = pix - hy * HX;
+            const int iy = iy0 + hy, ix = ix0 + hx;
+            hoff[i] = (u < HALO_U && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W)
+                          ? (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + q * VEC
+                          : -1;
+        }
+        for (int c0 = 0; c0 < p.nchunks; c0 += SG) {
+            const int ns = min(SG, p.nchunks - c0);
+            u32x4 rh[SG][HN], rw[SG][WN];
+#pragma unroll
+            for (int s = 0; s < SG; ++s) {
+                if (s >= ns) break;
+                const int cl0 = (c0 + s) * CK;
+#pragma unroll
+                for (int i = 0; i < HN; ++i) {
+                    const int q = (tid + i * NT) & 3;
+                    u32x4 v = {0u, 0u, 0u, 0u};
+                    if (hoff[i] >= 0 && cl0 + q * VEC < p.cin_g) v = *(const u32x4*)(xg + hoff[i] + cl0);
+                    rh[s][i] = v;
+                }
+                const u32x4* wsrc = (const u32x4*)(wg + ((long long)(g * p.nchunks + c0 + s) * p.nblk_g + nb0) *
+                                                             (long long)(NTAP * 16 * CK));
+#pragma unroll
+                for (int i = 0; i < WN; ++i) {
+                    const int u = tid + i * NT;
+                    rw[s][i] = u < W_U ? wsrc[u] : u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int s = 0; s < SG; ++s) {
+                if (s >= ns) break;
+#pragma unroll
+                for (int i = 0; i < HN; ++i) {
+                    const int u = tid + i * NT;
+                    u32x4 v = rh[s][i];
+                    if (p.relu6_in) v = relu6_vec<T>(v);
+                    if (u < HALO_U) s_lds[s * STG_U + u] = v;
+                }
+#pragma unroll
+                for (int i = 0; i < WN; ++i) {
+                    const int u = tid + i * NT;
+                    if (u < W_U) s_lds[s * STG_U + HALO_U + u] = rw[s][i];
+                }
+            }
+            __syncthreads();
+            for (int s = 0; s < ns; ++s) compute(s_lds + s * STG_U, s_lds + s * STG_U + HALO_U);
         }
     }
 
@@ -482,6 +544,7 @@ hipError_t launch_convT_narrow(int dtype, int coutp, const ConvParams& p, const 
 // ---------------------------------------------------------------------------------------------
 template <typename T, int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF>
 static hipError_t go(const ConvParams& p0, hipStream_t s) {
+    constexpr int SG = (KH * KW == 1 && !TR) ? 4 : 1;
     constexpr int TY = WP * PF;
     ConvParams p = p0;
     const int gh = TR ? (p.OH + 1) / 2 : p.OH;
@@ -491,7 +554,7 @@ static hipError_t go(const ConvParams& p0, hipStream_t s) {
     p.gy = (gh + TY - 1) / TY;
     const long long total = (long long)p.gx * p.gy * p.N * p.ntiles * (TR ? 4 : 1);
     if (total <= 0 || total > (1ll << 30)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((conv_igemm<T, KH, KW, S, TR, WC, WP, CF, PF>), dim3((unsigned)total),
+    hipLaunchKernelGGL((conv_igemm<T, KH, KW, S, TR, WC, WP, CF, PF, SG>), dim3((unsigned)total),
                        dim3(WC * WP * 64), 0, s, p);
     return hipGetLastError();
 }
