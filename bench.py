@@ -8,7 +8,9 @@ latents already resident in HBM (``Picture.run``: every tile on one HIP stream, 
 written by the last layers' epilogues).
 
 ``value`` is the fp32-MFMA parity path (the reference computes in f32). Extra lines in ``extra``:
-the same picture on the f16 / bf16 paths and BASELINE config 4 (SOP luma 1024x1024, 8-bit).
+the same picture on the f16 / bf16 paths, BASELINE config 4 (SOP luma 1024x1024, 8-bit), a 4 MP
+HOP picture (2048x2048, 1 MP header tiles) and BASELINE configs 1-3 as single layers (kernel time
+and TFLOP/s, f32 and bf16).
 
 ``roofline``: one profiled step (HIP events around every launch on the library's stream); the
 dominant kernel is the one with the largest summed time; achieved = its algorithmic FLOPs (all
@@ -48,6 +50,13 @@ def make_workload(name, eng, lanes=1):
         h, w, op, sv, sh, bits = 2160, 3840, "hop", 2, 2, 10
         lh, lw = 135, 240
         tiles = model.synthesis_tiles(h, w, lh, lw, (640, 128), (2, 3))
+        uv = True
+    elif name == "hop4mp":
+        # 2048 x 2048 (4.19 MP), the reference's 4 MP sweep size; header tiling without
+        # independent regions: 1 MP tiles (1024, overlap 64; src/encoder/tiles.rs:294-317).
+        h, w, op, sv, sh, bits = 2048, 2048, "hop", 2, 2, 10
+        lh, lw = 128, 128
+        tiles = model.synthesis_tiles(h, w, lh, lw, (1024, 64))
         uv = True
     elif name == "cfg4":
         h, w, op, sv, sh, bits = 1024, 1024, "sop", 1, 1, 8
@@ -98,6 +107,49 @@ def profile_step(eng, pic):
         d["flops"] += flops
         d["bytes"] += nbytes
     return by
+
+
+def layer_configs(prec, reps=10):
+    """BASELINE configs 1-3 as single-layer runs at their full sizes: kernel time per run (HIP
+    events around each launch) and conv TFLOP/s (all taps counted)."""
+    from zenjpegai_amd import _lib, nn, synth
+    eng = nn.Engine(0, prec)
+    he = lambda seed, name, shape, fan: synth.normal(seed, name, shape, float(np.sqrt(2.0 / fan)))
+    x1 = nn.BTensor.from_planar(eng, synth.uniform(1, "cfg1/x", (128, 256, 256), -1, 1))
+    c1 = nn.ConvLayer(nn.Conv2d(128, 128, (3, 3), 1, (1, 1), 1, he(1, "cfg1/w", (128, 128, 3, 3), 1152),
+                                synth.normal(1, "cfg1/b", (128,), 0.01)), eng)
+    x2 = nn.BTensor.from_planar(eng, synth.laplace(2, "cfg2/x", (192, 64, 64), 1.0))
+    c2 = nn.ConvTransposeLayer(nn.ConvTranspose2d(192, 128, 4, 2, 1, 0, he(2, "cfg2/w", (192, 128, 4, 4), 768),
+                                                  synth.normal(2, "cfg2/b", (128,), 0.01)), eng)
+    x3 = nn.BTensor.from_planar(eng, synth.uniform(3, "cfg3/x", (192, 128, 128), -2, 2))
+    mk = lambda k, name: nn.ConvLayer(nn.Conv2d(192, 192, (k, k), 1, (k // 2, k // 2), 1,
+                                                he(3, f"cfg3/{name}w", (192, 192, k, k), 192 * k * k),
+                                                synth.normal(3, f"cfg3/{name}b", (192,), 0.01)), eng)
+    t1, t2, gt = mk(3, "c1"), mk(3, "c2"), mk(1, "g")
+
+    def cfg3():
+        # t = conv3x3(leaky(conv3x3(x))) + x; out = t * sigmoid(conv1x1(x)), epilogues fused.
+        t = t1.forward_fused(eng, x3, act=_lib.ACT_LEAKY_RELU)
+        t = t2.forward_fused(eng, t, res=_lib.RES_ADD, r1=x3)
+        return gt.forward_fused(eng, x3, act=_lib.ACT_SIGMOID, res=_lib.RES_MUL, r1=t)
+
+    runs = {"cfg1_conv3x3_128_256sq": lambda: c1.forward(eng, x1),
+            "cfg2_convT4_192to128_leaky": lambda: c2.forward_fused(eng, x2, act=_lib.ACT_LEAKY_RELU),
+            "cfg3_res_attn_block_192_128sq": cfg3}
+    out = {}
+    for key, fn in runs.items():
+        for _ in range(3):
+            fn()
+        eng.sync()
+        eng.profile_begin()
+        for _ in range(reps):
+            fn()
+        recs = eng.profile_end()
+        ms = sum(r[3] for r in recs)
+        fl = sum(r[1] for r in recs)
+        out[f"{key}_{prec}_us"] = round(ms * 1e3 / reps, 2)
+        out[f"{key}_{prec}_tflops"] = round(fl / (ms / 1e3) / 1e12, 2)
+    return out
 
 
 def read_traffic(kernel, workload, precision):
@@ -153,7 +205,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="cfg5", choices=["cfg5", "cfg4"])
+    ap.add_argument("--workload", default="cfg5", choices=["cfg5", "cfg4", "hop4mp"])
     ap.add_argument("--precision", default="f32", choices=["f32", "f16", "bf16"])
     ap.add_argument("--lanes", type=int, default=4,
                     help="concurrent streams the picture's tile batches run on (1 = one stream)")
@@ -247,6 +299,17 @@ def main():
             extra[f"cfg4_sop_1mp_{args.precision}_mpix_s"] = round(i3["h"] * i3["w"] / (ms3 / 1e3) / 1e6, 3)
             log(f"[bench] cfg4: {ms3:.3f} ms/step")
             del p3, e3
+        if args.workload == "cfg5":
+            for prec in (args.precision, "bf16"):
+                e4 = nn.Engine(0, prec)
+                p4, i4 = make_workload("hop4mp", e4, args.lanes)
+                ms4 = time_steps(e4, p4, args.steps, args.warmup)
+                extra[f"hop_4mp_2048sq_{prec}_mpix_s"] = round(i4["h"] * i4["w"] / (ms4 / 1e3) / 1e6, 3)
+                log(f"[bench] hop 4 MP {prec}: {ms4:.2f} ms/step")
+                del p4, e4
+        for prec in ("f32", "bf16"):
+            extra.update(layer_configs(prec))
+        log("[bench] configs 1-3: " + ", ".join(f"{k}={v}" for k, v in extra.items() if k.startswith("cfg") and "tflops" in k))
 
     cpu = None
     if not args.no_cpu:
@@ -260,10 +323,13 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": args.precision, "data": "synthetic (He-normal random-init weights, Laplace latents)",
         "config": {
-            "workload": ("cfg5: HOP Y+UV synthesis 3840x2160 4:2:0 10-bit, 2x3 independent "
-                         "regions, tile 640 / overlap 128 (24 tiles), latents resident in HBM"
-                         if args.workload == "cfg5" else
-                         "cfg4: SOP luma synthesis 1024x1024 8-bit, untiled, latent resident"),
+            "workload": {
+                "cfg5": "cfg5: HOP Y+UV synthesis 3840x2160 4:2:0 10-bit, 2x3 independent regions, "
+                        "tile 640 / overlap 128 (24 tiles), latents resident in HBM",
+                "cfg4": "cfg4: SOP luma synthesis 1024x1024 8-bit, untiled, latent resident",
+                "hop4mp": "HOP Y+UV synthesis 2048x2048 4:2:0 10-bit, tile 1024 / overlap 64, "
+                          "latents resident in HBM"}[args.workload],
+            "lanes": args.lanes,
             "picture": f"{info['w']}x{info['h']}", "tiles": info["tiles"],
             "precision_path": args.precision},
         "roofline": roof,

@@ -312,3 +312,19 @@ def test_attention_one_position_kat(engines):
     q[16:18, 0, 0] = [10.0, 20.0]
     got = nn.channel_attention(eng, nn.BTensor.from_planar(eng, q), 4, np.ones(4, np.float32)).to_planar()
     assert got[0:2, 0, 0].tolist() == [15.0, 15.0]
+
+
+def test_tensors_and_layers_may_outlive_their_context():
+    """Destroying the context first is allowed: tensors return their blocks to the pool they
+    share with it (which lives until the last of them), layers free their own weights."""
+    eng = nn.Engine(0, "f32")
+    x = nn.BTensor.from_planar(eng, synth.normal(13, "life/x", (16, 6, 7), 1.0))
+    layer = nn.ConvLayer(nn.Conv2d(16, 16, (3, 3), 1, (1, 1), 1,
+                                   synth.normal(13, "life/w", (16, 16, 3, 3), 0.1)), eng)
+    y = layer.forward(eng, x)
+    eng.sync()
+    eng.close()
+    del x, y, layer
+    eng2 = nn.Engine(0, "f32")
+    z = nn.BTensor.from_planar(eng2, np.ones((8, 3, 3), np.float32))
+    assert np.array_equal(z.to_planar(), np.ones((8, 3, 3), np.float32))

@@ -80,7 +80,10 @@ struct ProfRec {
 struct Context {
     int device = 0;
     hipStream_t stream = nullptr;
-    Pool pool;
+    // The pool is shared with every tensor allocated from it, so a tensor that outlives its
+    // context (a caller destroying the context first) still returns its block to a live pool.
+    std::shared_ptr<Pool> pool_owner = std::make_shared<Pool>();
+    Pool& pool = *pool_owner;
     std::string last_error;
     volatile int stop = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;

@@ -81,8 +81,8 @@ TensorP Context::alloc(int n, int c, int h, int w, int dtype) {
     t->v.c_off = 0;
     const size_t bytes = (size_t)n * (size_t)t->v.bstride * dtype_size(dtype);
     void* p = pool.alloc(bytes);
-    Context* self = this;
-    t->keep = std::shared_ptr<void>(p, [self](void* q) { self->pool.release(q); });
+    std::shared_ptr<Pool> owner = pool_owner;
+    t->keep = std::shared_ptr<void>(p, [owner](void* q) { owner->release(q); });
     t->base = p;
     t->v.p = p;
     return t;
