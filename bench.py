@@ -12,9 +12,10 @@ the same picture on the f16 / bf16 paths, BASELINE config 4 (SOP luma 1024x1024,
 HOP picture (2048x2048, 1 MP header tiles) and BASELINE configs 1-3 as single layers (kernel time
 and TFLOP/s, f32 and bf16).
 
-``roofline``: one profiled step (HIP events around every launch on the library's stream); the
-dominant kernel is the one with the largest summed time; achieved = its algorithmic FLOPs (all
-taps, padding included) / its summed time. ``traffic``: HBM bytes per launch of that kernel
+``roofline``: one profiled step (HIP events around every launch, all on one stream); the
+dominant kernel is the one with the largest summed time; bound by its arithmetic intensity
+against the machine balance; achieved = its algorithmic FLOPs (all taps, padding included) or
+compulsory bytes / its summed time. ``traffic``: HBM bytes per launch of that kernel
 from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes summarised in ``profiles/`` (null if absent).
 
 ``cpu_baseline``: the reference's CPU engine ``nn::fast`` restated in C++ (``oracle/fast_cpu.cpp``,
@@ -251,7 +252,10 @@ def main():
     conv_flops = sum(d["flops"] for d in conv.values())
     conv_ms = sum(d["ms"] for d in conv.values())
     dom_name, dom = max(prof.items(), key=lambda kv: kv[1]["ms"])
-    if dom["flops"] > 0:
+    # Bound by arithmetic intensity against the machine balance (peak FLOP/s / peak bytes/s):
+    # below it the kernel is priced against HBM bandwidth, above it against the MFMA peak.
+    balance = PEAK_TFLOPS[args.precision] * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if dom["flops"] > 0 and dom["bytes"] > 0 and dom["flops"] / dom["bytes"] >= balance:
         ach = dom["flops"] / (dom["ms"] / 1e3) / 1e12
         peak = PEAK_TFLOPS[args.precision]
         roof = {"bound": "mfma", "achieved": round(ach, 3), "peak": peak, "unit": "TFLOP/s"}
