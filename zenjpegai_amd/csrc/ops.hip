@@ -114,70 +114,153 @@ __global__ void k_eltwise(int op, View xv, View sv, int N, int C, int h, int w) 
 // ------------------------------------------------------------------------- depthwise 3x3
 // Per output element: acc = bias; for ky, kx ascending: acc = fma(w, x, acc), padding taps
 // included (src/nn/fast/depthwise.rs:40-73). Weights are stored transposed, [9][C].
-// One thread: 4 channels x DW_X consecutive output columns of one row, with a sliding 3-row x
-// (DW_X + 2)-column window of input vectors (lanes run over channels, so every load instruction
-// of a wave reads contiguous channel runs).
-constexpr int DW_X = 4;
+// Row-sliding: a thread owns one 16-byte channel vector (V = 4 f32 or 8 f16/bf16 channels) of
+// DW_X consecutive output columns over DW_R consecutive output rows. It keeps a 3-row window of
+// input vectors in registers and loads one new input row per output row, so every input vector
+// is loaded once per thread instead of three times; the unrolled row loop lets the next row's
+// loads issue before the current row's FMAs. Lanes run over channels (a wave's load reads a
+// contiguous channel run). For the ELU-gated FFN variant the two halves of a wave compute the
+// two channel halves (first half: lanes 0-31, second half: lanes 32-63, same vectors) and swap
+// them across lanes before gating, so each lane holds one window.
+constexpr int DW_R = 8;
+
+template <typename T> struct Dw {
+    static constexpr int V = 16 / (int)sizeof(T);  // channels per 16-byte vector
+    static constexpr int X = sizeof(T) == 4 ? 4 : 2;  // output columns per thread
+};
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
-__device__ __forceinline__ void dw_strip(const View& src, int b, int y, int x0, int h, int w,
-                                         int c0, const float* wt, int C, const float* bias,
-                                         f32x4 (&acc)[DW_X]) {
-    f32x4 wv[9];
+__device__ __forceinline__ void dw_unpack(u32x4 v, float (&o)[Dw<T>::V]) {
+    if constexpr (sizeof(T) == 4) {
+        const f32x4 f = __builtin_bit_cast(f32x4, v);
 #pragma unroll
-    for (int t = 0; t < 9; ++t) wv[t] = *(const f32x4*)(wt + t * C + c0);
+        for (int i = 0; i < 4; ++i) o[i] = f[i];
+    } else {
+        typedef T t8 __attribute__((ext_vector_type(8)));
+        const t8 hv = __builtin_bit_cast(t8, v);
 #pragma unroll
-    for (int j = 0; j < DW_X; ++j)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) acc[j][k] = bias ? bias[c0 + k] : 0.0f;
-#pragma unroll
-    for (int ky = 0; ky < 3; ++ky) {
-        const int yy = y + ky - 1;
-        const bool row_ok = yy >= 0 && yy < h;
-        f32x4 win[DW_X + 2];
-#pragma unroll
-        for (int j = 0; j < DW_X + 2; ++j) {
-            const int xx = x0 + j - 1;
-            win[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (row_ok && xx >= 0 && xx < w) win[j] = load4<T>(at<T>(src, b, yy, xx, c0));
-        }
-        // Taps in (ky, kx) ascending order per output: acc = fma(w, x, acc).
-#pragma unroll
-        for (int j = 0; j < DW_X; ++j)
-#pragma unroll
-            for (int kx = 0; kx < 3; ++kx)
-#pragma unroll
-                for (int k = 0; k < 4; ++k) acc[j][k] = fmaf(wv[ky * 3 + kx][k], win[j + kx][k], acc[j][k]);
+        for (int i = 0; i < 8; ++i) o[i] = (float)hv[i];
     }
+}
+
+// Input vector at (y, x), channels [c, c + nv) (nv < V only at a channel tail), zero outside.
+template <typename T>
+__device__ __forceinline__ u32x4 dw_load(const View& src, int b, int y, int x, int h, int w, int c,
+                                         int nv, bool valid) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (!valid || y < 0 || y >= h || x < 0 || x >= w) return v;
+    const T* px = at<T>(src, b, y, x, c);
+    if (nv == Dw<T>::V) return *reinterpret_cast<const u32x4*>(px);
+    T tmp[Dw<T>::V];
+#pragma unroll
+    for (int k = 0; k < Dw<T>::V; ++k) tmp[k] = k < nv ? px[k] : (T)0.0f;
+    return __builtin_bit_cast(u32x4, tmp);
 }
 
 template <typename T>
 __global__ void __launch_bounds__(256) k_depthwise3x3(View src, View dst, int N, int C, int h, int w,
                                                       const float* wt, const float* bias, int elu_half) {
-    const int cout = elu_half > 0 ? elu_half : C;
-    const int q = cout / 4, wx = (w + DW_X - 1) / DW_X;
-    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)N * h * wx * q) return;
-    const Idx4 d = split(i, h, wx, q);
-    const int x0 = d.x * DW_X;
-    f32x4 a[DW_X];
-    dw_strip<T>(src, d.b, d.y, x0, h, w, d.cq * 4, wt, C, bias, a);
-    if (elu_half > 0) {
-        f32x4 g[DW_X];
-        dw_strip<T>(src, d.b, d.y, x0, h, w, d.cq * 4 + elu_half, wt, C, bias, g);
+    constexpr int V = Dw<T>::V, X = Dw<T>::X;
+    const bool gated = elu_half > 0;
+    const int cout = gated ? elu_half : C;
+    const int nvec = (cout + V - 1) / V, vpw = gated ? 32 : 64, nvw = (nvec + vpw - 1) / vpw;
+    const int lane = threadIdx.x & 63;
+    const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int gx = (w + X - 1) / X, gr = (h + DW_R - 1) / DW_R;
+    if (wave >= (long long)N * gr * gx * nvw) return;  // whole waves only
+    const int cw = (int)(wave % nvw);
+    long long t = wave / nvw;
+    const int xg = (int)(t % gx);
+    t /= gx;
+    const int rs = (int)(t % gr), b = (int)(t / gr);
+    const int vidx = cw * vpw + (gated ? (lane & 31) : lane), half = gated ? lane >> 5 : 0;
+    const bool valid = vidx < nvec;
+    const int nv = valid ? min(V, cout - vidx * V) : 0;
+    const int c0 = vidx * V + half * elu_half;  // channel of this lane's strip
+    const int x0 = xg * X, y0 = rs * DW_R;
+
+    float wv[9][V], bv[V];
 #pragma unroll
-        for (int j = 0; j < DW_X; ++j)
+    for (int k = 0; k < V; ++k) bv[k] = (bias && k < nv) ? bias[c0 + k] : 0.0f;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float v = a[j][k];
-                const float e = cephes_exp(v) - 1.0f;
-                const float elu = v > 0.0f ? v : e;
-                a[j][k] = elu * g[j][k];
-            }
+    for (int tp = 0; tp < 9; ++tp)
+#pragma unroll
+        for (int k = 0; k < V; ++k) wv[tp][k] = k < nv ? wt[tp * C + c0 + k] : 0.0f;
+
+    u32x4 win[3][X + 2];
+#pragma unroll
+    for (int j = 0; j < X + 2; ++j) {
+        win[0][j] = dw_load<T>(src, b, y0 - 1, x0 + j - 1, h, w, c0, nv, valid);
+        win[1][j] = dw_load<T>(src, b, y0, x0 + j - 1, h, w, c0, nv, valid);
     }
 #pragma unroll
-    for (int j = 0; j < DW_X; ++j)
-        if (x0 + j < w) store4<T>(at_mut<T>(dst, d.b, d.y, x0 + j, d.cq * 4), a[j]);
+    for (int r = 0; r < DW_R; ++r) {
+        const int oy = y0 + r;
+        if (oy >= h) break;  // uniform per wave
+#pragma unroll
+        for (int j = 0; j < X + 2; ++j) win[2][j] = dw_load<T>(src, b, oy + 1, x0 + j - 1, h, w, c0, nv, valid);
+        float acc[X][V];
+#pragma unroll
+        for (int j = 0; j < X; ++j)
+#pragma unroll
+            for (int k = 0; k < V; ++k) acc[j][k] = bv[k];
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky) {
+            float row[X + 2][V];
+#pragma unroll
+            for (int j = 0; j < X + 2; ++j) dw_unpack<T>(win[ky][j], row[j]);
+            // Taps in (ky, kx) ascending order per output: acc = fma(w, x, acc).
+#pragma unroll
+            for (int j = 0; j < X; ++j)
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx)
+#pragma unroll
+                    for (int k = 0; k < V; ++k) acc[j][k] = fmaf(wv[ky * 3 + kx][k], row[j + kx][k], acc[j][k]);
+        }
+        if (gated) {
+            // Lane l < 32 holds the first-half channels, lane l + 32 the matching second half.
+#pragma unroll
+            for (int j = 0; j < X; ++j)
+#pragma unroll
+                for (int k = 0; k < V; ++k) {
+                    const float g = __shfl_xor(acc[j][k], 32);
+                    const float v = acc[j][k];
+                    const float e = cephes_exp(v) - 1.0f;
+                    const float elu = v > 0.0f ? v : e;
+                    acc[j][k] = elu * g;
+                }
+        }
+        if (valid && half == 0) {
+#pragma unroll
+            for (int j = 0; j < X; ++j) {
+                const int ox = x0 + j;
+                if (ox >= w) continue;
+                T* po = at_mut<T>(dst, b, oy, ox, vidx * V);
+                if (nv == V) {
+                    if constexpr (sizeof(T) == 4) {
+                        *reinterpret_cast<f32x4*>(po) = f32x4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
+                    } else {
+                        typedef T t8 __attribute__((ext_vector_type(8)));
+                        t8 hv;
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) hv[k] = (T)acc[j][k];
+                        *reinterpret_cast<t8*>(po) = hv;
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < V; ++k)
+                        if (k < nv) po[k] = from_f32<T>(acc[j][k]);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < X + 2; ++j) {
+            win[0][j] = win[1][j];
+            win[1][j] = win[2][j];
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------ layer norm
@@ -416,9 +499,15 @@ hipError_t launch_depthwise3x3(View src, View dst, int dtype, int N, int C, int 
                                const float* weight, const float* bias, int elu_half,
                                hipStream_t s) {
     const int cout = elu_half > 0 ? elu_half : C;
-    const long long n = (long long)N * h * ((w + DW_X - 1) / DW_X) * (cout / 4);
-    if (n == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_depthwise3x3, <<<grid_for(n), 256, 0, s>>>(src, dst, N, C, h, w, weight, bias, elu_half))
+    if (cout % 4 || C % 4 || (elu_half > 0 && 2 * elu_half != C)) return hipErrorInvalidValue;
+    const int V = dtype == DT_F32 ? 4 : 8, X = dtype == DT_F32 ? 4 : 2;  // Dw<T>
+    const int vpw = elu_half > 0 ? 32 : 64;
+    const long long waves = (long long)N * ((h + DW_R - 1) / DW_R) * ((w + X - 1) / X) *
+                            (((cout + V - 1) / V + vpw - 1) / vpw);
+    if (waves == 0) return hipSuccess;
+    const long long blocks = (waves + 3) / 4;
+    if (blocks > (1ll << 31) - 1) return hipErrorInvalidValue;
+    ZJAI_DISPATCH(dtype, k_depthwise3x3, <<<dim3((unsigned)blocks), 256, 0, s>>>(src, dst, N, C, h, w, weight, bias, elu_half))
     return hipGetLastError();
 }
 
