@@ -74,7 +74,11 @@ typedef struct zjai_picture zjai_picture;
 /* ------------------------------------------------------------------ context / diagnostics */
 
 /* Replaces `Engine` construction (src/nn/fast/mod.rs:128-172) for the HIP backend: binds a
- * device and creates its stream. flags: reserved, 0. */
+ * device and creates its stream. flags: 0 or ZJAI_CTX_UNFUSED_FFN (other bits are rejected). */
+/* Run the transformer blocks' feed-forward half (src/model/attention.rs:346-369) as separate
+ * layer-norm, 1x1, depthwise+gate and 1x1 kernels instead of the fused kernel the 16-bit
+ * precisions use by default (the two give bit-identical results). */
+#define ZJAI_CTX_UNFUSED_FFN 0x1u
 ZJAI_API int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out);
 ZJAI_API int32_t zjai_ctx_destroy(zjai_ctx* ctx);
 /* Copies the last failure message (NUL-terminated, truncated to len). Works with ctx == NULL

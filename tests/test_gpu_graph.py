@@ -20,7 +20,7 @@ import pytest
 import oracle
 import oracle.graphs as og
 from oracle import geometry as geo
-from zenjpegai_amd import model, nn, synth
+from zenjpegai_amd import _lib, model, nn, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -96,6 +96,38 @@ def test_fast_paths_psnr(engines, prec, floor, op):
     v = psnr(got, want)
     print(f"{op} {prec}: PSNR vs fp32 oracle {v:.1f} dB")
     assert np.isfinite(got).all() and v >= floor
+
+
+@pytest.mark.parametrize("prec", ["bf16", "f16"])
+@pytest.mark.parametrize("comp", ["y", "uv"])
+def test_fused_ffn_is_bit_identical_to_unfused(prec, comp):
+    """The fused feed-forward kernel (HOP luma TAM: dim 128, chroma: dim 64) against the same
+    net run with layer norm, 1x1, depthwise+gate and 1x1 as separate kernels. The feature maps
+    (64 x 96 and 64 x 48) span several 14 x 14 tiles with partial ones at the right and bottom."""
+    fused = nn.Engine(0, prec)
+    plain = nn.Engine(0, prec, flags=_lib.CTX_UNFUSED_FFN)
+    p = synth.random_params("hop", comp, seed=24, gain=0.5)
+    outs, names = [], []
+    for eng in (fused, plain):
+        eng.profile_begin()
+        if comp == "y":
+            y = synth.latent(24, "ffn/y", 160, 16, 24)
+            net = model.SynthesisPrimary.load(p, "hop", eng)
+            out = net.forward(eng, nn.BTensor.from_planar(eng, y), 256, 384)
+        else:
+            y = synth.latent(24, "ffn/y", 160, 16, 12)
+            uv = synth.latent(24, "ffn/uv", 96, 16, 12)
+            net = model.SynthesisSecondary.load(p, "hop", eng)
+            out = net.forward(eng, nn.BTensor.from_planar(eng, y), nn.BTensor.from_planar(eng, uv), 256, 192)
+        names.append([r[0] for r in eng.profile_end()])
+        outs.append(out)
+    dim = 128 if comp == "y" else 64
+    assert sum(n.startswith("k_ffn<") and n.endswith(f", {dim}>") for n in names[0]) == 2
+    assert not any(n.startswith("k_ffn") for n in names[1])
+    assert np.isfinite(outs[0]).all()
+    np.testing.assert_array_equal(outs[0], outs[1])
+    fused.close()
+    plain.close()
 
 
 def _picture(eng, op, h, w, tiling, regions, sv, sh, bits, seed, gain=0.5):

@@ -74,9 +74,10 @@ TensorP planar_upload(Context& c, const float* data, int ch, int h, int w, int d
 
 // ------------------------------------------------------------------------------- context
 extern "C" int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out) {
-    (void)flags;
     if (!out) return ZJAI_E_INVALID_ARGUMENT;
     *out = nullptr;
+    if (flags & ~ZJAI_CTX_UNFUSED_FFN)
+        return guard(nullptr, [] { throw Error(ZJAI_E_INVALID_ARGUMENT, "zjai_ctx_create: unknown flags"); });
     zjai_ctx* ctx = new (std::nothrow) zjai_ctx();
     if (!ctx) return ZJAI_E_LIMIT;
     const int32_t rc = guard(nullptr, [&] {
@@ -91,6 +92,7 @@ extern "C" int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** ou
             throw Error(ZJAI_E_UNSUPPORTED, std::string("kernels are built for gfx950, device is ") + prop.gcnArchName);
         ZJAI_HIP(hipSetDevice(device));
         ctx->c.device = device;
+        ctx->c.flags = flags;
         ZJAI_HIP(hipStreamCreateWithFlags(&ctx->c.stream, hipStreamNonBlocking));
         ZJAI_HIP(hipEventCreate(&ctx->c.ev0));
         ZJAI_HIP(hipEventCreate(&ctx->c.ev1));

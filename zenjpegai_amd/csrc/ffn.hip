@@ -1,0 +1,394 @@
+// The feed-forward half of a transformer block as one kernel (16-bit storage types):
+//   u = LayerNorm(x); p = project_in(u) (1x1, dim -> 2 * hid); d = depthwise3x3(p);
+//   g = elu(d[:hid]) * d[hid:]; y = x + project_out(g) (1x1, hid -> dim)
+// (TransformerBlock::forward, src/model/attention.rs:346-369; LayerNorm :267-279).
+//
+// Unfused, the 2 * hid = 8 * dim channel tensor p and the hid-channel g make the round trip to
+// HBM (6.8 KB per position at dim 128 in bf16, against 0.5 KB for x and y); here they never
+// leave the workgroup. One workgroup (8 waves) owns a 14 x 14 output tile and its 16 x 16 halo
+// (256 positions):
+//   1. loads x over the halo, LayerNorms every halo position into LDS (u, storage type);
+//   2. for each slice of 32 gate pairs (p channels j and hid + j, j in [32 s, 32 s + 32)):
+//      a. p slice [256 positions x 64 channels] = u x W_in slice on v_mfma_f32_16x16x32
+//         (bias first, then K in 32-channel chunks: the unfused 1x1 conv's instruction
+//         sequence), rounded to the storage type, zero outside the picture (the depthwise
+//         conv's zero padding) -> LDS;
+//      b. depthwise 3x3 + ELU gate on the 14 x 14 interior (f32 FMAs in the unfused kernel's
+//         order), rounded to the storage type -> LDS;
+//      c. y accumulators [dim x 196] += W_out slice x g slice on v_mfma_f32_16x16x32 (the
+//         slice is the packed project_out weight's K chunk s, so K runs in channel order).
+//   3. adds the residual x and stores y through an LDS transpose (whole channel runs per
+//      position).
+// Every intermediate is rounded to the storage type exactly where the unfused path stores it
+// and every sum runs in the unfused kernels' order, so the two paths agree bit for bit.
+// The weights of slice s + 1 are fetched into registers while slice s computes.
+
+#include "mfma.h"
+#include "ops.h"
+
+namespace zjai {
+
+namespace {
+
+constexpr int FT = 14;          // output tile side
+constexpr int FH = FT + 2;      // halo side
+constexpr int FNP = FH * FH;    // halo positions (256: sixteen 16-position MFMA blocks)
+constexpr int FOP = FT * FT;    // output positions (196)
+constexpr int FPB = 13;         // 16-position blocks covering the output positions
+constexpr int FTHREADS = 512;
+
+template <typename T>
+__device__ __forceinline__ void unpack8(u32x4 v, float (&o)[8]) {
+    typedef T t8 __attribute__((ext_vector_type(8)));
+    const t8 hv = __builtin_bit_cast(t8, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (float)hv[i];
+}
+
+template <typename T>
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
+    typedef T t8 __attribute__((ext_vector_type(8)));
+    t8 hv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) hv[i] = (T)f[i];
+    return __builtin_bit_cast(u32x4, hv);
+}
+
+template <typename T>
+__device__ __forceinline__ void unpack2(unsigned v, float (&o)[2]) {
+    typedef T t2 __attribute__((ext_vector_type(2)));
+    const t2 hv = __builtin_bit_cast(t2, v);
+    o[0] = (float)hv[0];
+    o[1] = (float)hv[1];
+}
+
+}  // namespace
+
+template <typename T, int DIM>
+__global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
+    constexpr int HID = 4 * DIM, C2 = 2 * HID, NS = HID / 32;
+    constexpr int UPR = DIM / 8;  // 16-byte units per u / W_in row
+    // u / W_in rows: unit q of row r sits at q ^ key(r), so that the 16 rows one half-wave
+    // reads for an MFMA fragment cover all 16 four-bank groups.
+    constexpr int KSH = DIM == 128 ? 0 : 1;
+    constexpr int CB2 = DIM / 16, WPC = 8 / CB2, NPB = (FPB + WPC - 1) / WPC;
+    constexpr int U_U = FNP * UPR, WIN_U = 64 * UPR, P_U = FNP * 8, G_U = FPB * 16 * 4, WO_U = DIM * 4;
+    constexpr int WIN_PT = WIN_U / FTHREADS, LN_PT = U_U / FTHREADS;
+    static_assert(WIN_U % FTHREADS == 0 && U_U % FTHREADS == 0 && WO_U <= FTHREADS, "fetch shapes");
+    static_assert(FOP * (DIM + 4) * 4 <= (U_U + WIN_U + P_U) * 16, "output transpose fits");
+    __shared__ u32x4 s_lds[U_U + WIN_U + P_U + G_U + 2 * WO_U];
+    __shared__ float s_stat[2 * FNP];
+    u32x4* s_u = s_lds;
+    u32x4* s_win = s_u + U_U;
+    u32x4* s_p = s_win + WIN_U;
+    u32x4* s_g = s_p + P_U;
+    u32x4* s_wo = s_g + G_U;
+    auto key = [](int r) { return (r >> KSH) & (UPR - 1); };
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;  // 16x16 MFMA fragment lane
+    const int bid = (int)blockIdx.x;
+    const int tx = bid % p.gx, ty = (bid / p.gx) % p.gy, b = bid / (p.gx * p.gy);
+    const int y0 = ty * FT, x0 = tx * FT;
+    const T* xb = (const T*)p.x.p + (long long)b * p.x.bstride + p.x.c_off;
+    const T* w_in = (const T*)p.w_in;
+    const T* w_out = (const T*)p.w_out;
+
+    // Slice s weights: W_in rows j and hid + j (j in [32 s, 32 s + 32)) of the packed 1x1
+    // weight [chunk][nblk][16][32]; W_out = chunk s of the packed project_out weight.
+    u32x4 rwi[WIN_PT], rwo = {0u, 0u, 0u, 0u};
+    auto fetch_w = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < WIN_PT; ++i) {
+            const int u = tid + i * FTHREADS, r = u / UPR, q = u % UPR;
+            const int o = r < 32 ? 32 * s + r : HID + 32 * s + (r - 32);
+            const long long off = ((long long)((q >> 2) * p.nblk_in + (o >> 4)) * 16 + (o & 15)) * 32 + (q & 3) * 8;
+            rwi[i] = *(const u32x4*)(w_in + off);
+        }
+        if (tid < WO_U) {
+            const int r = tid >> 2, q = tid & 3;
+            const long long off = ((long long)(s * p.nblk_out + (r >> 4)) * 16 + (r & 15)) * 32 + q * 8;
+            rwo = *(const u32x4*)(w_out + off);
+        }
+    };
+    auto put_w = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < WIN_PT; ++i) {
+            const int u = tid + i * FTHREADS, r = u / UPR, q = u % UPR;
+            s_win[r * UPR + (q ^ key(r))] = rwi[i];
+        }
+        if (tid < WO_U) s_wo[(s & 1) * WO_U + tid] = rwo;
+    };
+
+    // ---- 1. x over the halo (zero outside the picture), then LayerNorm in place.
+    fetch_w(0);
+#pragma unroll
+    for (int i = 0; i < LN_PT; ++i) {
+        const int u = tid + i * FTHREADS, pos = u / UPR, q = u % UPR;
+        const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (iy >= 0 && iy < p.h && ix >= 0 && ix < p.w)
+            v = *(const u32x4*)(xb + (long long)iy * p.x.row + (long long)ix * p.x.cs + q * 8);
+        s_u[pos * UPR + (q ^ key(pos))] = v;
+    }
+    __syncthreads();
+    if (tid < FNP) {
+        // k_layer_norm's statistics: f64 sums in channel order.
+        const int pos = tid;
+        double mean = 0.0;
+        for (int q = 0; q < UPR; ++q) {
+            float f[8];
+            unpack8<T>(s_u[pos * UPR + (q ^ key(pos))], f);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) mean += (double)f[k];
+        }
+        mean /= (double)DIM;
+        double var = 0.0;
+        for (int q = 0; q < UPR; ++q) {
+            float f[8];
+            unpack8<T>(s_u[pos * UPR + (q ^ key(pos))], f);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const double e = (double)f[k] - mean;
+                var = var + e * e;
+            }
+        }
+        s_stat[pos] = (float)mean;
+        s_stat[FNP + pos] = sqrtf((float)(var / (double)DIM) + 1e-5f);
+    }
+    __syncthreads();
+    {
+        const int q = tid % UPR;  // the same unit for every i (FTHREADS % UPR == 0)
+        float lw[8], lb[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            lw[k] = p.ln_w[q * 8 + k];
+            lb[k] = p.ln_b[q * 8 + k];
+        }
+#pragma unroll
+        for (int i = 0; i < LN_PT; ++i) {
+            const int pos = (tid + i * FTHREADS) / UPR;
+            u32x4* a = &s_u[pos * UPR + (q ^ key(pos))];
+            float f[8];
+            unpack8<T>(*a, f);
+            const float m = s_stat[pos], d = s_stat[FNP + pos];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                float e = f[k] - m;
+                e = e / d;
+                e = e * lw[k];
+                f[k] = e + lb[k];
+            }
+            *a = pack8<T>(f);
+        }
+    }
+    put_w(0);
+
+    // ---- 2. slices of 32 gate pairs.
+    const int cb1 = wave & 1;            // GEMM1 half (0: first-half channels, 1: second half)
+    const int pb1 = wave >> 1;           // GEMM1 position blocks 4 pb1 .. 4 pb1 + 3
+    const int cb2 = wave % CB2;          // GEMM2 output-channel block
+    const int pw2 = wave / CB2;          // GEMM2 position blocks pw2 + WPC * i
+    f32x4 acc2[NPB];
+    {
+        f32x4 bo;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bo[r] = p.b_out ? p.b_out[cb2 * 16 + 4 * grp + r] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPB; ++i) acc2[i] = bo;
+    }
+    // Depthwise role: thread (pair group pg, column c, row half rh) for tid < 28 * 16.
+    const int pg = tid & 15, dc = (tid >> 4) % FT, rh = (tid >> 4) / FT;
+    const bool dw_thread = tid < 2 * FT * 16;
+
+    for (int s = 0; s < NS; ++s) {
+        __syncthreads();  // u, W_in(s), W_out(s) ready; g and p free
+        if (s + 1 < NS) fetch_w(s + 1);
+
+        // a. p slice = bias + u x W_in: the two 16-channel blocks of half cb1 (0: channels
+        //    32 s .., 1: hid + 32 s ..) x position blocks 4 pb1 .. 4 pb1 + 3.
+        //    16x16x32 MFMAs with K in 32-channel chunks, bias first: the unfused 1x1 conv's
+        //    instruction sequence, so p matches it bit for bit.
+        f32x4 acc1[2][4];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            f32x4 bi;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int cl = c * 16 + 4 * grp + r;  // channel within the half
+                const int o = cb1 ? HID + 32 * s + cl : 32 * s + cl;
+                bi[r] = p.b_in ? p.b_in[o] : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc1[c][i] = bi;
+        }
+#pragma unroll
+        for (int kc = 0; kc < DIM / 32; ++kc) {
+            const int q = 4 * kc + grp;
+            u32x4 a[2], bv[4];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int ra = cb1 * 32 + c * 16 + col;
+                a[c] = s_win[ra * UPR + (q ^ key(ra))];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rb = (pb1 * 4 + i) * 16 + col;
+                bv[i] = s_u[rb * UPR + (q ^ key(rb))];
+            }
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) Mma16<T>::run(acc1[c][i], a[c], bv[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int pos = (pb1 * 4 + i) * 16 + col;
+            const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
+            const bool inside = iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
+            const int sw = ((pos >> 1) & 1) << 2;  // a/b unit swap of odd row pairs (see dw reads)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                typedef T t4 __attribute__((ext_vector_type(4)));
+                t4 v;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[k] = inside ? (T)acc1[c][i][k] : (T)0.0f;
+                const int ch = cb1 * 32 + c * 16 + 4 * grp;  // local channel (0..63)
+                T* dst = (T*)s_p + pos * 64 + ((ch >> 3) ^ sw) * 8 + (ch & 7);
+                *reinterpret_cast<t4*>(dst) = v;
+            }
+        }
+        __syncthreads();  // p ready; W_in(s) consumed
+        if (s + 1 < NS) put_w(s + 1);
+
+        // b. depthwise 3x3 + gate: rows 7 rh .. 7 rh + 6 of column dc, pairs 32 s + 2 pg + {0, 1}.
+        if (dw_thread) {
+            const int ja = 32 * s + 2 * pg;
+            float wa[9][2], wb[9][2], ba[2], bb[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                ba[k] = p.dw_b ? p.dw_b[ja + k] : 0.0f;
+                bb[k] = p.dw_b ? p.dw_b[HID + ja + k] : 0.0f;
+#pragma unroll
+                for (int tp = 0; tp < 9; ++tp) {
+                    wa[tp][k] = p.dw_w[tp * C2 + ja + k];
+                    wb[tp][k] = p.dw_w[tp * C2 + HID + ja + k];
+                }
+            }
+            // 16-byte unit (pg / 4) of the first half, 4 + pg / 4 of the second, swapped on odd
+            // row pairs: the 16 lanes of a position read 64 contiguous bytes, and four
+            // consecutive positions land on disjoint bank groups.
+            auto ld = [&](int hr, int kx, float (&oa)[2], float (&ob)[2]) {
+                const int pos = hr * FH + dc + kx;
+                const int sw = ((pos >> 1) & 1) << 2;
+                const T* row = (const T*)s_p + pos * 64 + 2 * (pg & 3);
+                unpack2<T>(*(const unsigned*)(row + ((pg >> 2) ^ sw) * 8), oa);
+                unpack2<T>(*(const unsigned*)(row + ((4 + (pg >> 2)) ^ sw) * 8), ob);
+            };
+            float xa[3][3][2], xb[3][3][2];
+            const int r0 = rh * (FT / 2);
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                ld(r0, kx, xa[0][kx], xb[0][kx]);
+                ld(r0 + 1, kx, xa[1][kx], xb[1][kx]);
+            }
+#pragma unroll
+            for (int r = 0; r < FT / 2; ++r) {
+                const int oy = r0 + r;
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx) ld(oy + 2, kx, xa[2][kx], xb[2][kx]);
+                float g[2];
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    float a = ba[k], bq = bb[k];
+#pragma unroll
+                    for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+                        for (int kx = 0; kx < 3; ++kx) {
+                            a = fmaf(wa[ky * 3 + kx][k], xa[ky][kx][k], a);
+                            bq = fmaf(wb[ky * 3 + kx][k], xb[ky][kx][k], bq);
+                        }
+                    const float e = cephes_exp(a) - 1.0f;
+                    const float elu = a > 0.0f ? a : e;
+                    g[k] = elu * bq;
+                }
+                typedef T t2 __attribute__((ext_vector_type(2)));
+                *reinterpret_cast<t2*>((T*)s_g + (oy * FT + dc) * 32 + 2 * pg) = t2{(T)g[0], (T)g[1]};
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx)
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        xa[0][kx][k] = xa[1][kx][k];
+                        xa[1][kx][k] = xa[2][kx][k];
+                        xb[0][kx][k] = xb[1][kx][k];
+                        xb[1][kx][k] = xb[2][kx][k];
+                    }
+            }
+        }
+        __syncthreads();  // g ready
+
+        // c. y += W_out(s) x g (output-channel block cb2, position blocks pw2 + WPC * i).
+        const u32x4 a = s_wo[(s & 1) * WO_U + (cb2 * 16 + col) * 4 + grp];
+#pragma unroll
+        for (int i = 0; i < NPB; ++i) {
+            const int pb = pw2 + WPC * i;
+            if (pb < FPB) Mma16<T>::run(acc2[i], a, s_g[(pb * 16 + col) * 4 + grp]);
+        }
+    }
+
+    // ---- 3. y = acc + x through an LDS transpose.
+    __syncthreads();
+    constexpr int OLD = DIM + 4;
+    float* so = reinterpret_cast<float*>(s_lds);
+#pragma unroll
+    for (int i = 0; i < NPB; ++i) {
+        const int pb = pw2 + WPC * i, pos = pb * 16 + col;
+        if (pb < FPB && pos < FOP) {
+            float* d = so + pos * OLD + cb2 * 16 + 4 * grp;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) d[r] = acc2[i][r];
+        }
+    }
+    __syncthreads();
+    T* yb = (T*)p.y.p + (long long)b * p.y.bstride + p.y.c_off;
+    for (int u = tid; u < FOP * (DIM / 4); u += FTHREADS) {
+        const int pos = u / (DIM / 4), q = u % (DIM / 4);
+        const int oy = y0 + pos / FT, ox = x0 + pos % FT;
+        if (oy >= p.h || ox >= p.w) continue;
+        const float* sv = so + pos * OLD + q * 4;
+        f32x4 v = {sv[0], sv[1], sv[2], sv[3]};
+        const f32x4 r = load4<T>(xb + (long long)oy * p.x.row + (long long)ox * p.x.cs + q * 4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = v[k] + r[k];
+        store4<T>(yb + (long long)oy * p.y.row + (long long)ox * p.y.cs + q * 4, v);
+    }
+}
+
+bool ffn_fused_supported(int dtype, int dim) {
+    return (dtype == DT_F16 || dtype == DT_BF16) && (dim == 64 || dim == 128);
+}
+
+hipError_t launch_ffn_fused(const FfnArgs& a, int dtype, int dim, hipStream_t s) {
+    if (!ffn_fused_supported(dtype, dim)) return hipErrorInvalidValue;
+    // 16-byte vector accesses of x and y.
+    if (a.x.cs % 8 || a.x.c_off % 8 || a.x.row % 8 || a.x.bstride % 8 || a.y.cs % 8 || a.y.c_off % 8 ||
+        a.y.row % 8 || a.y.bstride % 8)
+        return hipErrorInvalidValue;
+    if (a.N <= 0 || a.h <= 0 || a.w <= 0) return hipSuccess;
+    FfnArgs p = a;
+    p.gx = (a.w + FT - 1) / FT;
+    p.gy = (a.h + FT - 1) / FT;
+    const long long blocks = (long long)p.gx * p.gy * a.N;
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)blocks), block(FTHREADS);
+    if (dtype == DT_BF16) {
+        if (dim == 128) k_ffn<__bf16, 128><<<grid, block, 0, s>>>(p);
+        else k_ffn<__bf16, 64><<<grid, block, 0, s>>>(p);
+    } else {
+        if (dim == 128) k_ffn<_Float16, 128><<<grid, block, 0, s>>>(p);
+        else k_ffn<_Float16, 64><<<grid, block, 0, s>>>(p);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace zjai

@@ -253,6 +253,27 @@ struct Fwd {
                                    net.vec.at(pfx + ".bias"), ctx.stream));
         return y;
     }
+    // The fused feed-forward kernel applies to 16-bit nets with dim 64 / 128 whose 1x1 weights
+    // are packed unpadded (K chunks of 32 channels, 16-row blocks) and whose input is a whole
+    // 16-byte-aligned NHWC tensor.
+    bool ffn_fusable(const std::string& p, const TensorP& x) {
+        if (ctx.top().flags & ZJAI_CTX_UNFUSED_FFN) return false;
+        const int dim = x->c, hidden = 4 * dim;
+        if (!ffn_fused_supported(x->dtype, dim)) return false;
+        const Layer& pin = L(p + ".ffn.project_in");
+        const Layer& dwl = L(p + ".ffn.dwconv");
+        const Layer& pout = L(p + ".ffn.project_out");
+        const int ck = 64 / dtype_size(x->dtype);
+        if (pin.kind != CK_1x1 || pin.groups != 1 || pin.transposed || pin.dtype != x->dtype ||
+            pin.nblk_g * 16 != 2 * hidden || pin.nchunks * ck != dim || pin.cin != dim)
+            return false;
+        if (pout.kind != CK_1x1 || pout.groups != 1 || pout.transposed || pout.dtype != x->dtype ||
+            pout.nblk_g * 16 != dim || pout.nchunks * ck != hidden || pout.cin != hidden)
+            return false;
+        if (!dwl.depthwise || dwl.cin != 2 * hidden || !dwl.dw_w) return false;
+        const View& v = x->v;
+        return v.cs % 8 == 0 && v.c_off % 8 == 0 && v.row % 8 == 0 && v.bstride % 8 == 0;
+    }
     // TransformerBlock::forward (src/model/attention.rs:328-372)
     TensorP transformer_block(const std::string& p, TensorP x) {
         const int dim = x->c, heads = 4, hidden = 4 * dim;
@@ -270,6 +291,35 @@ struct Fwd {
         conv(p + ".attn.project_out", channel_view(t, 2 * dim, dim), ea, x);
         t.reset();
         // x = x + ffn(x)
+        if (ffn_fusable(p, x)) {
+            const Layer& pin = L(p + ".ffn.project_in");
+            const Layer& dwl = L(p + ".ffn.dwconv");
+            const Layer& pout = L(p + ".ffn.project_out");
+            TensorP y = ctx.alloc(x->n, dim, x->h, x->w, x->dtype);
+            FfnArgs a{};
+            a.x = x->v;
+            a.y = y->v;
+            a.N = x->n;
+            a.h = x->h;
+            a.w = x->w;
+            a.ln_w = net.vec.at(p + ".ffn.norm1.weight");
+            a.ln_b = net.vec.at(p + ".ffn.norm1.bias");
+            a.w_in = pin.wpk;
+            a.nblk_in = pin.nblk_g;
+            a.b_in = pin.bias;
+            a.dw_w = dwl.dw_w;
+            a.dw_b = dwl.bias;
+            a.w_out = pout.wpk;
+            a.nblk_out = pout.nblk_g;
+            a.b_out = pout.bias;
+            const double npos = (double)x->n * x->h * x->w;
+            const std::string kn = kname("k_ffn", x->dtype);
+            LaunchScope sc(ctx, kn.substr(0, kn.size() - 1) + ", " + std::to_string(dim) + ">",
+                           2.0 * npos * (2.0 * hidden * dim + 9.0 * 2 * hidden + (double)hidden * dim),
+                           2.0 * dtype_size(x->dtype) * npos * dim);
+            ZJAI_HIP(launch_ffn_fused(a, x->dtype, dim, ctx.stream));
+            return y;
+        }
         TensorP u = layer_norm(p + ".ffn.norm1", x);
         u = conv(p + ".ffn.project_in", u);
         const Layer& dw = L(p + ".ffn.dwconv");

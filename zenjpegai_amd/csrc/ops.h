@@ -47,6 +47,27 @@ hipError_t launch_depthwise3x3(View src, View dst, int dtype, int N, int C, int 
 // Layer norm over channels per position (f64 sums), src -> dst.
 hipError_t launch_layer_norm(View src, View dst, int dtype, int N, int C, int h, int w,
                              const float* weight, const float* bias, hipStream_t s);
+// The feed-forward half of a transformer block in one kernel (16-bit storage types, dim 64 or
+// 128): y = x + project_out(elu(dw(project_in(LN(x)))[:hid]) * dw(...)[hid:]), hid = 4 * dim.
+// Weights: the packed 1x1 layers ([chunk][nblk][16][32], storage type) and the depthwise
+// [9][2 * hid] f32. y must not alias x (neighbouring tiles read x over their halos).
+struct FfnArgs {
+    View x, y;
+    int N, h, w;
+    int gx, gy;  // tile grid (set by the launcher)
+    const float* ln_w;
+    const float* ln_b;
+    const void* w_in;  // project_in: dim -> 2 * hid
+    int nblk_in;
+    const float* b_in;
+    const float* dw_w;
+    const float* dw_b;
+    const void* w_out;  // project_out: hid -> dim
+    int nblk_out;
+    const float* b_out;
+};
+bool ffn_fused_supported(int dtype, int dim);
+hipError_t launch_ffn_fused(const FfnArgs& a, int dtype, int dim, hipStream_t s);
 // Channel attention (src/nn/fast/math.rs:512-603), three phases per batch item:
 // 1. per-head Gram partial sums over chunks of positions (f32 MFMA): qkv view holds 3*dim
 //    channels; partial[N][nchunk][heads][c*c + 2c] f32 (c = dim / heads <= 32);

@@ -79,6 +79,7 @@ struct ProfRec {
 
 struct Context {
     int device = 0;
+    uint32_t flags = 0;  // ZJAI_CTX_* (read from the root context)
     hipStream_t stream = nullptr;
     // The pool is shared with every tensor allocated from it, so a tensor that outlives its
     // context (a caller destroying the context first) still returns its block to a live pool.

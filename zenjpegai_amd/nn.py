@@ -84,11 +84,13 @@ class Engine:
     """The HIP counterpart of ``nn::fast::Engine`` (src/nn/fast/mod.rs:128-172): one context
     (device + stream) and the precision layers are packed for ("f32", "f16" or "bf16")."""
 
-    def __init__(self, device: int = 0, precision: str = "f32"):
+    def __init__(self, device: int = 0, precision: str = "f32", flags: int = 0):
+        """``flags``: 0 or ``_lib.CTX_UNFUSED_FFN`` (the transformer blocks' feed-forward half
+        as separate kernels instead of the fused one the 16-bit precisions use)."""
         self.precision = precision
         self.dtype = _lib.PRECISIONS[precision]
         self._h = ctypes.c_void_p()
-        check(lib().zjai_ctx_create(device, 0, ctypes.byref(self._h)), None)
+        check(lib().zjai_ctx_create(device, flags, ctypes.byref(self._h)), None)
 
     @property
     def handle(self):
