@@ -45,8 +45,10 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_workload(name, eng, lanes=1):
+def make_workload(name, eng, lanes=1, bits=None):
+    """``bits``: output bit depth override (0 = float planes)."""
     from zenjpegai_amd import model, synth
+    bits_override = bits
     if name == "cfg5":
         h, w, op, sv, sh, bits = 2160, 3840, "hop", 2, 2, 10
         lh, lw = 135, 240
@@ -74,6 +76,8 @@ def make_workload(name, eng, lanes=1):
         puv = synth.random_params(op, "uv", seed=1)
         sec = model.SynthesisSecondary.load(puv, op, eng)
         uvl = synth.latent(1, f"{name}/uv", 96, lh, lw)
+    if bits_override is not None:
+        bits = bits_override
     pic = model.Picture(eng, prim, sec, lh, lw, h, w, tiles, sv, sh, bit_depth=bits, lanes=lanes)
     pic.upload(y, uvl)
     return pic, dict(h=h, w=w, op=op, tiles=len(tiles), bits=bits, sv=sv, sh=sh,
@@ -108,6 +112,28 @@ def profile_step(eng, pic):
         d["flops"] += flops
         d["bytes"] += nbytes
     return by
+
+
+def rgb_output_stage(prec, lanes, reps=5):
+    """The decoder's output stage for a BT.709 stream on the config-5 picture (float planes):
+    bicubic 4:2:0 -> 4:4:4 chroma, BT.709 -> RGB, clip, 10-bit quantisation, one kernel.
+    Kernel time from HIP events (best of ``reps``); bytes are the luma read, the chroma planes
+    read once and the interleaved uint16 RGB written."""
+    from zenjpegai_amd import nn
+    eng = nn.Engine(0, prec)
+    pic, info = make_workload("cfg5", eng, lanes, bits=0)
+    pic.run()
+    best = None
+    for _ in range(reps):
+        eng.profile_begin()
+        pic.download_rgb(10)
+        recs = [r for r in eng.profile_end() if r[0] == "k_picture_rgb"]
+        best = recs[0] if best is None or recs[0][3] < best[3] else best
+    n = info["h"] * info["w"]
+    nbytes = n * (4 + 6) + 2 * 4 * (-(-info["h"] // 2)) * (-(-info["w"] // 2))
+    us = best[3] * 1e3
+    return {"kernel_us": round(us, 2), "algorithmic_GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "mpix_s": round(n / (us * 1e-6) / 1e6, 1)}
 
 
 def layer_configs(prec, reps=10):
@@ -311,6 +337,9 @@ def main():
                 extra[f"hop_4mp_2048sq_{prec}_mpix_s"] = round(i4["h"] * i4["w"] / (ms4 / 1e3) / 1e6, 3)
                 log(f"[bench] hop 4 MP {prec}: {ms4:.2f} ms/step")
                 del p4, e4
+        if args.workload == "cfg5":
+            extra["rgb_output_stage_cfg5"] = rgb_output_stage(args.precision, args.lanes)
+            log(f"[bench] RGB output stage: {extra['rgb_output_stage_cfg5']}")
         for prec in ("f32", "bf16"):
             extra.update(layer_configs(prec))
         log("[bench] configs 1-3: " + ", ".join(f"{k}={v}" for k, v in extra.items() if k.startswith("cfg") and "tflops" in k))

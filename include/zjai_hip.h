@@ -253,6 +253,26 @@ ZJAI_API int32_t zjai_picture_set_lanes(zjai_ctx* ctx, zjai_picture* pic, int32_
  * samples each, as float (bit_depth 0) or uint16. u/v may be NULL without net_uv. */
 ZJAI_API int32_t zjai_picture_download(zjai_ctx* ctx, zjai_picture* pic, void* y, void* u, void* v);
 
+/* ------------------------------------------------------------------------ output stage */
+
+#define ZJAI_RESIZE_BICUBIC 0  /* decoder::output::resize_bicubic (src/decoder/output.rs:117) */
+#define ZJAI_RESIZE_BILINEAR 1 /* nn::resize_bilinear (src/nn/resample.rs:43) */
+
+/* `F.interpolate(x, (out_h, out_w), mode, align_corners=True)` with PyTorch's CPU arithmetic, as
+ * the reference restates it (the resamplers behind `Image.to_444_` / `to_420_` / `to_422_`):
+ * host planar [c][h][w] f32 -> host planar [c][out_h][out_w] f32 (synchronises). Empty input
+ * sizes are ZJAI_E_INVALID_ARGUMENT, like the reference. */
+ZJAI_API int32_t zjai_resize(zjai_ctx* ctx, int32_t mode, const float* src, int32_t c, int32_t h,
+                             int32_t w, int32_t out_h, int32_t out_w, float* dst);
+/* The decoder's output stage for a BT.709 stream on the device: `to_source_format`
+ * (src/decoder/output.rs:153-199, chroma bicubic to 4:4:4) then `finish` (:346-366:
+ * `to_rgb_planes`, clip, `quantize` with round half to even) over a picture run with float
+ * planes (bit_depth 0 at zjai_picture_create) and a chroma net. Writes interleaved RGB
+ * uint16 [out_h][out_w][3] at bit_depth 8 or 10 and, when rgb_planes is not NULL, the float
+ * planes [3][out_h][out_w] in [0, 255] (the reference's `RgbPlanes`). Synchronises. */
+ZJAI_API int32_t zjai_picture_download_rgb(zjai_ctx* ctx, zjai_picture* pic, int32_t bit_depth,
+                                           uint16_t* rgb, float* rgb_planes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,6 +75,11 @@ def lib():
         L.fc_threads.restype = ctypes.c_int
         L.fc_force_tier.restype = ctypes.c_int
         L.fc_force_tier.argtypes = [ctypes.c_int]
+        for name in ("or_resize_bicubic", "or_resize_bilinear"):
+            getattr(L, name).argtypes = [_f32p] + [ctypes.c_int] * 5 + [_f32p]
+            getattr(L, name).restype = ctypes.c_int
+        L.or_yuv_to_rgb.argtypes = [_f32p, _f32p, _f32p, ctypes.c_long, _f32p, _f32p, _f32p]
+        L.or_quantize_rgb.argtypes = [_f32p, _f32p, _f32p, ctypes.c_long, ctypes.c_int, _u16p]
         _lib = L
     return _lib
 
@@ -226,6 +231,60 @@ def quantize_plane(x, bit_depth):
     out = np.empty(x.shape, np.uint16)
     lib().or_quantize_plane(_p(x), x.size, bit_depth, out.ctypes.data_as(_u16p))
     return out
+
+
+def resize_bicubic(x, oh, ow):
+    """``F.interpolate(x, (oh, ow), mode="bicubic", align_corners=True)`` as the reference's
+    ``decoder::output::resize_bicubic`` (src/decoder/output.rs:100-147) computes it; x is
+    [c][h][w]."""
+    x = _c(x)
+    c, h, w = x.shape
+    y = np.empty((c, oh, ow), np.float32)
+    if lib().or_resize_bicubic(_p(x), c, h, w, oh, ow, _p(y)):
+        raise ValueError("resize: empty input")
+    return y
+
+
+def resize_bilinear(x, oh, ow):
+    """``nn::resize_bilinear`` (src/nn/resample.rs:43-69), align_corners; x is [c][h][w]."""
+    x = _c(x)
+    c, h, w = x.shape
+    y = np.empty((c, oh, ow), np.float32)
+    if lib().or_resize_bilinear(_p(x), c, h, w, oh, ow, _p(y)):
+        raise ValueError("resize: empty dimension")
+    return y
+
+
+def yuv_to_rgb(y, u, v):
+    """BT.709 4:4:4 planes in [0, 255] -> clipped RGB planes (src/decoder/output.rs:232-257)."""
+    y, u, v = _c(y), _c(u), _c(v)
+    assert y.shape == u.shape == v.shape
+    r, g, b = (np.empty(y.shape, np.float32) for _ in range(3))
+    lib().or_yuv_to_rgb(_p(y), _p(u), _p(v), y.size, _p(r), _p(g), _p(b))
+    return r, g, b
+
+
+def quantize_rgb(r, g, b, bit_depth):
+    """Interleaved [h][w][3] uint16 RGB samples (src/decoder/output.rs:407-437)."""
+    r, g, b = _c(r), _c(g), _c(b)
+    out = np.empty(r.shape + (3,), np.uint16)
+    lib().or_quantize_rgb(_p(r), _p(g), _p(b), r.size, bit_depth, out.ctypes.data_as(_u16p))
+    return out
+
+
+def picture_rgb(y, u, v, bit_depth):
+    """`finish` for a BT.709 stream (src/decoder/output.rs:346-366) after `to_source_format`
+    (:153-199): chroma planes of any coded subsampling are bicubic-resampled to the luma size,
+    converted and quantised. Returns (interleaved uint16 RGB, float RGB planes)."""
+    y = _c(y)
+    h, w = y.shape
+    u = _c(u)[None]
+    v = _c(v)[None]
+    if u.shape[1:] != (h, w):
+        u = resize_bicubic(u, h, w)
+        v = resize_bicubic(v, h, w)
+    r, g, b = yuv_to_rgb(y, u[0], v[0])
+    return quantize_rgb(r, g, b, bit_depth), np.stack([r, g, b])
 
 
 def f32_to_f16_bits(v: float) -> int:

@@ -389,4 +389,161 @@ void or_f16_round_trip(const float* x, long n, float* y) {
     for (long i = 0; i < n; ++i) y[i] = or_f16_to_f32(or_f32_to_f16(x[i]));
 }
 
+// ---------------------------------------------------------------------------------------------
+// Output stage (src/decoder/output.rs). Chroma resampling restates PyTorch's CPU kernels as the
+// reference pins them operation for operation:
+//   * bicubic, align_corners (`resize_bicubic`, :100-147): per output coordinate scale =
+//     (in - 1) / (out - 1), real = scale * dst, base = floor(real), t = real - base, taps
+//     clamp(base - 1 + k); A = -0.75 cubic weights with the fused forms of :64-79; four
+//     horizontal dot4 = fma(x3, c3, fma(x2, c2, fma(x0, c0, x1 * c1))) (:85-90), then the
+//     vertical dot4 over them;
+//   * bilinear, align_corners (`nn::resize_bilinear`, src/nn/resample.rs:22-69): i0 = (int)real,
+//     i1 = i0 + (i0 < in - 1), l1 = real - i0, l0 = 1 - l1; equal sizes map straight through;
+//     pre-multiplied corner weights accumulated fma(p0, a, p1 * b), fma(p2, c, _), fma(p3, d, _).
+// Planes are [c][h][w]; returns 0, or -1 for an empty input.
+// ---------------------------------------------------------------------------------------------
+static float or_cubic1(float x) {
+    const float A = -0.75f;
+    const float p = std::fma(A + 2.0f, x, -(A + 3.0f));
+    return std::fma(p * x, x, 1.0f);
+}
+static float or_cubic2(float x) {
+    const float A = -0.75f;
+    float p = std::fma(A, x, -5.0f * A);
+    p = std::fma(p, x, 8.0f * A);
+    return std::fma(p, x, -4.0f * A);
+}
+static float or_dot4(const float* x, const float* c) {
+    float acc = x[1] * c[1];
+    acc = std::fma(x[0], c[0], acc);
+    acc = std::fma(x[2], c[2], acc);
+    return std::fma(x[3], c[3], acc);
+}
+static void or_cubic_taps(int dst, int in_len, int out_len, int* idx, float* wt) {
+    const float scale = out_len > 1 ? (float)(in_len - 1) / (float)(out_len - 1) : 0.0f;
+    const float real = scale * (float)dst;
+    const float basef = std::floor(real);
+    const float t = real - basef;
+    const int base = (int)basef;
+    for (int k = 0; k < 4; ++k) {
+        int i = base - 1 + k;
+        i = i < 0 ? 0 : (i > in_len - 1 ? in_len - 1 : i);
+        idx[k] = i;
+    }
+    const float u = 1.0f - t;
+    wt[0] = or_cubic2(t + 1.0f);
+    wt[1] = or_cubic1(t);
+    wt[2] = or_cubic1(u);
+    wt[3] = or_cubic2(u + 1.0f);
+}
+
+int or_resize_bicubic(const float* src, int c, int h, int w, int oh, int ow, float* dst) {
+    if (h <= 0 || w <= 0) return -1;
+    std::vector<int> xi((size_t)ow * 4), yi((size_t)oh * 4);
+    std::vector<float> xw((size_t)ow * 4), yw((size_t)oh * 4);
+    for (int x = 0; x < ow; ++x) or_cubic_taps(x, w, ow, &xi[(size_t)x * 4], &xw[(size_t)x * 4]);
+    for (int y = 0; y < oh; ++y) or_cubic_taps(y, h, oh, &yi[(size_t)y * 4], &yw[(size_t)y * 4]);
+    for (int ch = 0; ch < c; ++ch) {
+        const float* sp = src + (size_t)ch * h * w;
+        float* dp = dst + (size_t)ch * oh * ow;
+        for (int y = 0; y < oh; ++y)
+            for (int x = 0; x < ow; ++x) {
+                float rows[4];
+                for (int k = 0; k < 4; ++k) {
+                    const float* row = sp + (size_t)yi[(size_t)y * 4 + k] * w;
+                    const int* ix = &xi[(size_t)x * 4];
+                    const float v[4] = {row[ix[0]], row[ix[1]], row[ix[2]], row[ix[3]]};
+                    rows[k] = or_dot4(v, &xw[(size_t)x * 4]);
+                }
+                dp[(size_t)y * ow + x] = or_dot4(rows, &yw[(size_t)y * 4]);
+            }
+    }
+    return 0;
+}
+
+static void or_linear_taps(int dst, int in_len, int out_len, int* i0, int* i1, float* l0, float* l1) {
+    if (in_len == out_len) {
+        *i0 = *i1 = dst;
+        *l0 = 1.0f;
+        *l1 = 0.0f;
+        return;
+    }
+    const float scale = out_len > 1 ? (float)(in_len - 1) / (float)(out_len - 1) : 0.0f;
+    const float real = scale * (float)dst;
+    const int a = (int)real;
+    *i0 = a;
+    *i1 = a + (a < in_len - 1 ? 1 : 0);
+    *l1 = real - (float)a;
+    *l0 = 1.0f - *l1;
+}
+
+int or_resize_bilinear(const float* src, int c, int h, int w, int oh, int ow, float* dst) {
+    if (h <= 0 || w <= 0 || oh <= 0 || ow <= 0) return -1;
+    for (int ch = 0; ch < c; ++ch) {
+        const float* sp = src + (size_t)ch * h * w;
+        float* dp = dst + (size_t)ch * oh * ow;
+        for (int y = 0; y < oh; ++y) {
+            int y0, y1;
+            float h0, h1;
+            or_linear_taps(y, h, oh, &y0, &y1, &h0, &h1);
+            for (int x = 0; x < ow; ++x) {
+                int x0, x1;
+                float w0, w1;
+                or_linear_taps(x, w, ow, &x0, &x1, &w0, &w1);
+                const float p0 = h0 * w0, p1 = h0 * w1, p2 = h1 * w0, p3 = h1 * w1;
+                const float* r0 = sp + (size_t)y0 * w;
+                const float* r1 = sp + (size_t)y1 * w;
+                float acc = std::fma(p0, r0[x0], p1 * r0[x1]);
+                acc = std::fma(p2, r1[x0], acc);
+                dp[(size_t)y * ow + x] = std::fma(p3, r1[x1], acc);
+            }
+        }
+    }
+    return 0;
+}
+
+// `to_rgb_planes_owned_par` (src/decoder/output.rs:232-257) on 4:4:4 planes: BT.709 constants
+// combined in f64 and narrowed to f32 (:27-33, :225-228); convert_range(x, a, b) =
+// ((x - 0) / a) * b + 0 (:36-40); clamp to [0, 255]. In place is allowed.
+static float or_convert_range(float x, float in_max, float out_max) {
+    float v = x - 0.0f;
+    v = v / in_max;
+    v = v * out_max;
+    return v + 0.0f;
+}
+static float or_clamp255(float v) { return v < 0.0f ? 0.0f : (v > 255.0f ? 255.0f : v); }
+
+void or_yuv_to_rgb(const float* y, const float* u, const float* v, long n, float* r, float* g,
+                   float* b) {
+    const double KR = 0.2126, KG = 0.7152, KB = 0.0722, KBY = 1.8556, KRY = 1.5748;
+    const float kry = (float)KRY, kby = (float)KBY;
+    const float gu = (float)(KB * KBY / KG), gv = (float)(KR * KRY / KG);
+    for (long i = 0; i < n; ++i) {
+        const float yy = or_convert_range(y[i], 255.0f, 1.0f);
+        const float uu = or_convert_range(u[i], 255.0f, 1.0f) - 0.5f;
+        const float vv = or_convert_range(v[i], 255.0f, 1.0f) - 0.5f;
+        const float rv = yy + kry * vv;
+        float gvv = yy - gu * uu;
+        gvv = gvv - gv * vv;
+        const float bv = yy + kby * uu;
+        r[i] = or_clamp255(or_convert_range(rv, 1.0f, 255.0f));
+        g[i] = or_clamp255(or_convert_range(gvv, 1.0f, 255.0f));
+        b[i] = or_clamp255(or_convert_range(bv, 1.0f, 255.0f));
+    }
+}
+
+// `quantize_par` (src/decoder/output.rs:407-437): interleaved [n][3] samples,
+// convert_range(x, 255, max), round half to even, clamp to [0, max].
+void or_quantize_rgb(const float* r, const float* g, const float* b, long n, int bit_depth,
+                     uint16_t* out) {
+    const float mx = (float)((1u << bit_depth) - 1);
+    const float* pl[3] = {r, g, b};
+    for (long i = 0; i < n; ++i)
+        for (int k = 0; k < 3; ++k) {
+            float v = std::rint(or_convert_range(pl[k][i], 255.0f, mx));
+            v = v < 0.0f ? 0.0f : (v > mx ? mx : v);
+            out[i * 3 + k] = (uint16_t)v;
+        }
+}
+
 }  // extern "C"

@@ -2,7 +2,8 @@
 
 Format (as `tests/nn_vectors.rs:16-48` of the reference reads it): magic ``ZJTB``, u32 LE count,
 then per array: u16 LE name length, UTF-8 name, u8 ndim, ndim x u32 LE dims, f32 LE data.
-The fixtures were produced by PyTorch 1.10.2 (`scripts/ref_vectors/gen_nn_vectors.py`).
+The fixtures were produced by PyTorch 1.10.2 (the reference's `scripts/ref_vectors/gen_nn_vectors.py`;
+`bicubic_align_corners` / `bilinear_align_corners` by its `gen_resize_vectors.py`).
 """
 
 import os

@@ -473,3 +473,89 @@ def test_fast_graph_equals_reference_graph():
         got = (og.primary(py, "hop", y, 64, 96), og.secondary(puv, "hop", y, uv, 64, 96))
     for g, wv in zip(got, want):
         assert np.array_equal(_bits(g), _bits(wv))
+
+
+# ----------------------------------------------------------------------------- output stage
+@pytest.mark.parametrize("name,mode,cases", [("bicubic_align_corners", "bicubic", 6),
+                                             ("bilinear_align_corners", "bilinear", 8)])
+def test_resize_matches_reference_fixture_exactly(name, mode, cases):
+    """The reference's PyTorch vectors (tests/nn_vectors.rs:136-196): exact up-/down-sampling,
+    odd sizes, a 4:2:2 width-only case and one-sample axes, bit for bit."""
+    t = zjtb.load(name)
+    fn = oracle.resize_bicubic if mode == "bicubic" else oracle.resize_bilinear
+    for i in range(cases):
+        x, want = t[f"x{i}"], t[f"y{i}"]
+        got = fn(x, want.shape[1], want.shape[2])
+        assert got.tobytes() == want.astype(np.float32).tobytes(), (i, x.shape, want.shape)
+
+
+def test_resize_closed_forms():
+    """Sizes that reduce the resamplers to something known: equal sizes are the identity;
+    align_corners keeps the corner samples; a constant plane stays constant (cubic weights sum
+    to 1); linear data is reproduced by bilinear (a plausible swapped weight fails this)."""
+    rng = np.random.default_rng(5)
+    x = rng.uniform(0, 255, (2, 7, 9)).astype(np.float32)
+    assert np.array_equal(oracle.resize_bilinear(x, 7, 9), x)
+    assert np.array_equal(oracle.resize_bicubic(x, 7, 9), x)
+    up = oracle.resize_bicubic(x, 13, 17)
+    assert np.array_equal(up[:, [0, 0, -1, -1], [0, -1, 0, -1]], x[:, [0, 0, -1, -1], [0, -1, 0, -1]])
+    c = np.full((1, 5, 6), 77.25, np.float32)
+    assert np.allclose(oracle.resize_bicubic(c, 9, 11), 77.25, atol=1e-4)
+    yy, xx = np.mgrid[0:6, 0:8].astype(np.float32)
+    lin = (3 * yy + 2 * xx)[None]
+    out = oracle.resize_bilinear(lin, 11, 15)
+    oy, ox = np.mgrid[0:11, 0:15].astype(np.float64)
+    want = 3 * oy * 5 / 10 + 2 * ox * 7 / 14
+    assert np.allclose(out[0], want, atol=1e-4)
+
+
+def _bt709_yuv(r, g, b):
+    """Forward BT.709 (f64): the transform `to_RGB_` inverts, on [0, 255] samples."""
+    KR, KG, KB, KBY, KRY = 0.2126, 0.7152, 0.0722, 1.8556, 1.5748
+    r, g, b = (np.asarray(a, np.float64) / 255 for a in (r, g, b))
+    y = KR * r + KG * g + KB * b
+    return y * 255, ((b - y) / KBY + 0.5) * 255, ((r - y) / KRY + 0.5) * 255
+
+
+def test_yuv_to_rgb_inverts_bt709_and_keeps_gray():
+    rng = np.random.default_rng(6)
+    rgb = rng.uniform(0, 255, (3, 64, 64))
+    y, u, v = _bt709_yuv(*rgb)
+    r, g, b = oracle.yuv_to_rgb(y, u, v)
+    assert np.abs(np.stack([r, g, b]) - rgb).max() < 2e-3
+    # u = v = 127.5 is exactly 0.5 after the range conversion: R = G = B.
+    y = rng.uniform(0, 255, (1000,)).astype(np.float32)
+    half = np.full_like(y, 127.5)
+    r, g, b = oracle.yuv_to_rgb(y, half, half)
+    assert np.array_equal(r, g) and np.array_equal(g, b)
+    assert np.abs(r - y).max() < 1e-4
+    # Out-of-gamut colours clip to [0, 255].
+    r, g, b = oracle.yuv_to_rgb(np.float32([255, 0]), np.float32([127.5, 0]), np.float32([255, 127.5]))
+    assert r[0] == 255.0 and b[1] == 0.0  # 1 + 1.5748 / 2 and 0 - 1.8556 / 2 clip
+
+
+def test_quantize_rgb_interleaves_and_rounds_half_even():
+    r = np.float32([0.0, 127.5, 255.0, 300.0])
+    g = np.float32([255.0, 0.0, 63.75, -1.0])
+    b = np.float32([1.0, 2.0, 3.0, 4.0])
+    q8 = oracle.quantize_rgb(r, g, b, 8)
+    assert q8.shape == (4, 3)
+    assert q8[:, 0].tolist() == [0, 128, 255, 255]  # 127.5 -> 128 (even), clamped at 255
+    assert q8[:, 1].tolist() == [255, 0, 64, 0]
+    q10 = oracle.quantize_rgb(r, g, b, 10)
+    assert q10[:, 0].tolist() == [0, 512, 1023, 1023]  # 0.5 * 1023 = 511.5 -> 512
+    x = np.linspace(0, 255, 4097, dtype=np.float32)
+    q = oracle.quantize_rgb(x, x, x, 10)[:, 0].astype(int)
+    assert (np.diff(q) >= 0).all() and q[0] == 0 and q[-1] == 1023
+
+
+def test_picture_rgb_upsamples_chroma_to_luma_size():
+    rng = np.random.default_rng(7)
+    y = rng.uniform(0, 255, (9, 13)).astype(np.float32)
+    u = rng.uniform(0, 255, (5, 7)).astype(np.float32)
+    v = rng.uniform(0, 255, (5, 7)).astype(np.float32)
+    q, planes = oracle.picture_rgb(y, u, v, 10)
+    uu = oracle.resize_bicubic(u[None], 9, 13)[0]
+    vv = oracle.resize_bicubic(v[None], 9, 13)[0]
+    want = np.stack(oracle.yuv_to_rgb(y, uu, vv))
+    assert np.array_equal(planes, want) and q.shape == (9, 13, 3)

@@ -34,6 +34,7 @@ OPS = {"sop": 0, "bop": 1, "hop": 2}
 ACT_NONE, ACT_RELU, ACT_LEAKY_RELU, ACT_SIGMOID = 0, 1, 2, 3
 RES_NONE, RES_ADD, RES_GATE, RES_CAB, RES_MUL = 0, 1, 2, 3, 4
 CTX_UNFUSED_FFN = 0x1  # zjai_ctx_create flag
+RESIZE_BICUBIC, RESIZE_BILINEAR = 0, 1
 
 
 class ZjaiTile(ctypes.Structure):
@@ -110,6 +111,8 @@ PROTOTYPES = {
     "zjai_picture_run": [_vp, _vp],
     "zjai_picture_set_lanes": [_vp, _vp, _i32],
     "zjai_picture_download": [_vp, _vp, _vp, _vp, _vp],
+    "zjai_resize": [_vp, _i32, _f32p, _i32, _i32, _i32, _i32, _i32, _f32p],
+    "zjai_picture_download_rgb": [_vp, _vp, _i32, _vp, _f32p],
 }
 
 _lib = None

@@ -619,6 +619,8 @@ struct zjai_picture {
     float* uv_hat = nullptr;  // device planar [96][lh][lw]
     void* out_y = nullptr;    // device planes
     void* out_uv = nullptr;   // [2][ch][cw]
+    uint16_t* out_rgb = nullptr;  // [out_h][out_w][3] (zjai_picture_download_rgb)
+    float* out_rgbf = nullptr;    // [3][out_h][out_w]
     bool uploaded = false;
     ~zjai_picture() {
         for (hipEvent_t e : lane_ev) (void)hipEventDestroy(e);
@@ -626,6 +628,8 @@ struct zjai_picture {
         if (uv_hat) (void)hipFree(uv_hat);
         if (out_y) (void)hipFree(out_y);
         if (out_uv) (void)hipFree(out_uv);
+        if (out_rgb) (void)hipFree(out_rgb);
+        if (out_rgbf) (void)hipFree(out_rgbf);
     }
     size_t sample_bytes() const { return bit_depth ? 2 : 4; }
     int ch() const { return ceil_div(out_h, sv); }
@@ -799,5 +803,56 @@ extern "C" int32_t zjai_picture_download(zjai_ctx* ctx, zjai_picture* pic, void*
             ZJAI_HIP(hipMemcpyAsync(v, (char*)pic->out_uv + sb * n, sb * n, hipMemcpyDeviceToHost, ctx->c.stream));
         }
         ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
+    });
+}
+
+// ------------------------------------------------------------------------- output stage
+extern "C" int32_t zjai_resize(zjai_ctx* ctx, int32_t mode, const float* src, int32_t c, int32_t h,
+                               int32_t w, int32_t out_h, int32_t out_w, float* dst) {
+    if (!ctx || !src || !dst) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(mode == ZJAI_RESIZE_BICUBIC || mode == ZJAI_RESIZE_BILINEAR, "resize: unknown mode");
+        need(c > 0 && h > 0 && w > 0 && out_h > 0 && out_w > 0, "resize: empty dimension");
+        const size_t n_in = (size_t)c * h * w, n_out = (size_t)c * out_h * out_w;
+        Context& cx = ctx->c;
+        // Flat f32 scratch from the context's pool: [1][1][n / 8][8] tensors.
+        TensorP a = cx.alloc(1, 8, 1, (int)((n_in + 7) / 8), DT_F32);
+        TensorP b = cx.alloc(1, 8, 1, (int)((n_out + 7) / 8), DT_F32);
+        ZJAI_HIP(hipMemcpyAsync(a->v.p, src, n_in * 4, hipMemcpyHostToDevice, cx.stream));
+        {
+            LaunchScope sc(cx, mode == ZJAI_RESIZE_BICUBIC ? "k_resize_bicubic" : "k_resize_bilinear",
+                           0.0, 4.0 * (double)(n_in + n_out));
+            ZJAI_HIP(launch_resize(mode, (const float*)a->v.p, c, h, w, (float*)b->v.p, out_h, out_w, cx.stream));
+        }
+        ZJAI_HIP(hipMemcpyAsync(dst, b->v.p, n_out * 4, hipMemcpyDeviceToHost, cx.stream));
+        ZJAI_HIP(hipStreamSynchronize(cx.stream));
+    });
+}
+
+extern "C" int32_t zjai_picture_download_rgb(zjai_ctx* ctx, zjai_picture* pic, int32_t bit_depth,
+                                             uint16_t* rgb, float* rgb_planes) {
+    if (!ctx || !pic || !rgb) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(bit_depth == 8 || bit_depth == 10, "output bit depth must be 8 or 10");
+        need(pic->bit_depth == 0, "RGB output needs a picture with float planes (bit_depth 0)");
+        need(pic->net_uv != nullptr, "RGB output needs the chroma planes");
+        need(pic->uploaded, "picture latents have not been uploaded");
+        Context& cx = ctx->c;
+        const size_t n = (size_t)pic->out_h * pic->out_w;
+        if (!pic->out_rgb) ZJAI_HIP(hipMalloc((void**)&pic->out_rgb, n * 3 * sizeof(uint16_t)));
+        if (rgb_planes && !pic->out_rgbf) ZJAI_HIP(hipMalloc((void**)&pic->out_rgbf, n * 3 * sizeof(float)));
+        const int ch = pic->ch(), cw = pic->cw();
+        const float* u = (const float*)pic->out_uv;
+        const float* v = u + (size_t)ch * cw;
+        {
+            LaunchScope sc(cx, "k_picture_rgb", 0.0,
+                           (double)n * (4.0 + 6.0 + (rgb_planes ? 12.0 : 0.0)) + 8.0 * (double)ch * cw);
+            ZJAI_HIP(launch_picture_rgb((const float*)pic->out_y, pic->out_h, pic->out_w, u, v, ch, cw, bit_depth,
+                                        pic->out_rgb, rgb_planes ? pic->out_rgbf : nullptr, cx.stream));
+        }
+        ZJAI_HIP(hipMemcpyAsync(rgb, pic->out_rgb, n * 3 * sizeof(uint16_t), hipMemcpyDeviceToHost, cx.stream));
+        if (rgb_planes)
+            ZJAI_HIP(hipMemcpyAsync(rgb_planes, pic->out_rgbf, n * 3 * sizeof(float), hipMemcpyDeviceToHost, cx.stream));
+        ZJAI_HIP(hipStreamSynchronize(cx.stream));
     });
 }

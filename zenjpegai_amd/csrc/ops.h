@@ -67,6 +67,13 @@ struct FfnArgs {
     const float* b_out;
 };
 bool ffn_fused_supported(int dtype, int dim);
+// Output stage (src/decoder/output.rs): align_corners resampling of planar f32 [c][h][w] planes
+// and the BT.709 picture -> interleaved uint16 RGB (+ optional float planes [3][H][W]).
+enum ResizeMode : int { RESIZE_BICUBIC = 0, RESIZE_BILINEAR = 1 };
+hipError_t launch_resize(int mode, const float* src, int c, int h, int w, float* dst, int oh, int ow,
+                         hipStream_t s);
+hipError_t launch_picture_rgb(const float* y, int H, int W, const float* u, const float* v, int ch,
+                              int cw, int bit_depth, uint16_t* rgb, float* rgbf, hipStream_t s);
 hipError_t launch_ffn_fused(const FfnArgs& a, int dtype, int dim, hipStream_t s);
 // Channel attention (src/nn/fast/math.rs:512-603), three phases per batch item:
 // 1. per-head Gram partial sums over chunks of positions (f32 MFMA): qkv view holds 3*dim

@@ -185,6 +185,18 @@ class Picture:
             v.ctypes.data_as(ctypes.c_void_p) if v is not None else None), self.eng.handle)
         return y, u, v
 
+    def download_rgb(self, bit_depth=8, planes=False):
+        """The output stage of a BT.709 stream on the device (``to_source_format`` then
+        ``finish``, src/decoder/output.rs:153-199, :346-366): interleaved uint16 RGB
+        [out_h][out_w][3], plus the float RGB planes [3][out_h][out_w] when ``planes``. The
+        picture must have float planes (bit_depth 0) and a chroma net."""
+        rgb = np.empty((self.out_h, self.out_w, 3), np.uint16)
+        f = np.empty((3, self.out_h, self.out_w), np.float32) if planes else None
+        check(lib().zjai_picture_download_rgb(
+            self.eng.handle, self._h, bit_depth, rgb.ctypes.data_as(ctypes.c_void_p),
+            f.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) if planes else None), self.eng.handle)
+        return (rgb, f) if planes else rgb
+
     def __del__(self):
         try:
             if self._h:

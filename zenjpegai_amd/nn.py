@@ -285,6 +285,18 @@ def mul_assign(eng: Engine, a: BTensor, b: BTensor) -> None:
     check(lib().zjai_mul_assign(eng.handle, a._h, b._h), eng.handle)
 
 
+def resize(eng: Engine, x, out_h: int, out_w: int, mode: str = "bicubic") -> np.ndarray:
+    """``F.interpolate(x, (out_h, out_w), mode, align_corners=True)`` on the device, as the
+    reference's ``decoder::output::resize_bicubic`` (src/decoder/output.rs:117) / ``nn::resize_bilinear``
+    (src/nn/resample.rs:43) compute it; x is planar [c][h][w] float32."""
+    x = _f32(x)
+    c, h, w = x.shape
+    y = np.empty((c, out_h, out_w), np.float32)
+    m = {"bicubic": _lib.RESIZE_BICUBIC, "bilinear": _lib.RESIZE_BILINEAR}[mode]
+    check(lib().zjai_resize(eng.handle, m, _fp(x), c, h, w, out_h, out_w, _fp(y)), eng.handle)
+    return y
+
+
 def elu_gate(eng: Engine, a: BTensor, b: BTensor) -> None:
     check(lib().zjai_elu_gate(eng.handle, a._h, b._h), eng.handle)
 
