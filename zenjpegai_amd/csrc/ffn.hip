@@ -76,13 +76,17 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
     constexpr int WIN_PT = WIN_U / FTHREADS, LN_PT = U_U / FTHREADS;
     static_assert(WIN_U % FTHREADS == 0 && U_U % FTHREADS == 0 && WO_U <= FTHREADS, "fetch shapes");
     static_assert(FOP * (DIM + 4) * 4 <= (U_U + WIN_U + P_U) * 16, "output transpose fits");
-    __shared__ u32x4 s_lds[U_U + WIN_U + P_U + G_U + 2 * WO_U];
+    // Per slice also b_in [64] and the depthwise weights [9][64] + bias [64] (f32), two buffers.
+    constexpr int BIN_U = 16, DWW_U = (9 * 64 + 64) / 4, X_U = BIN_U + DWW_U;
+    static_assert(X_U <= FTHREADS, "fetch shapes");
+    __shared__ u32x4 s_lds[U_U + WIN_U + P_U + G_U + 2 * WO_U + 2 * X_U];
     __shared__ float s_stat[2 * FNP];
     u32x4* s_u = s_lds;
     u32x4* s_win = s_u + U_U;
     u32x4* s_p = s_win + WIN_U;
     u32x4* s_g = s_p + P_U;
     u32x4* s_wo = s_g + G_U;
+    u32x4* s_x = s_wo + 2 * WO_U;  // [2][b_in 16 units, depthwise 160 units]
     auto key = [](int r) { return (r >> KSH) & (UPR - 1); };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -96,7 +100,8 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
 
     // Slice s weights: W_in rows j and hid + j (j in [32 s, 32 s + 32)) of the packed 1x1
     // weight [chunk][nblk][16][32]; W_out = chunk s of the packed project_out weight.
-    u32x4 rwi[WIN_PT], rwo = {0u, 0u, 0u, 0u};
+    u32x4 rwi[WIN_PT], rwo = {0u, 0u, 0u, 0u}, rx = {0u, 0u, 0u, 0u};
+    auto gch = [](int s, int l) { return l < 32 ? 32 * s + l : HID + 32 * s + (l - 32); };
     auto fetch_w = [&](int s) {
 #pragma unroll
         for (int i = 0; i < WIN_PT; ++i) {
@@ -110,6 +115,20 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
             const long long off = ((long long)(s * p.nblk_out + (r >> 4)) * 16 + (r & 15)) * 32 + q * 8;
             rwo = *(const u32x4*)(w_out + off);
         }
+        // Thread u < 16: b_in of local channels 4u..4u+3; 16 <= u < 160: depthwise tap
+        // (u - 16) / 16 of local channels 4 (u % 16)..; 160 <= u < 176: depthwise bias.
+        if (tid < X_U) {
+            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (tid < BIN_U) {
+                if (p.b_in) v = *(const f32x4*)(p.b_in + gch(s, 4 * tid));
+            } else if (tid < BIN_U + 144) {
+                const int u = tid - BIN_U;
+                v = *(const f32x4*)(p.dw_w + (u >> 4) * C2 + gch(s, 4 * (u & 15)));
+            } else if (p.dw_b) {
+                v = *(const f32x4*)(p.dw_b + gch(s, 4 * (tid - BIN_U - 144)));
+            }
+            rx = __builtin_bit_cast(u32x4, v);
+        }
     };
     auto put_w = [&](int s) {
 #pragma unroll
@@ -118,6 +137,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
             s_win[r * UPR + (q ^ key(r))] = rwi[i];
         }
         if (tid < WO_U) s_wo[(s & 1) * WO_U + tid] = rwo;
+        if (tid < X_U) s_x[(s & 1) * X_U + tid] = rx;
     };
 
     // ---- 1. x over the halo (zero outside the picture), then LayerNorm in place.
@@ -136,6 +156,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
         // k_layer_norm's statistics: f64 sums in channel order.
         const int pos = tid;
         double mean = 0.0;
+#pragma unroll 2
         for (int q = 0; q < UPR; ++q) {
             float f[8];
             unpack8<T>(s_u[pos * UPR + (q ^ key(pos))], f);
@@ -144,6 +165,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
         }
         mean /= (double)DIM;
         double var = 0.0;
+#pragma unroll 2
         for (int q = 0; q < UPR; ++q) {
             float f[8];
             unpack8<T>(s_u[pos * UPR + (q ^ key(pos))], f);
@@ -165,7 +187,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
             lw[k] = p.ln_w[q * 8 + k];
             lb[k] = p.ln_b[q * 8 + k];
         }
-#pragma unroll
+#pragma unroll 2
         for (int i = 0; i < LN_PT; ++i) {
             const int pos = (tid + i * FTHREADS) / UPR;
             u32x4* a = &s_u[pos * UPR + (q ^ key(pos))];
@@ -210,15 +232,12 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
         //    16x16x32 MFMAs with K in 32-channel chunks, bias first: the unfused 1x1 conv's
         //    instruction sequence, so p matches it bit for bit.
         f32x4 acc1[2][4];
+        const float* sbin = reinterpret_cast<const float*>(s_x + (s & 1) * X_U);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             f32x4 bi;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int cl = c * 16 + 4 * grp + r;  // channel within the half
-                const int o = cb1 ? HID + 32 * s + cl : 32 * s + cl;
-                bi[r] = p.b_in ? p.b_in[o] : 0.0f;
-            }
+            for (int r = 0; r < 4; ++r) bi[r] = sbin[cb1 * 32 + c * 16 + 4 * grp + r];
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc1[c][i] = bi;
         }
@@ -263,16 +282,17 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
 
         // b. depthwise 3x3 + gate: rows 7 rh .. 7 rh + 6 of column dc, pairs 32 s + 2 pg + {0, 1}.
         if (dw_thread) {
-            const int ja = 32 * s + 2 * pg;
+            // Local channel 2 pg + k (first half) and 32 + 2 pg + k (second half).
+            const float* dww = reinterpret_cast<const float*>(s_x + (s & 1) * X_U + BIN_U);
             float wa[9][2], wb[9][2], ba[2], bb[2];
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
-                ba[k] = p.dw_b ? p.dw_b[ja + k] : 0.0f;
-                bb[k] = p.dw_b ? p.dw_b[HID + ja + k] : 0.0f;
+                ba[k] = dww[576 + 2 * pg + k];
+                bb[k] = dww[576 + 32 + 2 * pg + k];
 #pragma unroll
                 for (int tp = 0; tp < 9; ++tp) {
-                    wa[tp][k] = p.dw_w[tp * C2 + ja + k];
-                    wb[tp][k] = p.dw_w[tp * C2 + HID + ja + k];
+                    wa[tp][k] = dww[tp * 64 + 2 * pg + k];
+                    wb[tp][k] = dww[tp * 64 + 32 + 2 * pg + k];
                 }
             }
             // 16-byte unit (pg / 4) of the first half, 4 + pg / 4 of the second, swapped on odd
