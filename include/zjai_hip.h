@@ -74,11 +74,12 @@ typedef struct zjai_picture zjai_picture;
 /* ------------------------------------------------------------------ context / diagnostics */
 
 /* Replaces `Engine` construction (src/nn/fast/mod.rs:128-172) for the HIP backend: binds a
- * device and creates its stream. flags: 0 or ZJAI_CTX_UNFUSED_FFN (other bits are rejected). */
-/* Run the transformer blocks' feed-forward half (src/model/attention.rs:346-369) as separate
- * layer-norm, 1x1, depthwise+gate and 1x1 kernels instead of the fused kernel the 16-bit
- * precisions use by default (the two give bit-identical results). */
-#define ZJAI_CTX_UNFUSED_FFN 0x1u
+ * device and creates its stream. flags: 0 or ZJAI_CTX_UNFUSED_BLOCKS (other bits are rejected). */
+/* Run the transformer blocks (src/model/attention.rs:328-372) as the reference's separate ops --
+ * layer norm, 1x1, depthwise (+ ELU gate), 1x1 -- instead of the fused kernels the 16-bit
+ * precisions use by default for `prep_data` (LN + 1x1 + depthwise) and for the feed-forward half
+ * (the two give bit-identical results). */
+#define ZJAI_CTX_UNFUSED_BLOCKS 0x1u
 ZJAI_API int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out);
 ZJAI_API int32_t zjai_ctx_destroy(zjai_ctx* ctx);
 /* Copies the last failure message (NUL-terminated, truncated to len). Works with ctx == NULL

@@ -100,12 +100,12 @@ def test_fast_paths_psnr(engines, prec, floor, op):
 
 @pytest.mark.parametrize("prec", ["bf16", "f16"])
 @pytest.mark.parametrize("comp", ["y", "uv"])
-def test_fused_ffn_is_bit_identical_to_unfused(prec, comp):
-    """The fused feed-forward kernel (HOP luma TAM: dim 128, chroma: dim 64) against the same
-    net run with layer norm, 1x1, depthwise+gate and 1x1 as separate kernels. The feature maps
+def test_fused_transformer_blocks_are_bit_identical_to_unfused(prec, comp):
+    """The fused prep_data (LN + 1x1 + depthwise) and feed-forward kernels (HOP luma TAM: dim
+    128, chroma: dim 64) against the same net run with every op as a separate kernel. The feature maps
     (64 x 96 and 64 x 48) span several 14 x 14 tiles with partial ones at the right and bottom."""
     fused = nn.Engine(0, prec)
-    plain = nn.Engine(0, prec, flags=_lib.CTX_UNFUSED_FFN)
+    plain = nn.Engine(0, prec, flags=_lib.CTX_UNFUSED_BLOCKS)
     p = synth.random_params("hop", comp, seed=24, gain=0.5)
     outs, names = [], []
     for eng in (fused, plain):
@@ -122,8 +122,9 @@ def test_fused_ffn_is_bit_identical_to_unfused(prec, comp):
         names.append([r[0] for r in eng.profile_end()])
         outs.append(out)
     dim = 128 if comp == "y" else 64
-    assert sum(n.startswith("k_ffn<") and n.endswith(f", {dim}>") for n in names[0]) == 2
-    assert not any(n.startswith("k_ffn") for n in names[1])
+    for k in ("k_ffn<", "k_qkv<"):
+        assert sum(n.startswith(k) and n.endswith(f", {dim}>") for n in names[0]) == 2, k
+        assert not any(n.startswith(k) for n in names[1]), k
     assert np.isfinite(outs[0]).all()
     np.testing.assert_array_equal(outs[0], outs[1])
     fused.close()

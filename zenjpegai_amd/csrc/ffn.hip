@@ -62,18 +62,96 @@ __device__ __forceinline__ void unpack2(unsigned v, float (&o)[2]) {
     o[1] = (float)hv[1];
 }
 
+// u rows (halo positions, DIM channels of the storage type, UPR = DIM / 8 16-byte units): unit
+// q of row r sits at q ^ ukey(r), so that the 16 rows one half-wave reads for an MFMA fragment
+// cover all 16 four-bank groups.
+template <int DIM>
+__device__ __forceinline__ int ukey(int r) {
+    constexpr int UPR = DIM / 8, KSH = DIM == 128 ? 0 : 1;
+    return (r >> KSH) & (UPR - 1);
+}
+
+// x over the 16 x 16 halo of the tile at (y0, x0) (zero outside the picture) -> LayerNorm per
+// position, in place, into s_u (storage type, swizzled rows), as k_layer_norm computes it: f64
+// sums in channel order, mean and sqrt(var / C + 1e-5) narrowed to f32, then
+// ((x - m) / d) * w + b per element. s_stat: 2 x FNP floats. Ends without a barrier.
+template <typename T, int DIM>
+__device__ __forceinline__ void ln_halo(const T* xb, const View& xv, int y0, int x0, int h, int w,
+                                        const float* ln_w, const float* ln_b, u32x4* s_u,
+                                        float* s_stat, int tid) {
+    constexpr int UPR = DIM / 8, LN_PT = FNP * UPR / FTHREADS;
+    static_assert((FNP * UPR) % FTHREADS == 0, "halo shape");
+#pragma unroll
+    for (int i = 0; i < LN_PT; ++i) {
+        const int u = tid + i * FTHREADS, pos = u / UPR, q = u % UPR;
+        const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (iy >= 0 && iy < h && ix >= 0 && ix < w)
+            v = *(const u32x4*)(xb + (long long)iy * xv.row + (long long)ix * xv.cs + q * 8);
+        s_u[pos * UPR + (q ^ ukey<DIM>(pos))] = v;
+    }
+    __syncthreads();
+    if (tid < FNP) {
+        const int pos = tid;
+        double mean = 0.0;
+#pragma unroll 2
+        for (int q = 0; q < UPR; ++q) {
+            float f[8];
+            unpack8<T>(s_u[pos * UPR + (q ^ ukey<DIM>(pos))], f);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) mean += (double)f[k];
+        }
+        mean /= (double)DIM;
+        double var = 0.0;
+#pragma unroll 2
+        for (int q = 0; q < UPR; ++q) {
+            float f[8];
+            unpack8<T>(s_u[pos * UPR + (q ^ ukey<DIM>(pos))], f);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const double e = (double)f[k] - mean;
+                var = var + e * e;
+            }
+        }
+        s_stat[pos] = (float)mean;
+        s_stat[FNP + pos] = sqrtf((float)(var / (double)DIM) + 1e-5f);
+    }
+    __syncthreads();
+    const int q = tid % UPR;  // the same unit for every i (FTHREADS % UPR == 0)
+    float lw[8], lb[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        lw[k] = ln_w[q * 8 + k];
+        lb[k] = ln_b[q * 8 + k];
+    }
+#pragma unroll 2
+    for (int i = 0; i < LN_PT; ++i) {
+        const int pos = (tid + i * FTHREADS) / UPR;
+        u32x4* a = &s_u[pos * UPR + (q ^ ukey<DIM>(pos))];
+        float f[8];
+        unpack8<T>(*a, f);
+        const float m = s_stat[pos], d = s_stat[FNP + pos];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            float e = f[k] - m;
+            e = e / d;
+            e = e * lw[k];
+            f[k] = e + lb[k];
+        }
+        *a = pack8<T>(f);
+    }
+}
+
 }  // namespace
 
 template <typename T, int DIM>
 __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
     constexpr int HID = 4 * DIM, C2 = 2 * HID, NS = HID / 32;
     constexpr int UPR = DIM / 8;  // 16-byte units per u / W_in row
-    // u / W_in rows: unit q of row r sits at q ^ key(r), so that the 16 rows one half-wave
-    // reads for an MFMA fragment cover all 16 four-bank groups.
-    constexpr int KSH = DIM == 128 ? 0 : 1;
+    // u and W_in rows are swizzled by ukey (16-byte unit q of row r at q ^ ukey(r)).
     constexpr int CB2 = DIM / 16, WPC = 8 / CB2, NPB = (FPB + WPC - 1) / WPC;
     constexpr int U_U = FNP * UPR, WIN_U = 64 * UPR, P_U = FNP * 8, G_U = FPB * 16 * 4, WO_U = DIM * 4;
-    constexpr int WIN_PT = WIN_U / FTHREADS, LN_PT = U_U / FTHREADS;
+    constexpr int WIN_PT = WIN_U / FTHREADS;
     static_assert(WIN_U % FTHREADS == 0 && U_U % FTHREADS == 0 && WO_U <= FTHREADS, "fetch shapes");
     static_assert(FOP * (DIM + 4) * 4 <= (U_U + WIN_U + P_U) * 16, "output transpose fits");
     // Per slice also b_in [64] and the depthwise weights [9][64] + bias [64] (f32), two buffers.
@@ -87,7 +165,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
     u32x4* s_g = s_p + P_U;
     u32x4* s_wo = s_g + G_U;
     u32x4* s_x = s_wo + 2 * WO_U;  // [2][b_in 16 units, depthwise 160 units]
-    auto key = [](int r) { return (r >> KSH) & (UPR - 1); };
+    auto key = [](int r) { return ukey<DIM>(r); };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;  // 16x16 MFMA fragment lane
@@ -142,68 +220,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
 
     // ---- 1. x over the halo (zero outside the picture), then LayerNorm in place.
     fetch_w(0);
-#pragma unroll
-    for (int i = 0; i < LN_PT; ++i) {
-        const int u = tid + i * FTHREADS, pos = u / UPR, q = u % UPR;
-        const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (iy >= 0 && iy < p.h && ix >= 0 && ix < p.w)
-            v = *(const u32x4*)(xb + (long long)iy * p.x.row + (long long)ix * p.x.cs + q * 8);
-        s_u[pos * UPR + (q ^ key(pos))] = v;
-    }
-    __syncthreads();
-    if (tid < FNP) {
-        // k_layer_norm's statistics: f64 sums in channel order.
-        const int pos = tid;
-        double mean = 0.0;
-#pragma unroll 2
-        for (int q = 0; q < UPR; ++q) {
-            float f[8];
-            unpack8<T>(s_u[pos * UPR + (q ^ key(pos))], f);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) mean += (double)f[k];
-        }
-        mean /= (double)DIM;
-        double var = 0.0;
-#pragma unroll 2
-        for (int q = 0; q < UPR; ++q) {
-            float f[8];
-            unpack8<T>(s_u[pos * UPR + (q ^ key(pos))], f);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const double e = (double)f[k] - mean;
-                var = var + e * e;
-            }
-        }
-        s_stat[pos] = (float)mean;
-        s_stat[FNP + pos] = sqrtf((float)(var / (double)DIM) + 1e-5f);
-    }
-    __syncthreads();
-    {
-        const int q = tid % UPR;  // the same unit for every i (FTHREADS % UPR == 0)
-        float lw[8], lb[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            lw[k] = p.ln_w[q * 8 + k];
-            lb[k] = p.ln_b[q * 8 + k];
-        }
-#pragma unroll 2
-        for (int i = 0; i < LN_PT; ++i) {
-            const int pos = (tid + i * FTHREADS) / UPR;
-            u32x4* a = &s_u[pos * UPR + (q ^ key(pos))];
-            float f[8];
-            unpack8<T>(*a, f);
-            const float m = s_stat[pos], d = s_stat[FNP + pos];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                float e = f[k] - m;
-                e = e / d;
-                e = e * lw[k];
-                f[k] = e + lb[k];
-            }
-            *a = pack8<T>(f);
-        }
-    }
+    ln_halo<T, DIM>(xb, p.x, y0, x0, p.h, p.w, p.ln_w, p.ln_b, s_u, s_stat, tid);
     put_w(0);
 
     // ---- 2. slices of 32 gate pairs.
@@ -382,6 +399,208 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
         for (int k = 0; k < 4; ++k) v[k] = v[k] + r[k];
         store4<T>(yb + (long long)oy * p.y.row + (long long)ox * p.y.cs + q * 4, v);
     }
+}
+
+// The first half of a transformer block's attention branch as one kernel (16-bit storage
+// types): qkv = depthwise3x3(conv1x1(LayerNorm(x))), dim -> 3 dim channels
+// (TransformerBlock::forward, src/model/attention.rs:330-333: `prep_data`). Per 14 x 14 tile
+// (16 x 16 halo, 8 waves): the LayerNorm prologue of k_ffn, then per slice of 64 of the 3 dim
+// channels the 1x1 on 16x16x32 MFMAs (the unfused conv's instruction sequence) into LDS, zero
+// outside the picture, and the depthwise 3x3 in the unfused kernel's FMA order, stored to qkv.
+// The LayerNorm output and the 1x1's output never reach HBM; the results equal the unfused
+// kernels' bit for bit.
+template <typename T, int DIM>
+__global__ void __launch_bounds__(FTHREADS) k_qkv(const QkvArgs p) {
+    constexpr int C3 = 3 * DIM, NS = C3 / 64, UPR = DIM / 8;
+    constexpr int U_U = FNP * UPR, WIN_U = 64 * UPR, P_U = FNP * 8;
+    // Per slice: conv1 bias [64], depthwise weights [9][64] and bias [64] (f32), two buffers.
+    constexpr int BIN_U = 16, X_U = (64 + 9 * 64 + 64) / 4;
+    constexpr int WIN_PT = WIN_U / FTHREADS;
+    static_assert(WIN_U % FTHREADS == 0 && X_U <= FTHREADS && C3 % 64 == 0, "fetch shapes");
+    __shared__ u32x4 s_lds[U_U + WIN_U + P_U + 2 * X_U];
+    __shared__ float s_stat[2 * FNP];
+    u32x4* s_u = s_lds;
+    u32x4* s_win = s_u + U_U;
+    u32x4* s_p = s_win + WIN_U;
+    u32x4* s_x = s_p + P_U;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;  // 16x16 MFMA fragment lane
+    const int bid = (int)blockIdx.x;
+    const int tx = bid % p.gx, ty = (bid / p.gx) % p.gy, b = bid / (p.gx * p.gy);
+    const int y0 = ty * FT, x0 = tx * FT;
+    const T* xb = (const T*)p.x.p + (long long)b * p.x.bstride + p.x.c_off;
+    const T* w1 = (const T*)p.w1;
+
+    // Slice s: conv1 output channels 64 s .. 64 s + 63 (rows of the packed 1x1 weight
+    // [chunk][nblk][16][32]), their biases, depthwise taps and depthwise biases.
+    u32x4 rwi[WIN_PT], rx = {0u, 0u, 0u, 0u};
+    auto fetch = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < WIN_PT; ++i) {
+            const int u = tid + i * FTHREADS, r = u / UPR, q = u % UPR, o = 64 * s + r;
+            const long long off = ((long long)((q >> 2) * p.nblk1 + (o >> 4)) * 16 + (o & 15)) * 32 + (q & 3) * 8;
+            rwi[i] = *(const u32x4*)(w1 + off);
+        }
+        if (tid < X_U) {
+            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (tid < BIN_U) {
+                if (p.b1) v = *(const f32x4*)(p.b1 + 64 * s + 4 * tid);
+            } else if (tid < BIN_U + 144) {
+                const int u = tid - BIN_U;
+                v = *(const f32x4*)(p.dw_w + (u >> 4) * C3 + 64 * s + 4 * (u & 15));
+            } else if (p.dw_b) {
+                v = *(const f32x4*)(p.dw_b + 64 * s + 4 * (tid - BIN_U - 144));
+            }
+            rx = __builtin_bit_cast(u32x4, v);
+        }
+    };
+    auto put = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < WIN_PT; ++i) {
+            const int u = tid + i * FTHREADS, r = u / UPR, q = u % UPR;
+            s_win[r * UPR + (q ^ ukey<DIM>(r))] = rwi[i];
+        }
+        if (tid < X_U) s_x[(s & 1) * X_U + tid] = rx;
+    };
+
+    fetch(0);
+    ln_halo<T, DIM>(xb, p.x, y0, x0, p.h, p.w, p.ln_w, p.ln_b, s_u, s_stat, tid);
+    put(0);
+
+    const int cb1 = wave & 1;   // conv1 channel blocks 2 cb1, 2 cb1 + 1 of the slice
+    const int pb1 = wave >> 1;  // conv1 position blocks 4 pb1 .. 4 pb1 + 3
+    // Depthwise role (tid < 448, whole waves 0-6): channel pair pg, column dc, all 14 rows.
+    const int pg = tid & 31, dc = (tid >> 5) % FT;
+    const bool dw_thread = tid < 32 * FT;
+    T* yb = (T*)p.y.p + (long long)b * p.y.bstride + p.y.c_off;
+
+    for (int s = 0; s < NS; ++s) {
+        __syncthreads();  // u, W1(s) ready; p free
+        if (s + 1 < NS) fetch(s + 1);
+        const float* sx = reinterpret_cast<const float*>(s_x + (s & 1) * X_U);
+        {
+            f32x4 acc1[2][4];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                f32x4 bi;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) bi[r] = sx[cb1 * 32 + c * 16 + 4 * grp + r];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc1[c][i] = bi;
+            }
+#pragma unroll
+            for (int kc = 0; kc < DIM / 32; ++kc) {
+                const int q = 4 * kc + grp;
+                u32x4 a[2], bv[4];
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const int ra = cb1 * 32 + c * 16 + col;
+                    a[c] = s_win[ra * UPR + (q ^ ukey<DIM>(ra))];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int rb = (pb1 * 4 + i) * 16 + col;
+                    bv[i] = s_u[rb * UPR + (q ^ ukey<DIM>(rb))];
+                }
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) Mma16<T>::run(acc1[c][i], a[c], bv[i]);
+            }
+            T* sp = reinterpret_cast<T*>(s_p);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int pos = (pb1 * 4 + i) * 16 + col;
+                const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
+                const bool inside = iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    typedef T t4 __attribute__((ext_vector_type(4)));
+                    t4 v;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) v[k] = inside ? (T)acc1[c][i][k] : (T)0.0f;
+                    *reinterpret_cast<t4*>(sp + pos * 64 + cb1 * 32 + c * 16 + 4 * grp) = v;
+                }
+            }
+        }
+        __syncthreads();  // p ready; W1(s) consumed
+        if (s + 1 < NS) put(s + 1);
+        if (dw_thread) {
+            // Channels 2 pg, 2 pg + 1 of the slice; acc = bias, then (ky, kx) ascending.
+            const float* dww = sx + BIN_U * 4;
+            float wv[9][2], bv[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                bv[k] = dww[576 + 2 * pg + k];
+#pragma unroll
+                for (int tp = 0; tp < 9; ++tp) wv[tp][k] = dww[tp * 64 + 2 * pg + k];
+            }
+            const T* sp = reinterpret_cast<const T*>(s_p) + dc * 64 + 2 * pg;
+            float xw[3][3][2];
+            auto ld = [&](int hr, int kx, float (&o)[2]) {
+                unpack2<T>(*(const unsigned*)(sp + (hr * FH + kx) * 64), o);
+            };
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                ld(0, kx, xw[0][kx]);
+                ld(1, kx, xw[1][kx]);
+            }
+            const int ox = x0 + dc;
+#pragma unroll
+            for (int r = 0; r < FT; ++r) {
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx) ld(r + 2, kx, xw[2][kx]);
+                float o[2];
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    float a = bv[k];
+#pragma unroll
+                    for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+                        for (int kx = 0; kx < 3; ++kx) a = fmaf(wv[ky * 3 + kx][k], xw[ky][kx][k], a);
+                    o[k] = a;
+                }
+                const int oy = y0 + r;
+                if (oy < p.h && ox < p.w) {
+                    typedef T t2 __attribute__((ext_vector_type(2)));
+                    *reinterpret_cast<t2*>(yb + (long long)oy * p.y.row + (long long)ox * p.y.cs + 64 * s + 2 * pg) =
+                        t2{(T)o[0], (T)o[1]};
+                }
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx)
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        xw[0][kx][k] = xw[1][kx][k];
+                        xw[1][kx][k] = xw[2][kx][k];
+                    }
+            }
+        }
+    }
+}
+
+bool qkv_fused_supported(int dtype, int dim) { return (dtype == DT_F16 || dtype == DT_BF16) && (dim == 64 || dim == 128); }
+
+hipError_t launch_qkv_fused(const QkvArgs& a, int dtype, int dim, hipStream_t s) {
+    if (!qkv_fused_supported(dtype, dim)) return hipErrorInvalidValue;
+    if (a.x.cs % 8 || a.x.c_off % 8 || a.x.row % 8 || a.x.bstride % 8 || a.y.cs % 2 || a.y.c_off % 2 ||
+        a.y.row % 2 || a.y.bstride % 2)
+        return hipErrorInvalidValue;
+    if (a.N <= 0 || a.h <= 0 || a.w <= 0) return hipSuccess;
+    QkvArgs p = a;
+    p.gx = (a.w + FT - 1) / FT;
+    p.gy = (a.h + FT - 1) / FT;
+    const long long blocks = (long long)p.gx * p.gy * a.N;
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)blocks), block(FTHREADS);
+    if (dtype == DT_BF16) {
+        if (dim == 128) k_qkv<__bf16, 128><<<grid, block, 0, s>>>(p);
+        else k_qkv<__bf16, 64><<<grid, block, 0, s>>>(p);
+    } else {
+        if (dim == 128) k_qkv<_Float16, 128><<<grid, block, 0, s>>>(p);
+        else k_qkv<_Float16, 64><<<grid, block, 0, s>>>(p);
+    }
+    return hipGetLastError();
 }
 
 bool ffn_fused_supported(int dtype, int dim) {

@@ -257,7 +257,7 @@ struct Fwd {
     // are packed unpadded (K chunks of 32 channels, 16-row blocks) and whose input is a whole
     // 16-byte-aligned NHWC tensor.
     bool ffn_fusable(const std::string& p, const TensorP& x) {
-        if (ctx.top().flags & ZJAI_CTX_UNFUSED_FFN) return false;
+        if (ctx.top().flags & ZJAI_CTX_UNFUSED_BLOCKS) return false;
         const int dim = x->c, hidden = 4 * dim;
         if (!ffn_fused_supported(x->dtype, dim)) return false;
         const Layer& pin = L(p + ".ffn.project_in");
@@ -274,12 +274,54 @@ struct Fwd {
         const View& v = x->v;
         return v.cs % 8 == 0 && v.c_off % 8 == 0 && v.row % 8 == 0 && v.bstride % 8 == 0;
     }
+    // The fused prep_data kernel: same conditions, a dim -> 3 dim unpadded 1x1 and a 3 dim
+    // depthwise.
+    bool qkv_fusable(const std::string& p, const TensorP& x) {
+        if (ctx.top().flags & ZJAI_CTX_UNFUSED_BLOCKS) return false;
+        const int dim = x->c;
+        if (!qkv_fused_supported(x->dtype, dim)) return false;
+        const Layer& c1 = L(p + ".prep_data.conv1");
+        const Layer& c2 = L(p + ".prep_data.conv2");
+        const int ck = 64 / dtype_size(x->dtype);
+        if (c1.kind != CK_1x1 || c1.groups != 1 || c1.transposed || c1.dtype != x->dtype ||
+            c1.nblk_g * 16 != 3 * dim || c1.nchunks * ck != dim || c1.cin != dim)
+            return false;
+        if (!c2.depthwise || c2.cin != 3 * dim || !c2.dw_w) return false;
+        const View& v = x->v;
+        return v.cs % 8 == 0 && v.c_off % 8 == 0 && v.row % 8 == 0 && v.bstride % 8 == 0;
+    }
     // TransformerBlock::forward (src/model/attention.rs:328-372)
     TensorP transformer_block(const std::string& p, TensorP x) {
         const int dim = x->c, heads = 4, hidden = 4 * dim;
-        TensorP t = layer_norm(p + ".prep_data.norm1", x);
-        t = conv(p + ".prep_data.conv1", t);
-        t = conv(p + ".prep_data.conv2", t);  // depthwise 3x3
+        TensorP t;
+        if (qkv_fusable(p, x)) {
+            const Layer& c1 = L(p + ".prep_data.conv1");
+            const Layer& c2 = L(p + ".prep_data.conv2");
+            t = ctx.alloc(x->n, 3 * dim, x->h, x->w, x->dtype);
+            QkvArgs a{};
+            a.x = x->v;
+            a.y = t->v;
+            a.N = x->n;
+            a.h = x->h;
+            a.w = x->w;
+            a.ln_w = net.vec.at(p + ".prep_data.norm1.weight");
+            a.ln_b = net.vec.at(p + ".prep_data.norm1.bias");
+            a.w1 = c1.wpk;
+            a.nblk1 = c1.nblk_g;
+            a.b1 = c1.bias;
+            a.dw_w = c2.dw_w;
+            a.dw_b = c2.bias;
+            const double npos = (double)x->n * x->h * x->w;
+            const std::string kn = kname("k_qkv", x->dtype);
+            LaunchScope sc(ctx, kn.substr(0, kn.size() - 1) + ", " + std::to_string(dim) + ">",
+                           2.0 * npos * (3.0 * dim * dim + 9.0 * 3 * dim),
+                           (double)dtype_size(x->dtype) * npos * 4 * dim);
+            ZJAI_HIP(launch_qkv_fused(a, x->dtype, dim, ctx.stream));
+        } else {
+            t = layer_norm(p + ".prep_data.norm1", x);
+            t = conv(p + ".prep_data.conv1", t);
+            t = conv(p + ".prep_data.conv2", t);  // depthwise 3x3
+        }
         // channel_attention + project_out: fold attn into the projection, run it on v.
         Epilogue ea;
         std::shared_ptr<void> wfold =

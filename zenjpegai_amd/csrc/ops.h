@@ -67,6 +67,22 @@ struct FfnArgs {
     const float* b_out;
 };
 bool ffn_fused_supported(int dtype, int dim);
+// The attention branch's qkv = depthwise3x3(conv1x1(LN(x))) (dim -> 3 dim) in one kernel
+// (16-bit storage types, dim 64 or 128); weights as FfnArgs. y must not alias x.
+struct QkvArgs {
+    View x, y;
+    int N, h, w;
+    int gx, gy;  // tile grid (set by the launcher)
+    const float* ln_w;
+    const float* ln_b;
+    const void* w1;  // conv1: dim -> 3 dim, packed 1x1
+    int nblk1;
+    const float* b1;
+    const float* dw_w;  // [9][3 dim]
+    const float* dw_b;
+};
+bool qkv_fused_supported(int dtype, int dim);
+hipError_t launch_qkv_fused(const QkvArgs& a, int dtype, int dim, hipStream_t s);
 // Output stage (src/decoder/output.rs): align_corners resampling of planar f32 [c][h][w] planes
 // and the BT.709 picture -> interleaved uint16 RGB (+ optional float planes [3][H][W]).
 enum ResizeMode : int { RESIZE_BICUBIC = 0, RESIZE_BILINEAR = 1 };

@@ -85,8 +85,8 @@ class Engine:
     (device + stream) and the precision layers are packed for ("f32", "f16" or "bf16")."""
 
     def __init__(self, device: int = 0, precision: str = "f32", flags: int = 0):
-        """``flags``: 0 or ``_lib.CTX_UNFUSED_FFN`` (the transformer blocks' feed-forward half
-        as separate kernels instead of the fused one the 16-bit precisions use)."""
+        """``flags``: 0 or ``_lib.CTX_UNFUSED_BLOCKS`` (the transformer blocks as separate
+        kernels instead of the fused ones the 16-bit precisions use)."""
         self.precision = precision
         self.dtype = _lib.PRECISIONS[precision]
         self._h = ctypes.c_void_p()
