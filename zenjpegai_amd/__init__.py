@@ -17,7 +17,11 @@ import subprocess
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
-def build(jobs: int = 8) -> str:
-    """Compiles ``libzjai_hip.so`` for gfx950 in-tree and returns its path."""
-    subprocess.run(["make", "-s", f"-j{jobs}", "-C", os.path.join(HERE, "csrc")], check=True)
+def build(jobs: int = 8, force: bool = True) -> str:
+    """Compiles ``libzjai_hip.so`` for gfx950 in-tree and returns its path; ``force`` rebuilds
+    every object even where make finds it up to date."""
+    cmd = ["make", "-s", f"-j{jobs}", "-C", os.path.join(HERE, "csrc")]
+    if force:
+        cmd.insert(1, "-B")
+    subprocess.run(cmd, check=True)
     return os.path.join(HERE, "libzjai_hip.so")
