@@ -136,6 +136,57 @@ def rgb_output_stage(prec, lanes, reps=5):
             "mpix_s": round(n / (us * 1e-6) / 1e6, 1)}
 
 
+def latent_stage(prec, reps=3):
+    """The decoder's latent reconstruction of the config-5 picture (2x3 independent regions,
+    src/decoder/reconstruct.rs:81-234): per component the hyper-decoder on every region's z
+    window and the four-stage context model on its residual / psi windows, one
+    ``zjai_reconstruct_latent`` call each. Reports the summed kernel time (HIP events, best of
+    ``reps``), the call's wall time (host transfers of z_hat, residual, psi and y_hat included)
+    and the algorithmic FLOPs; returns the inputs for the CPU leg."""
+    from zenjpegai_amd import model, nn, synth
+    eng = nn.Engine(0, prec)
+    regions = model.Regions(2, 3, True)
+    out, inputs = {}, []
+    for ccs, tag in ((0, "luma"), (1, "chroma")):
+        c = synth.LATENT_CHANNELS[ccs]
+        p = synth.random_latent_params(ccs, seed=1)
+        m = model.LatentModel.load(p, ccs, eng)
+        z = synth.hyper_latent(1, f"cfg5/z{ccs}", c, 34, 60)
+        res = synth.residual(1, f"cfg5/r{ccs}", c, 135, 240)
+        m.reconstruct(2160, 3840, regions, z, res)
+        best_k, best_w, flops = None, None, 0.0
+        for _ in range(reps):
+            eng.profile_begin()
+            t0 = time.perf_counter()
+            m.reconstruct(2160, 3840, regions, z, res)
+            wall = (time.perf_counter() - t0) * 1e3
+            recs = eng.profile_end()
+            k = sum(r[3] for r in recs)
+            flops = sum(r[1] for r in recs)
+            best_k = k if best_k is None else min(best_k, k)
+            best_w = wall if best_w is None else min(best_w, wall)
+        out[f"{tag}_kernel_ms"] = round(best_k, 3)
+        out[f"{tag}_wall_ms"] = round(best_w, 3)
+        out[f"{tag}_gflop"] = round(flops / 1e9, 2)
+        inputs.append((ccs, p, z, res))
+        del m
+    eng.close()
+    return out, inputs
+
+
+def latent_stage_cpu(inputs):
+    """The same latent reconstruction on the CPU restatement (nn::fast convolutions)."""
+    import oracle.graphs as og
+    from oracle import geometry as geo
+    out = {}
+    for ccs, p, z, res in inputs:
+        t0 = time.perf_counter()
+        with og.fast_convs():
+            og.reconstruct_latent(p, ccs, 2160, 3840, geo.Regions(2, 3, True), z, res)
+        out[("luma" if ccs == 0 else "chroma") + "_cpu_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+    return out
+
+
 def layer_configs(prec, reps=10):
     """BASELINE configs 1-3 as single-layer runs at their full sizes: kernel time per run (HIP
     events around each launch) and conv TFLOP/s (all taps counted)."""
@@ -300,6 +351,7 @@ def main():
             json.dump({"workload": args.workload, "precision": args.precision, "kernels": prof},
                       f, indent=1, sort_keys=True)
 
+    latent_inputs = None
     extra = {
         "device_ms_per_step": round(eng.stats()["last_run_ms"], 3),
         "profiled_kernel_ms": round(total_ms, 3),
@@ -340,6 +392,8 @@ def main():
         if args.workload == "cfg5":
             extra["rgb_output_stage_cfg5"] = rgb_output_stage(args.precision, args.lanes)
             log(f"[bench] RGB output stage: {extra['rgb_output_stage_cfg5']}")
+            extra["latent_reconstruction_cfg5"], latent_inputs = latent_stage(args.precision)
+            log(f"[bench] latent reconstruction: {extra['latent_reconstruction_cfg5']}")
         for prec in ("f32", "bf16"):
             extra.update(layer_configs(prec))
         log("[bench] configs 1-3: " + ", ".join(f"{k}={v}" for k, v in extra.items() if k.startswith("cfg") and "tflops" in k))
@@ -349,6 +403,9 @@ def main():
         log("[bench] timing the CPU baseline (nn::fast restatement) on the config-5 tiles")
         cpu = cpu_baseline(info)
         log(f"[bench] cpu: {cpu}")
+        if latent_inputs:
+            extra["latent_reconstruction_cfg5"].update(latent_stage_cpu(latent_inputs))
+            log(f"[bench] latent reconstruction with cpu: {extra['latent_reconstruction_cfg5']}")
 
     out = {
         "metric": METRIC, "value": round(value, 3), "unit": "Mpixel/s", "n_gpus": 1,

@@ -274,6 +274,68 @@ ZJAI_API int32_t zjai_resize(zjai_ctx* ctx, int32_t mode, const float* src, int3
 ZJAI_API int32_t zjai_picture_download_rgb(zjai_ctx* ctx, zjai_picture* pic, int32_t bit_depth,
                                            uint16_t* rgb, float* rgb_planes);
 
+/* ----------------------------------------------------------------- latent reconstruction */
+
+/* Region partitioning of a picture header (`Regions`, src/header.rs; the grid of
+ * src/tools/regions.rs:104-150). A NULL zjai_regions* means "not partitioned". */
+typedef struct zjai_regions {
+    int32_t num_ver, num_hor;        /* region rows / columns (>= 1) */
+    int32_t independent;             /* independent regions: no overlap extension */
+    int32_t hyper_decoder_overlap;   /* signalled value (HyperDecoderOverlap = 2 x this) */
+    int32_t mcm_overlap;             /* signalled value (McmOverlap = 4 x this) */
+} zjai_regions;
+
+typedef struct zjai_area {
+    int32_t x, y, width, height;
+} zjai_area;
+
+#define ZJAI_PLANE_LATENT 0       /* y, 1/16 of luma (`Plane::Latent`) */
+#define ZJAI_PLANE_PSI 1          /* hyper-decoder output, 1/32 (`Plane::Psi`) */
+#define ZJAI_PLANE_HYPER_LATENT 2 /* z, 1/64 (`Plane::HyperLatent`) */
+#define ZJAI_PLANE_IMAGE 3        /* the picture in luma samples (`Plane::Image`) */
+
+/* `region_grid(hdr, ccs, plane)` (src/tools/regions.rs:116-150) of a height x width picture for
+ * component 0 (luma) or 1 (chroma): writes up to `cap` core and extended areas (row-major),
+ * *n = count (ZJAI_E_LIMIT if cap is too small). Host only; needs no context. */
+ZJAI_API int32_t zjai_region_grid(int32_t height, int32_t width, int32_t component,
+                                  const zjai_regions* regions, int32_t plane, zjai_area* core,
+                                  zjai_area* extended, int32_t cap, int32_t* n);
+
+/* The float networks of `CommonModel::load` (src/model/common.rs:117-129) for component 0 / 1
+ * (160 / 96 latent channels) from named checkpoint tensors: `HyperDecoder::load`
+ * (src/model/hyper_decoder.rs:24-45, "hyper_decoder.conv1..4") and, when
+ * "context.MCM.0.fusion_pred_net.conv1.weight" is present, `ContextModel::load`
+ * (src/model/mcm.rs:123-159, "context.MCM.{0..3}.{conv.0,conv.1,fusion_pred_net.conv1..3}"). */
+ZJAI_API int32_t zjai_latent_model_create(zjai_ctx* ctx, int32_t component, int32_t precision,
+                                          int32_t n_tensors, const char* const* names,
+                                          const int32_t* ndims, const int32_t* dims,
+                                          const float* const* data, zjai_net** out);
+/* Latent channels of the model and whether it holds a context model. */
+ZJAI_API int32_t zjai_latent_model_info(const zjai_net* net, int32_t* channels, int32_t* has_context);
+/* `HyperDecoder::forward` (src/model/hyper_decoder.rs:47-89): z_hat int8 [c][zh][zw] -> psi
+ * f32 [4c][out_h][out_w] on the host (the 2x upsampled map cropped to out_h x out_w). */
+ZJAI_API int32_t zjai_hyper_decoder_forward(zjai_ctx* ctx, const zjai_net* net, const int8_t* z_hat,
+                                            int32_t c, int32_t zh, int32_t zw, int32_t out_h,
+                                            int32_t out_w, float* psi, size_t len);
+/* `ContextModel::decompress` (src/model/mcm.rs:161-240): dequantised residual f32 [c][h][w] and
+ * psi f32 [4c][psi_h][psi_w] (psi_h = ceil(h/2), psi_w = ceil(w/2)) -> y_hat f32 [c][h][w].
+ * A model without a context model returns the up-shuffled psi plus the residual instead
+ * (src/decoder/reconstruct.rs:191-202, `upshuffle_psi_par` src/model/mcm.rs:742). */
+ZJAI_API int32_t zjai_context_decompress(zjai_ctx* ctx, const zjai_net* net, const float* residual,
+                                         int32_t c, int32_t h, int32_t w, const float* psi,
+                                         int32_t psi_h, int32_t psi_w, float* y_hat, size_t len);
+/* `reconstruct::reconstruct_latent` (src/decoder/reconstruct.rs:81-234) for the model's
+ * component of a height x width picture: hyper-decoder per region on its z window, psi merged
+ * in raster order, context model per region on its residual / psi windows, y_hat merged (whole
+ * latent areas for independent regions, one sample dropped per interior side otherwise).
+ * z_hat int8 [c][zh][zw], residual f32 [c][h][w] -> psi f32 [4c][ceil(h/2)][ceil(w/2)] and y_hat
+ * f32 [c][h][w] on the host (synchronises). */
+ZJAI_API int32_t zjai_reconstruct_latent(zjai_ctx* ctx, const zjai_net* net, int32_t height,
+                                         int32_t width, const zjai_regions* regions,
+                                         const int8_t* z_hat, int32_t zh, int32_t zw,
+                                         const float* residual, int32_t h, int32_t w, float* psi,
+                                         float* y_hat);
+
 #ifdef __cplusplus
 }
 #endif

@@ -191,6 +191,44 @@ def image_region_grid(height, width, rows, columns):
     return RegionGrid(rows, columns, g, g)
 
 
+@dataclass(frozen=True)
+class Regions:
+    """``Regions`` of a picture header: counts, independence, signalled overlaps."""
+    num_ver: int
+    num_hor: int
+    independent: bool = True
+    hyper_decoder_overlap: int = 0
+    mcm_overlap: int = 0
+
+
+# ``Plane`` (src/tools/regions.rs:103-114) -> (depth, extension from (hd, mcm) overlaps).
+_PLANES = {
+    "latent": (4, lambda hd, mcm: mcm >> 1),
+    "psi": (5, lambda hd, mcm: mcm >> 2),
+    "hyper_latent": (6, lambda hd, mcm: hd),
+    "image": (0, lambda hd, mcm: 64 * hd),
+}
+
+
+def region_grid(height, width, ccs, regions, plane):
+    """``region_grid(hdr, ccs, plane)`` (src/tools/regions.rs:120-150); ``regions`` None = not
+    partitioned. Chroma grids are built on the half-size plane scaled back up by 2."""
+    h, w = (height, width) if ccs == 0 else (2 * _ceil(height, 2), 2 * _ceil(width, 2))
+    r = regions if regions is not None else Regions(1, 1, False, 0, 0)
+    partitioned = regions is not None
+    hd, mcm = r.hyper_decoder_overlap * 2, r.mcm_overlap * 4
+    depth, ext = _PLANES[plane]
+    extend = 0 if r.independent else ext(hd, mcm)
+    ver = axis_coords(h, r.num_ver, depth, partitioned)
+    hor = axis_coords(w, r.num_hor, depth, partitioned)
+    return RegionGrid(r.num_ver, r.num_hor, tuple(grid(ver, hor, 0)), tuple(grid(ver, hor, extend)))
+
+
+def hyper_crop(length, divider):
+    """Rows / columns the hyper-decoder crops (src/decoder/reconstruct.rs:67-69)."""
+    return 2 * _ceil(length, 2 * divider) - _ceil(length, divider)
+
+
 def region_counts(height, width):
     if height * width <= NUM_SAMPLES_IN_REGION:
         return None

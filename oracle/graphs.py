@@ -244,3 +244,133 @@ def synthesize(py, puv, op, y_hat, uv_hat, height, width, tiles, sv=1, sh=1, out
 __all__ = ["crop", "res_au", "upsample", "residual_block", "cab", "transformer_block", "tam",
            "light_primary", "hop_primary", "primary", "secondary", "synthesize", "quantize_plane",
            "math"]
+
+
+# ---------------------------------------------------------------------------------------------
+# Latent reconstruction: src/model/hyper_decoder.rs, src/model/mcm.rs, src/decoder/reconstruct.rs
+# ---------------------------------------------------------------------------------------------
+
+# STAGE_POSITIONS (src/model/mcm.rs:26): (row, column) of stage s inside each 2x2 cell.
+STAGE_POSITIONS = ((0, 0), (1, 1), (0, 1), (1, 0))
+
+
+def hyper_decoder(p, z_hat, out_h, out_w):
+    """``HyperDecoder::forward_with`` (src/model/hyper_decoder.rs:58-89): int8 ``[C, hz, wz]``
+    -> psi ``[4C, out_h, out_w]``: conv1x1 -> convT4 s2 p1 -> crop -> relu6 -> conv3x3 ->
+    relu6 -> conv3x3 (C -> 4C)."""
+    x = np.ascontiguousarray(z_hat, dtype=np.float32)
+    x = conv1x1(p, "hyper_decoder.conv1", x)
+    x = conv_transpose2d(x, p["hyper_decoder.conv2.weight"], p["hyper_decoder.conv2.bias"], 2, 1, 0)
+    if x.shape[1:] != (out_h, out_w):
+        x = crop(x, out_h, out_w)
+    x = relu6(x)
+    x = conv3x3(p, "hyper_decoder.conv3", x)
+    x = relu6(x)
+    return conv3x3(p, "hyper_decoder.conv4", x)
+
+
+def _fusion(p, pfx, x):
+    """``FusionPredNet::forward`` (src/model/mcm.rs:60-66)."""
+    x = relu(conv1x1(p, f"{pfx}.conv1", x))
+    x = relu(conv1x1(p, f"{pfx}.conv2", x))
+    return conv1x1(p, f"{pfx}.conv3", x)
+
+
+def context_decompress(p, residual, psi):
+    """``ContextModel::decompress_with`` (src/model/mcm.rs:171-240): residual ``[C, H, W]``,
+    psi ``[4C, ceil(H/2), ceil(W/2)]`` -> y_hat ``[C, H, W]``. Stage s predicts a mean on the
+    half-resolution grid from psi quarter s and (s > 0) the stages so far; the stage becomes
+    mean + residual where its latent sample exists (padded border samples keep the mean)."""
+    c, h, w = residual.shape
+    hh, hw = _ceil(h, 2), _ceil(w, 2)
+    if psi.shape != (4 * c, hh, hw):
+        raise ValueError("context model: residual / psi shape mismatch")
+    y_hat = np.zeros((c, h, w), np.float32)
+    context = None
+    for s, (py, px) in enumerate(STAGE_POSITIONS):
+        pfx = f"context.MCM.{s}"
+        psi_s = psi[s * c:(s + 1) * c]
+        if s == 0:
+            mean = _fusion(p, f"{pfx}.fusion_pred_net", psi_s)
+        else:
+            t = conv1x1(p, f"{pfx}.conv.0", context)
+            t = conv3x3(p, f"{pfx}.conv.1", t, groups=c // 32)
+            mean = _fusion(p, f"{pfx}.fusion_pred_net", np.concatenate([t, psi_s]))
+        stage = mean.copy()
+        ys, xs = np.arange(hh) * 2 + py, np.arange(hw) * 2 + px
+        iy, ix = np.nonzero(ys < h)[0], np.nonzero(xs < w)[0]
+        sub = residual[:, ys[iy]][:, :, xs[ix]]
+        stage[:, iy[:, None], ix[None, :]] = (mean[:, iy[:, None], ix[None, :]] + sub).astype(np.float32)
+        y_hat[:, ys[iy][:, None], xs[ix][None, :]] = stage[:, iy[:, None], ix[None, :]]
+        context = stage if context is None else np.concatenate([context, stage])
+    return y_hat
+
+
+def upshuffle_psi(psi, h, w):
+    """``upshuffle_psi_par`` (src/model/mcm.rs:742-764): psi quarters to latent resolution,
+    sample (y, x) from quarter STAGE_LUT[(y % 2) * 2 + x % 2] at (y / 2, x / 2)."""
+    lut = (0, 2, 3, 1)
+    c = psi.shape[0] // 4
+    if psi.shape[0] % 4 or psi.shape[1] * 2 < h or psi.shape[2] * 2 < w:
+        raise ValueError("upshuffle_psi: shape mismatch")
+    out = np.empty((c, h, w), np.float32)
+    for py in range(2):
+        for px in range(2):
+            q = lut[py * 2 + px]
+            blk = psi[q * c:(q + 1) * c, :_ceil(h - py, 2), :_ceil(w - px, 2)]
+            out[:, py::2, px::2] = blk
+    return out
+
+
+def _assign(dst, core, src, offset):
+    """``assign_par`` (src/decoder/reconstruct.rs:38-62): clamped rectangle copy."""
+    ox, oy = offset
+    h = max(0, min(core.height, src.shape[1] - oy, dst.shape[1] - core.y))
+    w = max(0, min(core.width, src.shape[2] - ox, dst.shape[2] - core.x))
+    c = min(dst.shape[0], src.shape[0])
+    dst[:c, core.y:core.y + h, core.x:core.x + w] = src[:c, oy:oy + h, ox:ox + w]
+
+
+def _window(t, a):
+    if a.y + a.height > t.shape[1] or a.x + a.width > t.shape[2]:
+        raise ValueError("window outside tensor")
+    return np.ascontiguousarray(t[:, a.y:a.y + a.height, a.x:a.x + a.width])
+
+
+def reconstruct_latent(p, ccs, height, width, regions, z_hat, residual, context=True):
+    """``reconstruct_latent_timed`` (src/decoder/reconstruct.rs:104-234) for component ``ccs``
+    of a ``height x width`` picture: ``(psi, y_hat)``. ``context`` says whether the model has
+    a context model (else y_hat = up-shuffled psi + residual)."""
+    from .geometry import hyper_crop, region_grid
+    c, h, w = residual.shape
+    img = region_grid(height, width, ccs, regions, "image")
+    zg = region_grid(height, width, ccs, regions, "hyper_latent")
+    pg = region_grid(height, width, ccs, regions, "psi")
+    lg = region_grid(height, width, ccs, regions, "latent")
+    psi = np.zeros((4 * c, _ceil(h, 2), _ceil(w, 2)), np.float32)
+    for it, zt, core in zip(img.extended, zg.extended, pg.extended):
+        th, tw, div = (it.height, it.width, 32) if ccs == 0 else (_ceil(it.height, 2), _ceil(it.width, 2), 16)
+        out_h, out_w = 2 * zt.height - hyper_crop(th, div), 2 * zt.width - hyper_crop(tw, div)
+        t = hyper_decoder(p, _window(z_hat, zt), out_h, out_w)
+        _assign(psi, core, t, (0, 0))
+    y_hat = np.zeros((c, h, w), np.float32)
+    independent = regions is not None and regions.independent
+    for it, lt, pt in zip(img.extended, lg.extended, pg.extended):
+        res, ps = _window(residual, lt), _window(psi, pt)
+        if context:
+            y = context_decompress(p, res, ps)
+        else:
+            y = (upshuffle_psi(ps, lt.height, lt.width) + res).astype(np.float32)
+        if not independent:
+            # Picture-border branch of ``_get_core_of_overlapping_tile``: one latent sample
+            # (HD_MCM_TILE_OVERLAP / 2 / 16) dropped on every interior side.
+            cut = 48 // 2 // 16
+            left = 0 if it.x == 0 else cut
+            top = 0 if it.y == 0 else cut
+            right = 0 if it.x + it.width >= width else cut
+            bottom = 0 if it.y + it.height >= height else cut
+            core = type(lt)(lt.x + left, lt.y + top, lt.width - left - right, lt.height - top - bottom)
+            _assign(y_hat, core, y, (left, top))
+        else:
+            _assign(y_hat, lt, y, (0, 0))
+    return psi, y_hat

@@ -35,12 +35,22 @@ ACT_NONE, ACT_RELU, ACT_LEAKY_RELU, ACT_SIGMOID = 0, 1, 2, 3
 RES_NONE, RES_ADD, RES_GATE, RES_CAB, RES_MUL = 0, 1, 2, 3, 4
 CTX_UNFUSED_BLOCKS = 0x1  # zjai_ctx_create flag
 RESIZE_BICUBIC, RESIZE_BILINEAR = 0, 1
+PLANE_LATENT, PLANE_PSI, PLANE_HYPER_LATENT, PLANE_IMAGE = 0, 1, 2, 3
 
 
 class ZjaiTile(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
         "image_x", "image_y", "image_w", "image_h", "latent_x", "latent_y", "latent_w",
         "latent_h", "core_x", "core_y", "core_w", "core_h", "core_off_x", "core_off_y")]
+
+
+class ZjaiRegions(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "num_ver", "num_hor", "independent", "hyper_decoder_overlap", "mcm_overlap")]
+
+
+class ZjaiArea(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("x", "y", "width", "height")]
 
 
 class ZjaiStats(ctypes.Structure):
@@ -113,6 +123,17 @@ PROTOTYPES = {
     "zjai_picture_download": [_vp, _vp, _vp, _vp, _vp],
     "zjai_resize": [_vp, _i32, _f32p, _i32, _i32, _i32, _i32, _i32, _f32p],
     "zjai_picture_download_rgb": [_vp, _vp, _i32, _vp, _f32p],
+    "zjai_region_grid": [_i32, _i32, _i32, ctypes.POINTER(ZjaiRegions), _i32,
+                         ctypes.POINTER(ZjaiArea), ctypes.POINTER(ZjaiArea), _i32, _i32p],
+    "zjai_latent_model_create": [_vp, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_char_p), _i32p,
+                                 _i32p, ctypes.POINTER(_f32p), _pp],
+    "zjai_latent_model_info": [_vp, _i32p, _i32p],
+    "zjai_hyper_decoder_forward": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32p,
+                                   ctypes.c_size_t],
+    "zjai_context_decompress": [_vp, _vp, _f32p, _i32, _i32, _i32, _f32p, _i32, _i32, _f32p,
+                                ctypes.c_size_t],
+    "zjai_reconstruct_latent": [_vp, _vp, _i32, _i32, ctypes.POINTER(ZjaiRegions), _vp, _i32,
+                                _i32, _f32p, _i32, _i32, _f32p, _f32p],
 }
 
 _lib = None

@@ -409,6 +409,21 @@ extern "C" int32_t zjai_channel_attention(zjai_ctx* ctx, const zjai_tensor* qkv,
 }
 
 // ----------------------------------------------------------------------------------- nets
+static std::map<std::string, Param> params_of(int32_t n_tensors, const char* const* names, const int32_t* ndims,
+                                              const int32_t* dims, const float* const* data) {
+    std::map<std::string, Param> P;
+    const int32_t* d = dims;
+    for (int i = 0; i < n_tensors; ++i) {
+        need(names[i] != nullptr && ndims[i] >= 0 && ndims[i] <= 8, "tensor descriptor");
+        Param p;
+        p.shape.assign(d, d + ndims[i]);
+        d += ndims[i];
+        p.data = data[i];
+        P[names[i]] = p;
+    }
+    return P;
+}
+
 extern "C" int32_t zjai_net_create(zjai_ctx* ctx, int32_t op, int32_t component, int32_t precision,
                                    int32_t n_tensors, const char* const* names, const int32_t* ndims,
                                    const int32_t* dims, const float* const* data, zjai_net** out) {
@@ -416,17 +431,7 @@ extern "C" int32_t zjai_net_create(zjai_ctx* ctx, int32_t op, int32_t component,
         return ZJAI_E_INVALID_ARGUMENT;
     return guard(ctx, [&] {
         need(precision >= DT_F32 && precision <= DT_BF16, "precision");
-        std::map<std::string, Param> P;
-        const int32_t* d = dims;
-        for (int i = 0; i < n_tensors; ++i) {
-            need(names[i] != nullptr && ndims[i] >= 0 && ndims[i] <= 8, "tensor descriptor");
-            Param p;
-            p.shape.assign(d, d + ndims[i]);
-            d += ndims[i];
-            p.data = data[i];
-            P[names[i]] = p;
-        }
-        *out = new zjai_net{build_net(ctx->c, op, component, precision, P)};
+        *out = new zjai_net{build_net(ctx->c, op, component, precision, params_of(n_tensors, names, ndims, dims, data))};
     });
 }
 
@@ -436,7 +441,7 @@ extern "C" int32_t zjai_net_destroy(zjai_net* net) {
 }
 
 extern "C" int32_t zjai_net_out_size(const zjai_net* net, int32_t h, int32_t w, int32_t* oh, int32_t* ow) {
-    if (!net || !oh || !ow || h <= 0 || w <= 0) return ZJAI_E_INVALID_ARGUMENT;
+    if (!net || !oh || !ow || h <= 0 || w <= 0 || net->n->kind != NET_SYNTHESIS) return ZJAI_E_INVALID_ARGUMENT;
     if (net->n->comp == COMP_Y) primary_out_size(net->n->op, h, w, oh, ow);
     else secondary_out_size(net->n->op, h, w, oh, ow);
     return ZJAI_OK;
@@ -470,7 +475,7 @@ extern "C" int32_t zjai_primary_forward(zjai_ctx* ctx, const zjai_net* net, cons
                                         int32_t h, int32_t w, float* out, size_t len) {
     if (!ctx || !net || !y_hat) return ZJAI_E_INVALID_ARGUMENT;
     return guard(ctx, [&] {
-        need(net->n->comp == COMP_Y, "not a primary net");
+        need(net->n->kind == NET_SYNTHESIS && net->n->comp == COMP_Y, "not a primary net");
         need(y_hat->t->dtype == net->n->dtype, "latent precision differs from the net");
         run_to_host(ctx, net, y_hat->t, nullptr, h, w, out, len);
     });
@@ -481,7 +486,7 @@ extern "C" int32_t zjai_secondary_forward(zjai_ctx* ctx, const zjai_net* net, co
                                           size_t len) {
     if (!ctx || !net || !y_luma || !y_chroma) return ZJAI_E_INVALID_ARGUMENT;
     return guard(ctx, [&] {
-        need(net->n->comp == COMP_UV, "not a secondary net");
+        need(net->n->kind == NET_SYNTHESIS && net->n->comp == COMP_UV, "not a secondary net");
         run_to_host(ctx, net, y_luma->t, y_chroma->t, h, w, out, len);
     });
 }
@@ -642,8 +647,10 @@ extern "C" int32_t zjai_picture_create(zjai_ctx* ctx, const zjai_net* net_y, con
                                        int32_t out_h, int32_t out_w, int32_t bit_depth, zjai_picture** out) {
     if (!ctx || !net_y || !out || !tiles || n_tiles <= 0) return ZJAI_E_INVALID_ARGUMENT;
     return guard(ctx, [&] {
-        need(net_y->n->comp == COMP_Y, "net_y is not a primary net");
-        need(!net_uv || (net_uv->n->comp == COMP_UV && net_uv->n->op == net_y->n->op), "net_uv mismatch");
+        need(net_y->n->kind == NET_SYNTHESIS && net_y->n->comp == COMP_Y, "net_y is not a primary net");
+        need(!net_uv || (net_uv->n->kind == NET_SYNTHESIS && net_uv->n->comp == COMP_UV &&
+                         net_uv->n->op == net_y->n->op),
+             "net_uv mismatch");
         need(!net_uv || net_uv->n->dtype == net_y->n->dtype, "nets differ in precision");
         need(lh > 0 && lw > 0 && height > 0 && width > 0, "sizes");
         need(sv >= 1 && sv <= 2 && sh >= 1 && sh <= 2, "chroma subsampling");
@@ -854,5 +861,120 @@ extern "C" int32_t zjai_picture_download_rgb(zjai_ctx* ctx, zjai_picture* pic, i
         if (rgb_planes)
             ZJAI_HIP(hipMemcpyAsync(rgb_planes, pic->out_rgbf, n * 3 * sizeof(float), hipMemcpyDeviceToHost, cx.stream));
         ZJAI_HIP(hipStreamSynchronize(cx.stream));
+    });
+}
+
+// ------------------------------------------------------------------ latent reconstruction
+static RegionParams region_params(const zjai_regions* r) {
+    RegionParams p;
+    if (!r) return p;
+    need(r->num_ver >= 1 && r->num_hor >= 1, "region counts must be positive");
+    need(r->hyper_decoder_overlap >= 0 && r->mcm_overlap >= 0, "negative region overlap");
+    p.partitioned = true;
+    p.independent = r->independent != 0;
+    p.num_ver = r->num_ver;
+    p.num_hor = r->num_hor;
+    p.hyper_decoder_overlap = r->hyper_decoder_overlap;
+    p.mcm_overlap = r->mcm_overlap;
+    return p;
+}
+
+extern "C" int32_t zjai_region_grid(int32_t height, int32_t width, int32_t component, const zjai_regions* regions,
+                                    int32_t plane, zjai_area* core, zjai_area* extended, int32_t cap, int32_t* n) {
+    if (!n || cap < 0 || (cap > 0 && (!core || !extended))) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] {
+        need(component == 0 || component == 1, "component");
+        const RegionGrid g = region_grid(height, width, component, region_params(regions), plane);
+        *n = (int32_t)g.core.size();
+        if (*n > cap) throw Error(ZJAI_E_LIMIT, "zjai_region_grid: capacity too small");
+        for (int i = 0; i < *n; ++i) {
+            core[i] = zjai_area{g.core[i].x, g.core[i].y, g.core[i].w, g.core[i].h};
+            extended[i] = zjai_area{g.extended[i].x, g.extended[i].y, g.extended[i].w, g.extended[i].h};
+        }
+    });
+}
+
+extern "C" int32_t zjai_latent_model_create(zjai_ctx* ctx, int32_t component, int32_t precision, int32_t n_tensors,
+                                            const char* const* names, const int32_t* ndims, const int32_t* dims,
+                                            const float* const* data, zjai_net** out) {
+    if (!ctx || !out || n_tensors < 0 || (n_tensors && (!names || !ndims || !dims || !data)))
+        return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(precision >= DT_F32 && precision <= DT_BF16, "precision");
+        *out = new zjai_net{build_latent_net(ctx->c, component, precision, params_of(n_tensors, names, ndims, dims, data))};
+    });
+}
+
+extern "C" int32_t zjai_latent_model_info(const zjai_net* net, int32_t* channels, int32_t* has_context) {
+    if (!net || !channels || !has_context || net->n->kind != NET_LATENT) return ZJAI_E_INVALID_ARGUMENT;
+    *channels = net->n->chs;
+    *has_context = net->n->context ? 1 : 0;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_hyper_decoder_forward(zjai_ctx* ctx, const zjai_net* net, const int8_t* z_hat, int32_t c,
+                                              int32_t zh, int32_t zw, int32_t out_h, int32_t out_w, float* psi,
+                                              size_t len) {
+    if (!ctx || !net || !z_hat || !psi) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        const Net& m = *net->n;
+        need(m.kind == NET_LATENT, "not a latent model");
+        need(c == m.chs && zh > 0 && zw > 0, "z_hat shape");
+        need(out_h > 0 && out_w > 0 && out_h <= 2 * zh && out_w <= 2 * zw, "psi size");
+        need(len >= (size_t)4 * c * out_h * out_w, "output buffer too small");
+        Context& cx = ctx->c;
+        const size_t zn = (size_t)c * zh * zw;
+        void* zdev = cx.pool.alloc(zn);
+        std::shared_ptr<void> keep(zdev, [&cx](void* q) { cx.pool.release(q); });
+        ZJAI_HIP(hipMemcpyAsync(zdev, z_hat, zn, hipMemcpyHostToDevice, cx.stream));
+        TensorP z = cx.alloc(1, c, zh, zw, m.dtype);
+        {
+            LaunchScope sc(cx, kname("k_i8_planar_to_nhwc", m.dtype), 0.0, (1.0 + dtype_size(m.dtype)) * zn);
+            ZJAI_HIP(launch_i8_planar_to_nhwc((const int8_t*)zdev, c, zh, zw, 0, 0, zh, zw, z->v, m.dtype, cx.stream));
+        }
+        TensorP t = hyper_decoder_forward(cx, m, z, out_h, out_w);
+        const size_t pn = (size_t)4 * c * out_h * out_w;
+        float* dev = (float*)cx.pool.alloc(pn * 4);
+        std::shared_ptr<void> keep2(dev, [&cx](void* q) { cx.pool.release(q); });
+        {
+            LaunchScope sc(cx, kname("k_nhwc_to_planar", m.dtype), 0.0, (4.0 + dtype_size(m.dtype)) * pn);
+            ZJAI_HIP(launch_nhwc_to_planar(t->v, m.dtype, 1, 4 * c, out_h, out_w, dev, cx.stream));
+        }
+        ZJAI_HIP(hipMemcpyAsync(psi, dev, pn * 4, hipMemcpyDeviceToHost, cx.stream));
+        ZJAI_HIP(hipStreamSynchronize(cx.stream));
+    });
+}
+
+extern "C" int32_t zjai_context_decompress(zjai_ctx* ctx, const zjai_net* net, const float* residual, int32_t c,
+                                           int32_t h, int32_t w, const float* psi, int32_t psi_h, int32_t psi_w,
+                                           float* y_hat, size_t len) {
+    if (!ctx || !net || !residual || !psi || !y_hat) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        const Net& m = *net->n;
+        need(m.kind == NET_LATENT, "not a latent model");
+        need(c == m.chs && h > 0 && w > 0 && psi_h > 0 && psi_w > 0, "residual / psi shape");
+        need(len >= (size_t)c * h * w, "output buffer too small");
+        Context& cx = ctx->c;
+        const size_t rn = (size_t)c * h * w;
+        TensorP ps = planar_upload(cx, psi, 4 * c, psi_h, psi_w, m.dtype);
+        float* rdev = (float*)cx.pool.alloc(rn * 4);
+        std::shared_ptr<void> keep(rdev, [&cx](void* q) { cx.pool.release(q); });
+        float* ydev = (float*)cx.pool.alloc(rn * 4);
+        std::shared_ptr<void> keep2(ydev, [&cx](void* q) { cx.pool.release(q); });
+        ZJAI_HIP(hipMemcpyAsync(rdev, residual, rn * 4, hipMemcpyHostToDevice, cx.stream));
+        latent_decompress(cx, m, rdev, w, (long long)h * w, h, w, ps, ydev);
+        ZJAI_HIP(hipMemcpyAsync(y_hat, ydev, rn * 4, hipMemcpyDeviceToHost, cx.stream));
+        ZJAI_HIP(hipStreamSynchronize(cx.stream));
+    });
+}
+
+extern "C" int32_t zjai_reconstruct_latent(zjai_ctx* ctx, const zjai_net* net, int32_t height, int32_t width,
+                                           const zjai_regions* regions, const int8_t* z_hat, int32_t zh, int32_t zw,
+                                           const float* residual, int32_t h, int32_t w, float* psi, float* y_hat) {
+    if (!ctx || !net || !z_hat || !residual || !psi || !y_hat) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(net->n->kind == NET_LATENT, "not a latent model");
+        reconstruct_latent(ctx->c, *net->n, height, width, region_params(regions), z_hat, zh, zw, residual, h, w, psi,
+                           y_hat);
     });
 }

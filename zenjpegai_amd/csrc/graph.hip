@@ -186,6 +186,38 @@ NetP build_net(Context& ctx, int op, int comp, int dtype, const std::map<std::st
     return net;
 }
 
+NetP build_latent_net(Context& ctx, int comp, int dtype, const std::map<std::string, Param>& params) {
+    if (comp < COMP_Y || comp > COMP_UV) throw Error(ZJAI_E_INVALID_ARGUMENT, "latent model: unknown component");
+    auto net = std::make_shared<Net>();
+    net->kind = NET_LATENT;
+    net->comp = comp;
+    net->dtype = dtype;
+    const int c = comp == COMP_Y ? 160 : 96;  // LATENT_CHANNELS (src/header.rs:31)
+    net->chs = c;
+    Builder b{ctx, *net, params};
+    // HyperDecoder::load (src/model/hyper_decoder.rs:24-45)
+    b.conv1x1("hyper_decoder.conv1", c, c, false);
+    b.conv_t("hyper_decoder.conv2", c, c, 4, 1, 0);
+    b.conv3x3("hyper_decoder.conv3", c, c, 1, true);
+    b.conv3x3("hyper_decoder.conv4", c, 4 * c, 1, true);
+    // ContextModel::load (src/model/mcm.rs:123-159), when the checkpoint has one
+    // (src/model/common.rs:117-121).
+    if (params.count("context.MCM.0.fusion_pred_net.conv1.weight")) {
+        net->context = true;
+        for (int s = 0; s < 4; ++s) {
+            const std::string p = "context.MCM." + std::to_string(s);
+            if (s > 0) {
+                b.conv1x1(p + ".conv.0", s * c, c, false);
+                b.conv3x3(p + ".conv.1", c, c, c / 32, true);
+            }
+            b.conv1x1(p + ".fusion_pred_net.conv1", s == 0 ? c : 2 * c, c, false);
+            b.conv1x1(p + ".fusion_pred_net.conv2", c, c, false);
+            b.conv1x1(p + ".fusion_pred_net.conv3", c, c, false);
+        }
+    }
+    return net;
+}
+
 // -------------------------------------------------------------------------------- forward
 namespace {
 
@@ -535,6 +567,80 @@ void secondary_forward(Context& ctx, const Net& net, const TensorP& y_luma, cons
     Epilogue e;
     e.ps = 8;
     f.conv("conv4", x, e, nullptr, &out);
+}
+
+TensorP hyper_decoder_forward(Context& ctx, const Net& net, const TensorP& z, int out_h, int out_w) {
+    if (net.kind != NET_LATENT) throw Error(ZJAI_E_INVALID_ARGUMENT, "hyper-decoder: not a latent model");
+    if (z->c != net.chs || z->n != 1 || z->dtype != net.dtype)
+        throw Error(ZJAI_E_INVALID_ARGUMENT, "hyper-decoder: z_hat channels / precision differ from the model");
+    Fwd f{ctx, net};
+    TensorP x = f.conv("hyper_decoder.conv1", z);
+    ctx.check_stop();
+    x = f.conv("hyper_decoder.conv2", x);
+    if (x->h != out_h || x->w != out_w) {
+        if (out_h <= 0 || out_w <= 0 || out_h > x->h || out_w > x->w)
+            throw Error(ZJAI_E_INVALID_ARGUMENT, "hyper-decoder: crop larger than the upsampled map");
+        x = crop_view(x, out_h, out_w);
+    }
+    ctx.check_stop();
+    // relu6 after the crop and after conv3 run as relu6 on the next conv's loads.
+    Epilogue e;
+    e.relu6_in = 1;
+    x = f.conv("hyper_decoder.conv3", x, e);
+    ctx.check_stop();
+    return f.conv("hyper_decoder.conv4", x, e);
+}
+
+void latent_decompress(Context& ctx, const Net& net, const float* res, long long res_row, long long res_plane,
+                       int H, int W, const TensorP& psi, float* y_hat) {
+    if (net.kind != NET_LATENT) throw Error(ZJAI_E_INVALID_ARGUMENT, "context model: not a latent model");
+    const int C = net.chs, dt = net.dtype;
+    if (psi->dtype != dt || psi->n != 1) throw Error(ZJAI_E_INVALID_ARGUMENT, "context model: psi precision");
+    if (H <= 0 || W <= 0) throw Error(ZJAI_E_INVALID_ARGUMENT, "context model: empty residual");
+    if (!net.context) {
+        // upshuffle_psi_par (src/model/mcm.rs:742-746) checks
+        if (psi->c != 4 * C || 2 * psi->h < H || 2 * psi->w < W)
+            throw Error(ZJAI_E_INVALID_ARGUMENT, "upshuffle_psi: shape mismatch");
+        LaunchScope sc(ctx, kname("k_upshuffle_psi", dt), 0.0, (double)C * H * W * (8.0 + dtype_size(dt)));
+        ZJAI_HIP(launch_upshuffle_psi(psi->v, dt, C, psi->h, psi->w, res, res_row, res_plane, H, W, y_hat,
+                                      ctx.stream));
+        return;
+    }
+    const int hh = ceil_div(H, 2), hw = ceil_div(W, 2);
+    if (psi->c != 4 * C || psi->h != hh || psi->w != hw)
+        throw Error(ZJAI_E_INVALID_ARGUMENT, "context model: residual / psi shape mismatch");
+    // STAGE_POSITIONS (src/model/mcm.rs:26): (row, column) of each stage in the 2x2 cell.
+    static const int pos[4][2] = {{0, 0}, {1, 1}, {0, 1}, {1, 0}};
+    Fwd f{ctx, net};
+    // The reconstructed stages, concatenated along channels: stage s lands in [s C, (s + 1) C).
+    TensorP stages = ctx.alloc(1, 4 * C, hh, hw, dt);
+    const double es = dtype_size(dt);
+    for (int s = 0; s < 4; ++s) {
+        ctx.check_stop();
+        const std::string p = "context.MCM." + std::to_string(s);
+        TensorP psi_s = channel_view(psi, s * C, C);
+        TensorP in = psi_s;
+        if (s > 0) {
+            TensorP t = f.conv(p + ".conv.0", channel_view(stages, 0, s * C));
+            TensorP joined = ctx.alloc(1, 2 * C, hh, hw, dt);
+            f.conv(p + ".conv.1", t, Epilogue{}, channel_view(joined, 0, C));
+            {
+                LaunchScope sc(ctx, kname("k_copy", dt), 0.0, 2.0 * es * C * hh * hw);
+                ZJAI_HIP(launch_copy(psi_s->v, channel_view(joined, C, C)->v, dt, 1, C, hh, hw, ctx.stream));
+            }
+            in = joined;
+        }
+        // FusionPredNet::forward (src/model/mcm.rs:60-66)
+        Epilogue er;
+        er.act = ACT_RELU;
+        TensorP a = f.conv(p + ".fusion_pred_net.conv1", in, er);
+        a = f.conv(p + ".fusion_pred_net.conv2", a, er);
+        TensorP st = channel_view(stages, s * C, C);
+        f.conv(p + ".fusion_pred_net.conv3", a, Epilogue{}, st);
+        LaunchScope sc(ctx, kname("k_mcm_stage", dt), 0.0, (double)C * hh * hw * (2.0 * es + 8.0));
+        ZJAI_HIP(launch_mcm_stage(st->v, dt, C, hh, hw, res, res_row, res_plane, H, W, pos[s][0], pos[s][1], y_hat,
+                                  ctx.stream));
+    }
 }
 
 }  // namespace zjai

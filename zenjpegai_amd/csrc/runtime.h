@@ -211,8 +211,13 @@ struct Param {
     const float* data;
 };
 
+enum NetKind : int { NET_SYNTHESIS = 0, NET_LATENT = 1 };
+
 struct Net {
+    int kind = NET_SYNTHESIS;
     int op = 0, comp = 0, dtype = DT_F32;
+    int chs = 0;           // latent nets: latent channels (160 luma, 96 chroma)
+    bool context = false;  // latent nets: a multi-stage context model is present
     std::map<std::string, LayerP> L;
     std::map<std::string, float*> vec;  // device f32 vectors (layer norm, temperature)
     ~Net();
@@ -229,5 +234,43 @@ void secondary_forward(Context& ctx, const Net& net, const TensorP& y_luma,
                        const TensorP& y_chroma, int h, int w, const PlaneOut& out);
 void primary_out_size(int op, int h, int w, int* oh, int* ow);
 void secondary_out_size(int op, int h, int w, int* oh, int* ow);
+
+// ------------------------------------------------------------------- latent reconstruction
+// The float networks of `CommonModel::load` (src/model/common.rs:117-129) for component comp
+// (160 / 96 latent channels): the hyper-decoder and, when the checkpoint holds one, the
+// multi-stage context model.
+NetP build_latent_net(Context& ctx, int comp, int dtype, const std::map<std::string, Param>& params);
+// `HyperDecoder::forward_with` (src/model/hyper_decoder.rs:58-89): z (NHWC, C channels) -> psi
+// (NHWC, 4C channels, out_h x out_w).
+TensorP hyper_decoder_forward(Context& ctx, const Net& net, const TensorP& z, int out_h, int out_w);
+// `ContextModel::decompress_with` (src/model/mcm.rs:171-240), or for a net without a context
+// model the up-shuffled psi plus the residual (src/decoder/reconstruct.rs:191-202): residual
+// planar f32 on the device ([C] planes of H x W with the given row / plane strides) and psi
+// (NHWC, 4C, ceil(H/2) x ceil(W/2)) -> y_hat planar f32 [C][H][W] on the device.
+void latent_decompress(Context& ctx, const Net& net, const float* res, long long res_row, long long res_plane,
+                       int H, int W, const TensorP& psi, float* y_hat);
+
+// Region geometry (src/tools/regions.rs:47-150).
+enum RegionPlane : int { PLANE_LATENT = 0, PLANE_PSI = 1, PLANE_HYPER_LATENT = 2, PLANE_IMAGE = 3 };
+struct RegionParams {
+    bool partitioned = false, independent = false;
+    int num_ver = 1, num_hor = 1;
+    int hyper_decoder_overlap = 0, mcm_overlap = 0;  // signalled values
+};
+struct RArea {
+    int x = 0, y = 0, w = 0, h = 0;
+};
+struct RegionGrid {
+    int rows = 1, cols = 1;
+    std::vector<RArea> core, extended;
+};
+// `region_grid(hdr, ccs, plane)` of a height x width picture (luma samples).
+RegionGrid region_grid(int height, int width, int ccs, const RegionParams& r, int plane);
+// `reconstruct_latent` (src/decoder/reconstruct.rs:81-234) of the net's component: host z_hat
+// int8 [C][zh][zw] and dequantised residual f32 [C][H][W] -> host psi f32
+// [4C][ceil(H/2)][ceil(W/2)] and y_hat f32 [C][H][W] (synchronises).
+void reconstruct_latent(Context& ctx, const Net& net, int height, int width, const RegionParams& r,
+                        const int8_t* z_hat, int zh, int zw, const float* residual, int H, int W,
+                        float* psi, float* y_hat);
 
 }  // namespace zjai

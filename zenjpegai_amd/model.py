@@ -13,7 +13,8 @@ from ._lib import HipError, check, lib
 from .nn import BTensor, Engine, _f32, _fp
 
 
-def _net_create(eng: Engine, op: str, component: int, params: dict):
+def _descriptors(params: dict):
+    """(n, names, ndims, dims, data pointers, arrays kept alive) of named checkpoint tensors."""
     names, ndims, dims, ptrs, keep = [], [], [], [], []
     for name, arr in params.items():
         a = _f32(arr)
@@ -27,6 +28,11 @@ def _net_create(eng: Engine, op: str, component: int, params: dict):
     c_ndims = (ctypes.c_int32 * n)(*ndims)
     c_dims = (ctypes.c_int32 * max(len(dims), 1))(*dims)
     c_ptrs = (ctypes.POINTER(ctypes.c_float) * n)(*ptrs)
+    return n, c_names, c_ndims, c_dims, c_ptrs, keep
+
+
+def _net_create(eng: Engine, op: str, component: int, params: dict):
+    n, c_names, c_ndims, c_dims, c_ptrs, _keep = _descriptors(params)
     h = ctypes.c_void_p()
     check(lib().zjai_net_create(eng.handle, _lib.OPS[op], component, eng.dtype, n, c_names,
                                 c_ndims, c_dims, c_ptrs, ctypes.byref(h)), eng.handle)
@@ -216,3 +222,113 @@ def synthesize(eng: Engine, primary, secondary, y_hat, uv_hat, height, width, ti
     pic.upload(y_hat, uv_hat)
     pic.run()
     return pic.download()
+
+
+# ---------------------------------------------------------------------------------------------
+# Latent reconstruction (src/decoder/reconstruct.rs:81-234)
+# ---------------------------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class Regions:
+    """Region partitioning of a picture header (``Regions``, src/header.rs): region rows and
+    columns, independence and the signalled overlaps (hyper-decoder x2, context model x4)."""
+    num_ver: int
+    num_hor: int
+    independent: bool = True
+    hyper_decoder_overlap: int = 0
+    mcm_overlap: int = 0
+
+    def _c(self):
+        return _lib.ZjaiRegions(self.num_ver, self.num_hor, int(self.independent),
+                                self.hyper_decoder_overlap, self.mcm_overlap)
+
+
+PLANES = {"latent": _lib.PLANE_LATENT, "psi": _lib.PLANE_PSI,
+          "hyper_latent": _lib.PLANE_HYPER_LATENT, "image": _lib.PLANE_IMAGE}
+
+
+def _regions_ptr(regions):
+    if regions is None:
+        return None, None
+    r = regions._c()
+    return r, ctypes.byref(r)
+
+
+def region_grid(height: int, width: int, ccs: int, regions: Regions | None, plane: str):
+    """``region_grid(hdr, ccs, plane)`` (src/tools/regions.rs:116-150): ``(core, extended)``,
+    lists of ``Area`` in row-major region order. ``regions=None``: not partitioned."""
+    cap = 64
+    core = (_lib.ZjaiArea * cap)()
+    ext = (_lib.ZjaiArea * cap)()
+    n = ctypes.c_int32()
+    _keep, rp = _regions_ptr(regions)
+    check(lib().zjai_region_grid(height, width, ccs, rp, PLANES[plane], core, ext, cap,
+                                 ctypes.byref(n)))
+    conv = lambda a: Area(a.x, a.y, a.width, a.height)  # noqa: E731
+    return [conv(core[i]) for i in range(n.value)], [conv(ext[i]) for i in range(n.value)]
+
+
+class LatentModel:
+    """The float half of ``CommonModel`` (src/model/common.rs:117-129) for one component: the
+    ``HyperDecoder`` and, when the checkpoint holds one, the multi-stage ``ContextModel``."""
+
+    def __init__(self, eng: Engine, params: dict, component: int):
+        self.eng = eng
+        self.component = component
+        n, c_names, c_ndims, c_dims, c_ptrs, _keep = _descriptors(params)
+        self._h = ctypes.c_void_p()
+        check(lib().zjai_latent_model_create(eng.handle, component, eng.dtype, n, c_names, c_ndims,
+                                             c_dims, c_ptrs, ctypes.byref(self._h)), eng.handle)
+        c, ctx = ctypes.c_int32(), ctypes.c_int32()
+        check(lib().zjai_latent_model_info(self._h, ctypes.byref(c), ctypes.byref(ctx)))
+        self.channels, self.has_context = c.value, bool(ctx.value)
+
+    @classmethod
+    def load(cls, params: dict, component: int, eng: Engine):
+        return cls(eng, params, component)
+
+    def hyper_decoder(self, z_hat: np.ndarray, out_h: int, out_w: int) -> np.ndarray:
+        """``HyperDecoder::forward`` (src/model/hyper_decoder.rs:47): int8 ``[C, hz, wz]`` ->
+        psi ``[4C, out_h, out_w]``."""
+        z = np.ascontiguousarray(z_hat, dtype=np.int8)
+        c, zh, zw = z.shape
+        out = np.empty((4 * c, out_h, out_w), np.float32)
+        check(lib().zjai_hyper_decoder_forward(self.eng.handle, self._h, z.ctypes.data, c, zh, zw,
+                                               out_h, out_w, _fp(out), out.size), self.eng.handle)
+        return out
+
+    def decompress(self, residual: np.ndarray, psi: np.ndarray) -> np.ndarray:
+        """``ContextModel::decompress`` (src/model/mcm.rs:161), or the up-shuffled psi plus the
+        residual without a context model: residual ``[C, h, w]``, psi ``[4C, ceil(h/2),
+        ceil(w/2)]`` -> y_hat ``[C, h, w]``."""
+        r = np.ascontiguousarray(residual, dtype=np.float32)
+        p = np.ascontiguousarray(psi, dtype=np.float32)
+        c, h, w = r.shape
+        out = np.empty_like(r)
+        check(lib().zjai_context_decompress(self.eng.handle, self._h, _fp(r), c, h, w, _fp(p),
+                                            p.shape[1], p.shape[2], _fp(out), out.size),
+              self.eng.handle)
+        return out
+
+    def reconstruct(self, height: int, width: int, regions: Regions | None, z_hat: np.ndarray,
+                    residual: np.ndarray):
+        """``reconstruct_latent`` (src/decoder/reconstruct.rs:81): ``(psi, y_hat)`` of this
+        component of a ``height x width`` picture."""
+        z = np.ascontiguousarray(z_hat, dtype=np.int8)
+        r = np.ascontiguousarray(residual, dtype=np.float32)
+        c, h, w = r.shape
+        psi = np.empty((4 * c, -(-h // 2), -(-w // 2)), np.float32)
+        y = np.empty_like(r)
+        _keep, rp = _regions_ptr(regions)
+        check(lib().zjai_reconstruct_latent(self.eng.handle, self._h, height, width, rp,
+                                            z.ctypes.data, z.shape[1], z.shape[2], _fp(r), h, w,
+                                            _fp(psi), _fp(y)), self.eng.handle)
+        return psi, y
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib().zjai_net_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass

@@ -223,3 +223,57 @@ def random_params(op: str, component: str, seed: int = 1, gain: float = 1.0,
         else:
             params[name] = np.zeros(shape, np.float32)
     return params
+
+
+# ---------------------------------------------------------------------------------------------
+# Latent reconstruction networks (hyper-decoder + multi-stage context model) of one component.
+# ---------------------------------------------------------------------------------------------
+
+LATENT_CHANNELS = (160, 96)  # src/header.rs:31
+
+
+def latent_param_specs(component: int, context: bool = True):
+    """``[(name, shape, kind)]`` of a component's ``HyperDecoder`` (src/model/hyper_decoder.rs:
+    24-45) and, with ``context``, its ``ContextModel`` (src/model/mcm.rs:123-159)."""
+    c = LATENT_CHANNELS[component]
+    t: list = []
+    _conv1(t, "hyper_decoder.conv1", c, c, False)
+    _conv_t(t, "hyper_decoder.conv2", c, c, 4)
+    _conv3(t, "hyper_decoder.conv3", c, c)
+    _conv3(t, "hyper_decoder.conv4", c, 4 * c)
+    if context:
+        for s in range(4):
+            p = f"context.MCM.{s}"
+            if s > 0:
+                _conv1(t, f"{p}.conv.0", s * c, c, False)
+                t.append((f"{p}.conv.1.weight", (c, 32, 3, 3), "conv"))
+                t.append((f"{p}.conv.1.bias", (c,), "bias"))
+            _conv1(t, f"{p}.fusion_pred_net.conv1", c if s == 0 else 2 * c, c, False)
+            _conv1(t, f"{p}.fusion_pred_net.conv2", c, c, False)
+            _conv1(t, f"{p}.fusion_pred_net.conv3", c, c, False)
+    return t
+
+
+def random_latent_params(component: int, seed: int = 1, gain: float = 1.0,
+                         context: bool = True) -> dict:
+    """He-normal random-init parameters of a component's latent reconstruction networks."""
+    params = {}
+    for name, shape, kind in latent_param_specs(component, context):
+        tag = f"latent/{component}/{name}"
+        if kind == "conv":
+            params[name] = normal(seed, tag, shape, gain * np.sqrt(2.0 / (shape[1] * shape[2] * shape[3])))
+        elif kind == "convt":
+            params[name] = normal(seed, tag, shape, gain * np.sqrt(2.0 / (shape[0] * (shape[2] / 2.0) ** 2)))
+        else:
+            params[name] = normal(seed, tag, shape, 0.01)
+    return params
+
+
+def hyper_latent(seed: int, name: str, c: int, h: int, w: int, b: float = 1.5) -> np.ndarray:
+    """int8 ``z_hat`` ``[c, h, w]``: ``round(Laplace(0, b))`` clamped to the int8 range."""
+    return np.clip(latent(seed, name, c, h, w, b), -128, 127).astype(np.int8)
+
+
+def residual(seed: int, name: str, c: int, h: int, w: int, b: float = 0.5) -> np.ndarray:
+    """A dequantised residual ``[c, h, w]``: continuous Laplace(0, b) samples."""
+    return laplace(seed, name, (c, h, w), b)
