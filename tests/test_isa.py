@@ -1,0 +1,104 @@
+"""CPU check of the gfx950 machine code of the library built here (disassembled with the ROCm
+LLVM tools): no MFMA accumulates onto the result of an MFMA issued fewer than
+``MIN_RENAMED_DISTANCE`` instructions earlier while writing a different register range.
+
+Why: on MI355X an MFMA chain that renames its accumulator back to back -- ``v_mfma a[12:15],
+.., a[12:15]`` immediately followed by ``v_mfma a[24:27], .., a[12:15]`` -- produced wrong sums
+(the last accumulator register missed the earlier product), and the compiler emitted no wait
+states for it. In-place chains (destination = srcC) are fine back to back, and renamed chains
+six or more instructions apart (the fused transformer kernels have such) pass the GPU
+bit-identity tests. Register pressure in a kernel variant is what makes the compiler rename, so
+this guard runs on every build of every kernel."""
+
+import os
+import re
+import shutil
+import subprocess
+import tempfile
+
+import pytest
+
+from zenjpegai_amd import _lib
+
+LLVM = "/opt/rocm/llvm/bin"
+MIN_RENAMED_DISTANCE = 4
+MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
+TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
+
+_MFMA = re.compile(r"^\s*(v_mfma_\S+)\s+([av]\[\d+:\d+\]),\s*([^,]+),\s*([^,]+),\s*([av]\[\d+:\d+\]|[^\s/]+)")
+_KERNEL = re.compile(r"^[0-9a-f]+ <(\S+)>:")
+
+
+def _range(reg):
+    m = re.match(r"([av])\[(\d+):(\d+)\]", reg)
+    return (m.group(1), int(m.group(2)), int(m.group(3))) if m else None
+
+
+def _overlap(a, b):
+    return a is not None and b is not None and a[0] == b[0] and not (a[2] < b[1] or b[2] < a[1])
+
+
+def renamed_chains(disasm: str, window: int = MIN_RENAMED_DISTANCE):
+    """[(kernel, distance, instruction)] of MFMAs whose srcC overlaps the destination of an MFMA
+    fewer than ``window`` instructions earlier while their own destination differs."""
+    out, kernel, hist, idx = [], None, [], 0
+    for line in disasm.splitlines():
+        mk = _KERNEL.match(line)
+        if mk:
+            kernel, hist, idx = mk.group(1), [], 0
+            continue
+        if not line.startswith("\t") or not line.strip():
+            continue
+        idx += 1
+        m = _MFMA.match(line)
+        if not m:
+            continue
+        dst, src_c = m.group(2), m.group(5).strip()
+        for pidx, pdst in hist:
+            if idx - pidx < window and _overlap(_range(src_c), pdst) and dst != src_c:
+                out.append((kernel, idx - pidx, line.strip().split("//")[0].strip()))
+        hist = [h for h in hist if idx - h[0] < window] + [(idx, _range(dst))]
+    return out
+
+
+def _disassemble(so_path):
+    fat = subprocess.run(["objcopy", "--dump-section", ".hip_fatbin=/dev/stdout", so_path],
+                         capture_output=True, check=True).stdout
+    starts = [m.start() for m in re.finditer(re.escape(MAGIC), fat)] + [len(fat)]
+    text = []
+    with tempfile.TemporaryDirectory() as d:
+        for i in range(len(starts) - 1):
+            b = os.path.join(d, f"b{i}.bin")
+            co = os.path.join(d, f"b{i}.o")
+            with open(b, "wb") as f:
+                f.write(fat[starts[i]:starts[i + 1]])
+            subprocess.run([f"{LLVM}/clang-offload-bundler", "--type=o", f"--targets={TARGET}",
+                            f"--input={b}", f"--output={co}", "--unbundle"], check=True,
+                           capture_output=True)
+            text.append(subprocess.run([f"{LLVM}/llvm-objdump", "-d", "--mcpu=gfx950", co],
+                                       capture_output=True, text=True, check=True).stdout)
+    return "\n".join(text)
+
+
+def test_the_detector_flags_a_renamed_back_to_back_chain():
+    """The pattern the kernels must not contain, and two that are fine."""
+    bad = ("0000000000001000 <_ZN4zjai1kE>:\n"
+           "\tv_mfma_f32_16x16x4_f32 a[12:15], v12, v16, a[12:15]\n"
+           "\tv_mfma_f32_16x16x4_f32 a[24:27], v13, v17, a[12:15]\n")
+    inplace = bad.replace("a[24:27], v13", "a[12:15], v13")
+    far = ("0000000000001000 <_ZN4zjai1kE>:\n"
+           "\tv_mfma_f32_16x16x4_f32 a[12:15], v12, v16, a[12:15]\n" + "\ts_nop 0\n" * 6 +
+           "\tv_mfma_f32_16x16x4_f32 a[24:27], v13, v17, a[12:15]\n")
+    assert [(k, d) for k, d, _ in renamed_chains(bad)] == [("_ZN4zjai1kE", 1)]
+    assert renamed_chains(inplace) == []
+    assert renamed_chains(far) == []
+
+
+@pytest.mark.skipif(not (shutil.which("objcopy") and os.path.exists(f"{LLVM}/llvm-objdump")),
+                    reason="ROCm LLVM tools not installed")
+def test_no_kernel_renames_an_mfma_accumulator_back_to_back():
+    text = _disassemble(_lib.LIB_PATH)
+    n_mfma = len(re.findall(r"\bv_mfma_", text))
+    assert n_mfma > 500, n_mfma  # every conv / fused-block kernel was disassembled
+    bad = renamed_chains(text)
+    assert not bad, bad[:5]
