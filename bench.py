@@ -39,6 +39,7 @@ sys.path.insert(0, ROOT)
 METRIC = "synthesis decode Mpixel/s at 1MP & 4MP; conv TFLOP/s + % MFMA peak (1 GPU)"
 PEAK_TFLOPS = {"f32": 157.3, "f16": 2500.0, "bf16": 2500.0}
 PEAK_HBM_GBS = 8000.0
+CONV_KERNELS = ("conv_igemm", "conv_dma_f32")  # the MFMA convolution kernels (conv.hip)
 
 
 def log(msg):
@@ -325,7 +326,7 @@ def main():
     log(f"[bench] {ms:.2f} ms/step -> {value:.2f} Mpixel/s")
     prof = profile_step(eng, pic)
     total_ms = sum(d["ms"] for d in prof.values())
-    conv = {k: d for k, d in prof.items() if k.startswith("conv_igemm")}
+    conv = {k: d for k, d in prof.items() if k.startswith(CONV_KERNELS)}
     conv_flops = sum(d["flops"] for d in conv.values())
     conv_ms = sum(d["ms"] for d in conv.values())
     dom_name, dom = max(prof.items(), key=lambda kv: kv[1]["ms"])
@@ -368,7 +369,7 @@ def main():
             p2, _ = make_workload(args.workload, e2, args.lanes)
             ms2 = time_steps(e2, p2, args.steps, args.warmup)
             pr2 = profile_step(e2, p2)
-            cv = {k: d for k, d in pr2.items() if k.startswith("conv_igemm")}
+            cv = {k: d for k, d in pr2.items() if k.startswith(CONV_KERNELS)}
             cf, cm = sum(d["flops"] for d in cv.values()), sum(d["ms"] for d in cv.values())
             extra[f"{args.workload}_{prec}_mpix_s"] = round(pixels / (ms2 / 1e3) / 1e6, 3)
             extra[f"{args.workload}_{prec}_conv_tflops"] = round(cf / (cm / 1e3) / 1e12, 3)

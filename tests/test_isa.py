@@ -62,11 +62,18 @@ def renamed_chains(disasm: str, window: int = MIN_RENAMED_DISTANCE):
 
 
 def _disassemble(so_path):
-    fat = subprocess.run(["objcopy", "--dump-section", ".hip_fatbin=/dev/stdout", so_path],
-                         capture_output=True, check=True).stdout
-    starts = [m.start() for m in re.finditer(re.escape(MAGIC), fat)] + [len(fat)]
     text = []
     with tempfile.TemporaryDirectory() as d:
+        # objcopy rewrites its input when no output file is named: work on a copy and send the
+        # copied object to /dev/null.
+        lib = os.path.join(d, "lib.so")
+        shutil.copyfile(so_path, lib)
+        fatbin = os.path.join(d, "fatbin")
+        subprocess.run(["objcopy", "--dump-section", f".hip_fatbin={fatbin}", lib, "/dev/null"],
+                       capture_output=True, check=True)
+        with open(fatbin, "rb") as f:
+            fat = f.read()
+        starts = [m.start() for m in re.finditer(re.escape(MAGIC), fat)] + [len(fat)]
         for i in range(len(starts) - 1):
             b = os.path.join(d, f"b{i}.bin")
             co = os.path.join(d, f"b{i}.o")

@@ -19,6 +19,8 @@
 
 #include "conv.h"
 
+#include <type_traits>
+
 namespace zjai {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -413,6 +415,222 @@ conv_igemm(const ConvParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// fp32 pipelined variant of conv_igemm (dense tile shapes): the input halo and the weight blocks
+// of a K stage go global -> LDS with gfx950's direct LDS loads (global_load_lds_dwordx4: lane
+// i's 16 bytes land at the wave's LDS base + 16 i, no VGPR staging), double-buffered, so one
+// barrier per stage separates the loads of stage k + 1 from the MFMAs of stage k. Padding units
+// load from a zeroed device buffer. Numerics are conv_igemm's: bias first, then per K chunk and
+// tap the four k = 0..3 MFMAs of each accumulator in order -- issued k-outermost over the
+// CF x PF accumulators, so that dependent MFMAs are CF x PF instructions apart.
+// ---------------------------------------------------------------------------------------------
+__device__ u32x4 g_zero_units[4];
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF, int SG>
+__global__ void __launch_bounds__(WC * WP * 64)
+conv_dma_f32(const ConvParams p) {
+    using T = float;
+    constexpr int NT = WC * WP * 64;
+    constexpr int TY = WP * PF;
+    constexpr int HY = (TY - 1) * S + KH;
+    constexpr int HX = 15 * S + KW;
+    constexpr int NTAP = TR ? 4 : KH * KW;
+    constexpr int NB = WC * CF;
+    constexpr int VEC = 4;
+    constexpr int CK = 16;
+    constexpr int HALO_U = HY * HX * 4;
+    constexpr int W_U = NB * NTAP * 64;
+    constexpr int CH_U = HALO_U + W_U;  // one K chunk: halo units, then weight units
+    constexpr int STG_U = SG * CH_U;
+    constexpr int OUT_LD = NB * 16 + 4;
+    constexpr int OUT_U = (TY * 16 * OUT_LD + 3) / 4;
+    constexpr int LDS_U = (2 * STG_U) > OUT_U ? (2 * STG_U) : OUT_U;
+    constexpr int HN = (HALO_U + NT - 1) / NT, WN = (W_U + NT - 1) / NT;
+    __shared__ u32x4 s_lds[LDS_U];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wc = wave % WC, wp = wave / WC;
+    const int col = lane & 15, grp = lane >> 4;
+
+    // Workgroup -> tile: the XCD-aware order of conv_igemm.
+    const int nz = p.ntiles * (TR ? 4 : 1);
+    const int total = p.gx * p.gy * p.N * nz;
+    const int bid = (int)blockIdx.x, xj = bid & 7, xk = bid >> 3;
+    const int q8 = total >> 3, r8 = total & 7;
+    const int lid = xj < r8 ? xj * (q8 + 1) + xk : r8 * (q8 + 1) + (xj - r8) * q8 + xk;
+    int rest = lid / nz;
+    const int zl = lid - rest * nz;
+    const int tx = rest % p.gx;
+    rest /= p.gx;
+    const int ty = rest % p.gy, bi = rest / p.gy;
+    const int phase = TR ? (zl & 3) : 0;
+    const int nt = TR ? (zl >> 2) : zl;
+    const int gb = nt * NB;
+    const int g = gb / p.nblk_g, nb0 = gb - g * p.nblk_g;
+    const int ox0 = tx * 16, oy0 = ty * TY;
+
+    int ntap = NTAP;
+    int tdy[NTAP], tdx[NTAP];
+#pragma unroll
+    for (int t = 0; t < NTAP; ++t) {
+        if (TR) {
+            tdy[t] = p.tap_dy[phase][t];
+            tdx[t] = p.tap_dx[phase][t];
+        } else {
+            tdy[t] = t / KW;
+            tdx[t] = t % KW;
+        }
+    }
+    if (TR) ntap = p.ntaps[phase];
+
+    f32x4 acc[CF][PF];
+#pragma unroll
+    for (int cf = 0; cf < CF; ++cf) {
+        const int ocl = (nb0 + wc * CF + cf) * 16 + grp * 4;
+        f32x4 b;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            b[i] = (p.bias && ocl + i < p.cout_g) ? p.bias[g * p.cout_g + ocl + i] : 0.0f;
+#pragma unroll
+        for (int pf = 0; pf < PF; ++pf) acc[cf][pf] = b;
+    }
+
+    const int iy0 = TR ? oy0 - 1 : oy0 * S - p.pad_t;
+    const int ix0 = TR ? ox0 - 1 : ox0 * S - p.pad_l;
+    const T* xg = (const T*)p.x.p + (long long)bi * p.x.bstride;
+    const T* wg = (const T*)p.w + phase * p.phase_stride + (long long)bi * p.w_bstride;
+    const long long xbase = (long long)p.x.c_off + (long long)g * p.cin_g;
+
+    // Halo element offset of each of this thread's units (u = tid + i * NT), -1 in the padding.
+    // NT is a multiple of 4, so every unit of a thread holds the same channel quad.
+    long long hoff[HN];
+#pragma unroll
+    for (int i = 0; i < HN; ++i) {
+        const int u = tid + i * NT, pix = u >> 2, q = u & 3;
+        const int hy = pix / HX, hx = pix - hy * HX;
+        const int iy = iy0 + hy, ix = ix0 + hx;
+        hoff[i] = (u < HALO_U && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W)
+                      ? (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + q * VEC
+                      : -1;
+    }
+    const int qv = (tid & 3) * VEC;
+
+    // Direct LDS loads of stage st into buffer buf. Each wave covers whole 64-unit rows of the
+    // chunk's layout; its M0 base is the row start, lanes past the end are masked off.
+    auto issue = [&](int st, int buf) {
+#pragma unroll
+        for (int s = 0; s < SG; ++s) {
+            const int chunk = st * SG + s;
+            if (chunk >= p.nchunks) break;
+            const int cl0 = chunk * CK;
+            u32x4* dst = s_lds + buf * STG_U + s * CH_U;
+#pragma unroll
+            for (int i = 0; i < HN; ++i) {
+                const int ub = wave * 64 + i * NT;
+                if (ub >= HALO_U) break;
+                if (ub + lane < HALO_U) {
+                    const void* src = (hoff[i] >= 0 && cl0 + qv < p.cin_g) ? (const void*)(xg + hoff[i] + cl0)
+                                                                          : (const void*)g_zero_units;
+                    __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)(dst + ub), 16, 0, 0);
+                }
+            }
+            const u32x4* wsrc = (const u32x4*)(wg + ((long long)(g * p.nchunks + chunk) * p.nblk_g + nb0) *
+                                                        (long long)(NTAP * 16 * CK));
+#pragma unroll
+            for (int i = 0; i < WN; ++i) {
+                const int ub = wave * 64 + i * NT;
+                if (ub >= W_U) break;
+                if (ub + lane < W_U)
+                    __builtin_amdgcn_global_load_lds((const void*)(wsrc + ub + lane), (lds_ptr_t)(dst + HALO_U + ub),
+                                                     16, 0, 0);
+            }
+        }
+    };
+
+    const int nst = (p.nchunks + SG - 1) / SG;
+    issue(0, 0);
+    for (int st = 0; st < nst; ++st) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of stage st are in LDS
+        __syncthreads();                     // ... and every other wave's
+        if (st + 1 < nst) issue(st + 1, (st + 1) & 1);
+        const u32x4* sb = s_lds + (st & 1) * STG_U;
+        auto stage = [&](auto relu6) {
+#pragma unroll
+            for (int s = 0; s < SG; ++s) {
+                if (st * SG + s >= p.nchunks) break;
+                const u32x4* s_halo = sb + s * CH_U;
+                const u32x4* s_w = s_halo + HALO_U;
+                for (int t = 0; t < ntap; ++t) {
+                    const int ky = tdy[t], kx = tdx[t];
+                    u32x4 a[CF], b[PF];
+#pragma unroll
+                    for (int cf = 0; cf < CF; ++cf) a[cf] = s_w[((wc * CF + cf) * NTAP + t) * 64 + col * 4 + grp];
+#pragma unroll
+                    for (int pf = 0; pf < PF; ++pf) {
+                        const int hy = (wp * PF + pf) * S + ky, hx = col * S + kx;
+                        b[pf] = s_halo[(hy * HX + hx) * 4 + grp];
+                        if constexpr (decltype(relu6)::value) b[pf] = relu6_vec<T>(b[pf]);
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+#pragma unroll
+                        for (int cf = 0; cf < CF; ++cf)
+#pragma unroll
+                            for (int pf = 0; pf < PF; ++pf)
+                                acc[cf][pf] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                                    __builtin_bit_cast(f32x4, a[cf])[k], __builtin_bit_cast(f32x4, b[pf])[k],
+                                    acc[cf][pf], 0, 0, 0);
+                }
+            }
+        };
+        if (p.relu6_in) stage(std::true_type{});
+        else stage(std::false_type{});
+    }
+
+    if (p.out_mode == OUT_NHWC && p.ps == 1) {
+        __syncthreads();
+        float* so = reinterpret_cast<float*>(s_lds);
+#pragma unroll
+        for (int cf = 0; cf < CF; ++cf)
+#pragma unroll
+            for (int pf = 0; pf < PF; ++pf) {
+                float* d = so + ((wp * PF + pf) * 16 + col) * OUT_LD + (wc * CF + cf) * 16 + grp * 4;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) d[i] = acc[cf][pf][i];
+            }
+        __syncthreads();
+        constexpr int QP = NB * 4;
+        for (int u = tid; u < TY * 16 * QP; u += NT) {
+            const int pos = u / QP, cq = u - pos * QP;
+            const int r = pos >> 4, cx = pos & 15;
+            const int oy = TR ? 2 * (oy0 + r) + (phase >> 1) : oy0 + r;
+            const int ox = TR ? 2 * (ox0 + cx) + (phase & 1) : ox0 + cx;
+            const int ocl = nb0 * 16 + cq * 4;
+            if (oy >= p.OH || ox >= p.OW || ocl >= p.cout_g) continue;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + cq * 4);
+            epilogue_store<T>(p, bi, oy, ox, g * p.cout_g + ocl, min(4, p.cout_g - ocl), v);
+        }
+        return;
+    }
+
+#pragma unroll
+    for (int cf = 0; cf < CF; ++cf) {
+        const int ocl = (nb0 + wc * CF + cf) * 16 + grp * 4;
+        if (ocl >= p.cout_g) continue;
+        const int nvalid = min(4, p.cout_g - ocl);
+#pragma unroll
+        for (int pf = 0; pf < PF; ++pf) {
+            const int r = wp * PF + pf;
+            const int oy = TR ? 2 * (oy0 + r) + (phase >> 1) : oy0 + r;
+            const int ox = TR ? 2 * (ox0 + col) + (phase & 1) : ox0 + col;
+            if (oy >= p.OH || ox >= p.OW) continue;
+            epilogue_store<T>(p, bi, oy, ox, g * p.cout_g + ocl, nvalid, acc[cf][pf]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Narrow transposed convolution (stride 2, at most 8 output channels): the last synthesis layers
 // (HOP luma 128 -> 1, chroma 64 -> 8). An MFMA tile would leave at least half of its 16 or 32
 // output rows idle, so these run on the vector ALUs: one thread per phase-grid position (y', x')
@@ -542,6 +760,13 @@ hipError_t launch_convT_narrow(int dtype, int coutp, const ConvParams& p, const 
 // ---------------------------------------------------------------------------------------------
 // Launch dispatch.
 // ---------------------------------------------------------------------------------------------
+// The fp32 dense tile shapes run the direct-LDS-load kernel (1x1 layers stage two K chunks per
+// barrier); the 16-bit ones and the narrow shapes run conv_igemm.
+template <int WC, int WP, int CF, int PF>
+constexpr bool use_dma_f32() {
+    return (WC == 2 && WP == 2 && CF == 2 && PF == 4) || (WC == 2 && WP == 4 && CF == 2 && PF == 4);
+}
+
 template <typename T, int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF>
 static hipError_t go(const ConvParams& p0, hipStream_t s) {
     constexpr int SG = (KH * KW == 1 && !TR) ? 4 : 1;
@@ -554,8 +779,14 @@ static hipError_t go(const ConvParams& p0, hipStream_t s) {
     p.gy = (gh + TY - 1) / TY;
     const long long total = (long long)p.gx * p.gy * p.N * p.ntiles * (TR ? 4 : 1);
     if (total <= 0 || total > (1ll << 30)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((conv_igemm<T, KH, KW, S, TR, WC, WP, CF, PF, SG>), dim3((unsigned)total),
-                       dim3(WC * WP * 64), 0, s, p);
+    if constexpr (sizeof(T) == 4 && use_dma_f32<WC, WP, CF, PF>()) {
+        constexpr int SGD = (KH * KW == 1 && !TR) ? 2 : 1;
+        hipLaunchKernelGGL((conv_dma_f32<KH, KW, S, TR, WC, WP, CF, PF, SGD>), dim3((unsigned)total),
+                           dim3(WC * WP * 64), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((conv_igemm<T, KH, KW, S, TR, WC, WP, CF, PF, SG>), dim3((unsigned)total),
+                           dim3(WC * WP * 64), 0, s, p);
+    }
     return hipGetLastError();
 }
 
@@ -572,14 +803,15 @@ static hipError_t go_kind(int kind, const ConvParams& p, hipStream_t s) {
 }
 
 // Instantiated tile shapes: (wc, wp, cf, pf).
-//   {2,2,2,4}: 64 channels x 8 rows  (dense layers)
+//   {2,2,2,4}: 64 channels x 8 rows, 4 waves  (dense layers)
+//   {2,4,2,4}: 64 channels x 16 rows, 8 waves (dense stride-1 3x3 layers only)
 //   {1,4,2,2}: 32 channels x 8 rows  (32-channel groups / outputs)
 //   {1,4,1,2}: 16 channels x 8 rows  (16-channel groups / narrow outputs)
 #define ZJAI_CFGS(X) X(2, 2, 2, 4) X(1, 4, 2, 2) X(1, 4, 1, 2)
 
 bool conv_cfg_supported(int kind, int dtype, TileCfg c) {
-    (void)kind;
     (void)dtype;
+    if (c.wc == 2 && c.wp == 4 && c.cf == 2 && c.pf == 4) return kind == CK_3x3;
 #define ZJAI_CHECK(a, b, cc, d) if (c.wc == a && c.wp == b && c.cf == cc && c.pf == d) return true;
     ZJAI_CFGS(ZJAI_CHECK)
 #undef ZJAI_CHECK
@@ -588,6 +820,8 @@ bool conv_cfg_supported(int kind, int dtype, TileCfg c) {
 
 template <typename T>
 static hipError_t go_cfg(int kind, TileCfg c, const ConvParams& p, hipStream_t s) {
+    if (c.wc == 2 && c.wp == 4 && c.cf == 2 && c.pf == 4)
+        return kind == CK_3x3 ? go<T, 3, 3, 1, false, 2, 4, 2, 4>(p, s) : hipErrorInvalidValue;
 #define ZJAI_GO(a, b, cc, d) \
     if (c.wc == a && c.wp == b && c.cf == cc && c.pf == d) return go_kind<T, a, b, cc, d>(kind, p, s);
     ZJAI_CFGS(ZJAI_GO)
