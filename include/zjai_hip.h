@@ -74,12 +74,17 @@ typedef struct zjai_picture zjai_picture;
 /* ------------------------------------------------------------------ context / diagnostics */
 
 /* Replaces `Engine` construction (src/nn/fast/mod.rs:128-172) for the HIP backend: binds a
- * device and creates its stream. flags: 0 or ZJAI_CTX_UNFUSED_BLOCKS (other bits are rejected). */
+ * device and creates its stream. flags: 0 or an OR of ZJAI_CTX_UNFUSED_BLOCKS and
+ * ZJAI_CTX_PHASE_SPLIT_CONVT (other bits are rejected). */
 /* Run the transformer blocks (src/model/attention.rs:328-372) as the reference's separate ops --
  * layer norm, 1x1, depthwise (+ ELU gate), 1x1 -- instead of the fused kernels the 16-bit
  * precisions use by default for `prep_data` (LN + 1x1 + depthwise) and for the feed-forward half
  * (the two give bit-identical results). */
 #define ZJAI_CTX_UNFUSED_BLOCKS 0x1u
+/* Run every 3x3 stride-2 transposed convolution (`conv3x3_t`, src/model/attention.rs:78-91) one
+ * output phase per workgroup instead of all four phases per workgroup (same results bit for bit;
+ * for A/B runs and the parity test that proves it). */
+#define ZJAI_CTX_PHASE_SPLIT_CONVT 0x2u
 ZJAI_API int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out);
 ZJAI_API int32_t zjai_ctx_destroy(zjai_ctx* ctx);
 /* Copies the last failure message (NUL-terminated, truncated to len). Works with ctx == NULL

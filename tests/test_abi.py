@@ -68,6 +68,8 @@ def test_context_flags_match_the_header_and_unknown_flags_are_rejected():
     text = open(HEADER).read()
     m = re.search(r"#define\s+ZJAI_CTX_UNFUSED_BLOCKS\s+(0x[0-9a-fA-F]+)u", text)
     assert m and int(m.group(1), 16) == _lib.CTX_UNFUSED_BLOCKS
+    m = re.search(r"#define\s+ZJAI_CTX_PHASE_SPLIT_CONVT\s+(0x[0-9a-fA-F]+)u", text)
+    assert m and int(m.group(1), 16) == _lib.CTX_PHASE_SPLIT_CONVT
     L = _lib.lib()
     h = ctypes.c_void_p()
     assert L.zjai_ctx_create(0, 0x80, ctypes.byref(h)) == _lib.E_INVALID_ARGUMENT

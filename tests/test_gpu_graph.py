@@ -131,6 +131,40 @@ def test_fused_transformer_blocks_are_bit_identical_to_unfused(prec, comp):
     plain.close()
 
 
+@pytest.mark.parametrize("prec", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("comp", ["y", "uv"])
+def test_merged_phase_transposed_convs_are_bit_identical_to_phase_split(prec, comp):
+    """The 3x3 stride-2 transposed convs with all four output phases per workgroup against the
+    same net run one phase per workgroup (ZJAI_CTX_PHASE_SPLIT_CONVT). HOP luma has four such
+    layers (160 -> 128, 128 -> 128, the CAB upscale with its sigmoid epilogue, the TAM us_conv),
+    chroma two; the maps (up to 128 x 192 and 64 x 48) span several 32 x 32 output tiles with
+    partial ones, and the last layers (<= 8 outputs) stay on the narrow kernel in both runs."""
+    merged = nn.Engine(0, prec)
+    split = nn.Engine(0, prec, flags=_lib.CTX_PHASE_SPLIT_CONVT)
+    p = synth.random_params("hop", comp, seed=26, gain=0.5)
+    outs, names = [], []
+    for eng in (merged, split):
+        eng.profile_begin()
+        if comp == "y":
+            y = synth.latent(26, "trm/y", 160, 14, 23)
+            net = model.SynthesisPrimary.load(p, "hop", eng)
+            out = net.forward(eng, nn.BTensor.from_planar(eng, y), 224, 368)
+        else:
+            y = synth.latent(26, "trm/y", 160, 16, 12)
+            uv = synth.latent(26, "trm/uv", 96, 16, 12)
+            net = model.SynthesisSecondary.load(p, "hop", eng)
+            out = net.forward(eng, nn.BTensor.from_planar(eng, y), nn.BTensor.from_planar(eng, uv), 256, 192)
+        names.append([r[0] for r in eng.profile_end()])
+        outs.append(out)
+    n_tr = 4 if comp == "y" else 2
+    assert sum(n.startswith("conv_tr_merged<") for n in names[0]) == n_tr
+    assert not any(n.startswith("conv_tr_merged<") for n in names[1])
+    assert np.isfinite(outs[0]).all()
+    np.testing.assert_array_equal(outs[0], outs[1])
+    merged.close()
+    split.close()
+
+
 def _picture(eng, op, h, w, tiling, regions, sv, sh, bits, seed, gain=0.5):
     lh, lw = -(-h // 16), -(-w // 16)
     py = synth.random_params(op, "y", seed=seed, gain=gain)

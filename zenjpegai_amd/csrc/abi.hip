@@ -76,7 +76,7 @@ TensorP planar_upload(Context& c, const float* data, int ch, int h, int w, int d
 extern "C" int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out) {
     if (!out) return ZJAI_E_INVALID_ARGUMENT;
     *out = nullptr;
-    if (flags & ~ZJAI_CTX_UNFUSED_BLOCKS)
+    if (flags & ~(ZJAI_CTX_UNFUSED_BLOCKS | ZJAI_CTX_PHASE_SPLIT_CONVT))
         return guard(nullptr, [] { throw Error(ZJAI_E_INVALID_ARGUMENT, "zjai_ctx_create: unknown flags"); });
     zjai_ctx* ctx = new (std::nothrow) zjai_ctx();
     if (!ctx) return ZJAI_E_LIMIT;

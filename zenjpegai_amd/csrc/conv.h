@@ -69,6 +69,14 @@ enum ConvKind : int { CK_1x1 = 0, CK_2x2 = 1, CK_3x3 = 2, CK_3x3_S2 = 3, CK_T3 =
 hipError_t launch_conv(int kind, int dtype, TileCfg cfg, const ConvParams& p, hipStream_t s);
 bool conv_cfg_supported(int kind, int dtype, TileCfg cfg);
 
+// Stride-2 transposed conv with 3x3 kernels (9 taps over the four output phases), all four
+// phases of a tile in one workgroup: p.w is the phase-merged packing [chunk][nblk][9][16][CK]
+// (taps phase by phase, each phase's taps in its table order), p.ntiles = nblk_g / 4; NHWC
+// output without pixel shuffle, no relu6 on load.
+hipError_t launch_conv_tr_merged(int dtype, const ConvParams& p, hipStream_t s);
+constexpr int TR_MERGED_TAPS = 9;
+constexpr int TR_MERGED_NB = 4;
+
 // Stride-2 transposed conv with cout <= 8 on the vector ALUs (coutp = cout rounded up to 1, 2, 4
 // or 8); wn is [phase][tap][cin][coutp] f32. Uses p's input view, output geometry, tap tables,
 // bias and epilogue fields.

@@ -631,6 +631,227 @@ conv_dma_f32(const ConvParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Stride-2 transposed conv (3x3 kernel) with the four output phases of a tile in one
+// workgroup. The phase-per-workgroup form stages a halo and a weight block per K chunk for
+// 1, 2, 2 or 4 taps; here the 9 taps of all phases share one staged halo and one 9-tap weight
+// block, so a K chunk carries as much matrix work as a 3x3 conv. Each wave accumulates its
+// CF x PF tile for all four phases (acc[4][CF][PF]); the stage pipeline is conv_dma_f32's
+// (direct global -> LDS loads, double-buffered, one barrier per stage), for every storage type.
+// Per output the products are summed exactly as in the phase-per-workgroup kernel: bias, then
+// per K chunk the phase's taps in table order, k ascending within a tap.
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(512)
+conv_tr_merged(const ConvParams p) {
+    constexpr int WC = 2, WP = 4, CF = 2, PF = 4;
+    constexpr int NT = WC * WP * 64;
+    constexpr int TY = WP * PF;
+    constexpr int HY = TY + 2, HX = 18;
+    constexpr int NTALL = TR_MERGED_TAPS;
+    constexpr int NB = WC * CF;
+    static_assert(NB == TR_MERGED_NB, "packing block count");
+    constexpr int VEC = 16 / (int)sizeof(T);
+    constexpr int CK = 4 * VEC;
+    constexpr int HALO_U = HY * HX * 4;
+    constexpr int W_U = NB * NTALL * 64;
+    constexpr int CH_U = HALO_U + W_U;
+    constexpr int OUT_LD = NB * 16 + 4;
+    constexpr int OUT_U = (TY * 16 * OUT_LD + 3) / 4;
+    constexpr int LDS_U = (2 * CH_U) > OUT_U ? (2 * CH_U) : OUT_U;
+    constexpr int HN = (HALO_U + NT - 1) / NT, WN = (W_U + NT - 1) / NT;
+    __shared__ u32x4 s_lds[LDS_U];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wc = wave % WC, wp = wave / WC;
+    const int col = lane & 15, grp = lane >> 4;
+
+    const int nz = p.ntiles;
+    const int total = p.gx * p.gy * p.N * nz;
+    const int bid = (int)blockIdx.x, xj = bid & 7, xk = bid >> 3;
+    const int q8 = total >> 3, r8 = total & 7;
+    const int lid = xj < r8 ? xj * (q8 + 1) + xk : r8 * (q8 + 1) + (xj - r8) * q8 + xk;
+    int rest = lid / nz;
+    const int zl = lid - rest * nz;
+    const int tx = rest % p.gx;
+    rest /= p.gx;
+    const int ty = rest % p.gy, bi = rest / p.gy;
+    const int nb0 = zl * NB;
+    const int ox0 = tx * 16, oy0 = ty * TY;
+
+    f32x4 acc[4][CF][PF];
+#pragma unroll
+    for (int cf = 0; cf < CF; ++cf) {
+        const int ocl = (nb0 + wc * CF + cf) * 16 + grp * 4;
+        f32x4 b;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b[i] = (p.bias && ocl + i < p.cout_g) ? p.bias[ocl + i] : 0.0f;
+#pragma unroll
+        for (int ph = 0; ph < 4; ++ph)
+#pragma unroll
+            for (int pf = 0; pf < PF; ++pf) acc[ph][cf][pf] = b;
+    }
+
+    const int iy0 = oy0 - 1, ix0 = ox0 - 1;
+    const T* xg = (const T*)p.x.p + (long long)bi * p.x.bstride + p.x.c_off;
+    const u32x4* wg = (const u32x4*)p.w + (long long)nb0 * (NTALL * 64);
+    const long long wchunk = (long long)p.nblk_g * (NTALL * 64);
+
+    long long hoff[HN];
+#pragma unroll
+    for (int i = 0; i < HN; ++i) {
+        const int u = tid + i * NT, pix = u >> 2, q = u & 3;
+        const int hy = pix / HX, hx = pix - hy * HX;
+        const int iy = iy0 + hy, ix = ix0 + hx;
+        hoff[i] = (u < HALO_U && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W)
+                      ? (long long)iy * p.x.row + (long long)ix * p.x.cs + q * VEC
+                      : -1;
+    }
+    const int qv = (tid & 3) * VEC;
+
+    // Tap tables in registers (compile-time indices below), so that the kernel argument block
+    // is never indexed at run time.
+    int ntp[4], base[4], tdy[4][4], tdx[4][4];
+    base[0] = 0;
+#pragma unroll
+    for (int ph = 0; ph < 4; ++ph) {
+        ntp[ph] = p.ntaps[ph];
+        if (ph < 3) base[ph + 1] = base[ph] + ntp[ph];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            tdy[ph][t] = p.tap_dy[ph][t];
+            tdx[ph][t] = p.tap_dx[ph][t];
+        }
+    }
+    const int nchunks = p.nchunks, cin_g = p.cin_g;
+
+    auto issue = [&](int chunk, int buf) __attribute__((always_inline)) {
+        const int cl0 = chunk * CK;
+        u32x4* dst = s_lds + buf * CH_U;
+#pragma unroll
+        for (int i = 0; i < HN; ++i) {
+            const int ub = wave * 64 + i * NT;
+            if (ub >= HALO_U) break;
+            if (ub + lane < HALO_U) {
+                const void* src = (hoff[i] >= 0 && cl0 + qv < cin_g) ? (const void*)(xg + hoff[i] + cl0)
+                                                                      : (const void*)g_zero_units;
+                __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)(dst + ub), 16, 0, 0);
+            }
+        }
+        const u32x4* wsrc = wg + chunk * wchunk;
+#pragma unroll
+        for (int i = 0; i < WN; ++i) {
+            const int ub = wave * 64 + i * NT;
+            if (ub >= W_U) break;
+            if (ub + lane < W_U)
+                __builtin_amdgcn_global_load_lds((const void*)(wsrc + ub + lane), (lds_ptr_t)(dst + HALO_U + ub), 16,
+                                                 0, 0);
+        }
+    };
+
+
+    issue(0, 0);
+    for (int c = 0; c < nchunks; ++c) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of chunk c are in LDS
+        __syncthreads();                     // ... and every other wave's
+        if (c + 1 < nchunks) issue(c + 1, (c + 1) & 1);
+        const u32x4* s_halo = s_lds + (c & 1) * CH_U;
+        const u32x4* s_w = s_halo + HALO_U;
+        auto phase_taps = [&](auto phc) __attribute__((always_inline)) {
+            constexpr int ph = decltype(phc)::value;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (t >= ntp[ph]) break;
+                const int e = base[ph] + t;
+                const int dy = tdy[ph][t], dx = tdx[ph][t];
+                u32x4 a[CF], b[PF];
+#pragma unroll
+                for (int cf = 0; cf < CF; ++cf) a[cf] = s_w[((wc * CF + cf) * NTALL + e) * 64 + col * 4 + grp];
+#pragma unroll
+                for (int pf = 0; pf < PF; ++pf) {
+                    b[pf] = s_halo[((wp * PF + pf + dy) * HX + col + dx) * 4 + grp];
+                }
+                if constexpr (sizeof(T) == 4) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+#pragma unroll
+                        for (int cf = 0; cf < CF; ++cf)
+#pragma unroll
+                            for (int pf = 0; pf < PF; ++pf)
+                                acc[ph][cf][pf] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                                    __builtin_bit_cast(f32x4, a[cf])[k], __builtin_bit_cast(f32x4, b[pf])[k],
+                                    acc[ph][cf][pf], 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int cf = 0; cf < CF; ++cf)
+#pragma unroll
+                        for (int pf = 0; pf < PF; ++pf) Mma<T>::run(acc[ph][cf][pf], a[cf], b[pf]);
+                }
+            }
+        };
+        phase_taps(std::integral_constant<int, 0>{});
+        phase_taps(std::integral_constant<int, 1>{});
+        phase_taps(std::integral_constant<int, 2>{});
+        phase_taps(std::integral_constant<int, 3>{});
+    }
+
+    // One phase at a time through the LDS transpose (NHWC output without pixel shuffle; the
+    // launcher sends every other epilogue to the phase-per-workgroup kernel).
+    float* so = reinterpret_cast<float*>(s_lds);
+    auto put = [&](const f32x4 (&a)[CF][PF]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int cf = 0; cf < CF; ++cf)
+#pragma unroll
+            for (int pf = 0; pf < PF; ++pf) {
+                float* d = so + ((wp * PF + pf) * 16 + col) * OUT_LD + (wc * CF + cf) * 16 + grp * 4;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) d[i] = a[cf][pf][i];
+            }
+    };
+    for (int ph = 0; ph < 4; ++ph) {
+        __syncthreads();
+        if (ph == 0) put(acc[0]);
+        else if (ph == 1) put(acc[1]);
+        else if (ph == 2) put(acc[2]);
+        else put(acc[3]);
+        __syncthreads();
+        const int py = ph >> 1, px = ph & 1;
+        constexpr int QP = NB * 4;
+        for (int u = tid; u < TY * 16 * QP; u += NT) {
+            const int pos = u / QP, cq = u - pos * QP;
+            const int r = pos >> 4, cx = pos & 15;
+            const int oy = 2 * (oy0 + r) + py, ox = 2 * (ox0 + cx) + px;
+            const int ocl = nb0 * 16 + cq * 4;
+            if (oy >= p.OH || ox >= p.OW || ocl >= p.cout_g) continue;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + cq * 4);
+            epilogue_store<T>(p, bi, oy, ox, ocl, min(4, p.cout_g - ocl), v);
+        }
+    }
+}
+
+hipError_t launch_conv_tr_merged(int dtype, const ConvParams& p0, hipStream_t s) {
+    ConvParams p = p0;
+    if (p.groups != 1 || p.ntiles * TR_MERGED_NB != p.nblk_g || p.N < 1 || p.N > MAXB || p.out_mode != OUT_NHWC ||
+        p.ps != 1 || p.relu6_in)
+        return hipErrorInvalidValue;
+    if (p.ntaps[0] + p.ntaps[1] + p.ntaps[2] + p.ntaps[3] != TR_MERGED_TAPS) return hipErrorInvalidValue;
+    for (int ph = 0; ph < 4; ++ph)
+        for (int t = 0; t < p.ntaps[ph]; ++t)
+            if (p.tap_dy[ph][t] < 0 || p.tap_dy[ph][t] > 2 || p.tap_dx[ph][t] < 0 || p.tap_dx[ph][t] > 2)
+                return hipErrorInvalidValue;
+    p.gx = ((p.OW + 1) / 2 + 15) / 16;
+    p.gy = ((p.OH + 1) / 2 + 15) / 16;
+    const long long total = (long long)p.gx * p.gy * p.N * p.ntiles;
+    if (total <= 0 || total > (1ll << 30)) return hipErrorInvalidValue;
+    switch (dtype) {
+        case DT_F32: hipLaunchKernelGGL(conv_tr_merged<float>, dim3((unsigned)total), dim3(512), 0, s, p); break;
+        case DT_F16: hipLaunchKernelGGL(conv_tr_merged<_Float16>, dim3((unsigned)total), dim3(512), 0, s, p); break;
+        case DT_BF16: hipLaunchKernelGGL(conv_tr_merged<__bf16>, dim3((unsigned)total), dim3(512), 0, s, p); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
 // Narrow transposed convolution (stride 2, at most 8 output channels): the last synthesis layers
 // (HOP luma 128 -> 1, chroma 64 -> 8). An MFMA tile would leave at least half of its 16 or 32
 // output rows idle, so these run on the vector ALUs: one thread per phase-grid position (y', x')

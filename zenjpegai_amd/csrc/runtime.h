@@ -148,6 +148,8 @@ struct Layer {
     float* dw_w = nullptr;     // depthwise [9][C]
     float* w_f32 = nullptr;    // f32 [cout][cin] copy (1x1 only, for attention folding)
     float* wn = nullptr;       // narrow transposed conv: [phase][tap][cin][coutp] f32
+    void* wpk_m = nullptr;     // 3x3 transposed conv, all phases per workgroup: [chunk][nblk][9][16][CK]
+    size_t wpk_m_bytes = 0;
     int coutp = 0;             // cout rounded up to 1, 2, 4 or 8 (narrow transposed conv)
     size_t wpk_bytes = 0;
     ~Layer();

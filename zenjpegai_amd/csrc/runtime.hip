@@ -262,6 +262,7 @@ Layer::~Layer() {
     if (dw_w) (void)hipFree(dw_w);
     if (w_f32) (void)hipFree(w_f32);
     if (wn) (void)hipFree(wn);
+    if (wpk_m) (void)hipFree(wpk_m);
 }
 
 void Layer::out_size(int h, int w, int* oh, int* ow) const {
@@ -406,6 +407,24 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
     }
     L->wpk = upload_as(ctx, pk, dtype, &L->wpk_bytes);
     if (bias) L->bias = upload_f32(bias, cout);
+    if (k == 3 && cout > 8 && L->ntaps[0] + L->ntaps[1] + L->ntaps[2] + L->ntaps[3] == TR_MERGED_TAPS &&
+        L->nblk_g % TR_MERGED_NB == 0) {
+        // All four phases per workgroup (launch_conv_tr_merged): the nine taps side by side per
+        // K chunk and block, phase by phase, each phase's taps in its table order.
+        std::vector<float> pm((size_t)L->nchunks * L->nblk_g * TR_MERGED_TAPS * 16 * CK, 0.0f);
+        for (int ch = 0; ch < L->nchunks; ++ch)
+            for (int nb = 0; nb < L->nblk_g; ++nb) {
+                int e = 0;
+                for (int ph = 0; ph < 4; ++ph)
+                    for (int t = 0; t < L->ntaps[ph]; ++t, ++e) {
+                        const float* src = pk.data() + (size_t)ph * L->phase_stride +
+                                           (((size_t)ch * L->nblk_g + nb) * 4 + t) * 16 * CK;
+                        float* dst = pm.data() + (((size_t)ch * L->nblk_g + nb) * TR_MERGED_TAPS + e) * 16 * CK;
+                        std::copy(src, src + 16 * CK, dst);
+                    }
+            }
+        L->wpk_m = upload_as(ctx, pm, dtype, &L->wpk_m_bytes);
+    }
     if (cout <= 8) {
         // Narrow layers run on the vector ALUs (launch_convT_narrow) from an f32 copy of the
         // storage-rounded weights, [phase][tap][cin][coutp].
@@ -556,6 +575,16 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
         snprintf(name, sizeof name, "k_convT_narrow<%s, %d>", ty[L.dtype], L.coutp);
         LaunchScope sc(ctx, name, 2.0 * macs, bytes);
         ZJAI_HIP(launch_convT_narrow(L.dtype, L.coutp, p, L.wn, L.cin, ctx.stream));
+        return y;
+    }
+    if (L.wpk_m && !e.w_batch && !plane && ps == 1 && !e.relu6_in &&
+        !(ctx.top().flags & ZJAI_CTX_PHASE_SPLIT_CONVT)) {
+        static const char* ty[] = {"float", "_Float16", "__bf16"};
+        p.w = L.wpk_m;
+        p.ntiles = L.nblk_g / TR_MERGED_NB;
+        LaunchScope sc(ctx, std::string("conv_tr_merged<") + ty[L.dtype] + ">", 2.0 * macs,
+                       bytes - (double)L.wpk_bytes + (double)L.wpk_m_bytes);
+        ZJAI_HIP(launch_conv_tr_merged(L.dtype, p, ctx.stream));
         return y;
     }
     LaunchScope sc(ctx, conv_kernel_name(L.kind, L.dtype, L.cfg), 2.0 * macs, bytes);
