@@ -985,7 +985,8 @@ hipError_t launch_convT_narrow(int dtype, int coutp, const ConvParams& p, const 
 // barrier); the 16-bit ones and the narrow shapes run conv_igemm.
 template <int WC, int WP, int CF, int PF>
 constexpr bool use_dma_f32() {
-    return (WC == 2 && WP == 2 && CF == 2 && PF == 4) || (WC == 2 && WP == 4 && CF == 2 && PF == 4);
+    return (WC == 2 && WP == 2 && CF == 2 && PF == 4) || (WC == 2 && WP == 4 && CF == 2 && PF == 4) ||
+           (WC == 4 && WP == 2 && CF == 2 && PF == 4);
 }
 
 template <typename T, int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF>
@@ -1026,13 +1027,14 @@ static hipError_t go_kind(int kind, const ConvParams& p, hipStream_t s) {
 // Instantiated tile shapes: (wc, wp, cf, pf).
 //   {2,2,2,4}: 64 channels x 8 rows, 4 waves  (dense layers)
 //   {2,4,2,4}: 64 channels x 16 rows, 8 waves (dense stride-1 3x3 layers only)
+//   {4,2,2,4}: 128 channels x 8 rows, 8 waves (fp32 1x1 layers with >= 256 outputs only)
 //   {1,4,2,2}: 32 channels x 8 rows  (32-channel groups / outputs)
 //   {1,4,1,2}: 16 channels x 8 rows  (16-channel groups / narrow outputs)
 #define ZJAI_CFGS(X) X(2, 2, 2, 4) X(1, 4, 2, 2) X(1, 4, 1, 2)
 
 bool conv_cfg_supported(int kind, int dtype, TileCfg c) {
-    (void)dtype;
     if (c.wc == 2 && c.wp == 4 && c.cf == 2 && c.pf == 4) return kind == CK_3x3;
+    if (c.wc == 4 && c.wp == 2 && c.cf == 2 && c.pf == 4) return kind == CK_1x1 && dtype == DT_F32;
 #define ZJAI_CHECK(a, b, cc, d) if (c.wc == a && c.wp == b && c.cf == cc && c.pf == d) return true;
     ZJAI_CFGS(ZJAI_CHECK)
 #undef ZJAI_CHECK
@@ -1043,6 +1045,10 @@ template <typename T>
 static hipError_t go_cfg(int kind, TileCfg c, const ConvParams& p, hipStream_t s) {
     if (c.wc == 2 && c.wp == 4 && c.cf == 2 && c.pf == 4)
         return kind == CK_3x3 ? go<T, 3, 3, 1, false, 2, 4, 2, 4>(p, s) : hipErrorInvalidValue;
+    if (c.wc == 4 && c.wp == 2 && c.cf == 2 && c.pf == 4) {
+        if constexpr (sizeof(T) == 4) return kind == CK_1x1 ? go<T, 1, 1, 1, false, 4, 2, 2, 4>(p, s) : hipErrorInvalidValue;
+        return hipErrorInvalidValue;
+    }
 #define ZJAI_GO(a, b, cc, d) \
     if (c.wc == a && c.wp == b && c.cf == cc && c.pf == d) return go_kind<T, a, b, cc, d>(kind, p, s);
     ZJAI_CFGS(ZJAI_GO)

@@ -277,11 +277,13 @@ void Layer::out_size(int h, int w, int* oh, int* ow) const {
 
 // Tile shape of a layer: narrow groups / outputs take 16- or 32-channel tiles; dense stride-1
 // 3x3 layers take the 8-wave 64-channel x 16-row tile (two waves per SIMD from one workgroup hide
-// each other's LDS and barrier waits: +2-3 % on the config-5 picture in every precision).
-static TileCfg pick_cfg(int cout_g, int kind) {
+// each other's LDS and barrier waits: +2-3 % on the config-5 picture in every precision); fp32
+// 1x1 layers with >= 256 outputs the 8-wave 128-channel x 8-row tile (+2 % in fp32).
+static TileCfg pick_cfg(int cout_g, int kind, int dtype) {
     if (cout_g <= 16) return TileCfg{1, 4, 1, 2};
     if (cout_g <= 32) return TileCfg{1, 4, 2, 2};
     if (kind == CK_3x3) return TileCfg{2, 4, 2, 4};
+    if (kind == CK_1x1 && dtype == DT_F32 && cout_g >= 256 && cout_g % 128 == 0) return TileCfg{4, 2, 2, 4};
     return TileCfg{2, 2, 2, 4};
 }
 
@@ -320,7 +322,7 @@ LayerP make_conv(Context& ctx, int cin, int cout, int kh, int kw, int stride, in
     else throw Error(ZJAI_E_UNSUPPORTED, "conv2d: kernel geometry without a HIP kernel");
     const int vec = 16 / dtype_size(dtype);
     if (cin_g % vec) throw Error(ZJAI_E_UNSUPPORTED, "conv2d: channels per group not vector aligned");
-    L->cfg = pick_cfg(cout_g, L->kind);
+    L->cfg = pick_cfg(cout_g, L->kind, dtype);
     const int NB = L->cfg.wc * L->cfg.cf;
     const int CK = 64 / dtype_size(dtype);
     const int T = kh * kw;
@@ -383,7 +385,7 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
     }
     const int vec = 16 / dtype_size(dtype);
     if (cin % vec) throw Error(ZJAI_E_UNSUPPORTED, "conv_transpose2d: channels not vector aligned");
-    L->cfg = pick_cfg(cout, CK_T3);
+    L->cfg = pick_cfg(cout, CK_T3, dtype);
     const int NB = L->cfg.wc * L->cfg.cf;
     const int CK = 64 / dtype_size(dtype);
     L->nblk_g = round_up(ceil_div(cout, 16), NB);
@@ -454,7 +456,8 @@ std::string conv_kernel_name(int kind, int dtype, TileCfg c) {
                                 "3, 3, 1, true"};
     static const char* ty[] = {"float", "_Float16", "__bf16"};
     char buf[128];
-    const bool dma = dtype == DT_F32 && c.wc == 2 && c.cf == 2 && c.pf == 4 && (c.wp == 2 || c.wp == 4);
+    const bool dma = dtype == DT_F32 && c.cf == 2 && c.pf == 4 &&
+                     ((c.wc == 2 && (c.wp == 2 || c.wp == 4)) || (c.wc == 4 && c.wp == 2));
     if (dma)  // the fp32 dense shapes run conv_dma_f32 (conv.hip)
         snprintf(buf, sizeof buf, "conv_dma_f32<%s, %d, %d, %d, %d>", geo[kind], c.wc, c.wp, c.cf, c.pf);
     else
