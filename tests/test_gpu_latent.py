@@ -113,11 +113,17 @@ def test_reconstruct_latent_matches_oracle(eng, ccs, height, width, regions):
 
 
 @pytest.mark.parametrize("ccs", [0, 1])
-@pytest.mark.parametrize("regions", [None, geo.Regions(2, 3, True), geo.Regions(2, 2, False, 1, 4)])
-def test_reconstruct_latent_with_index_map_weights_is_exact(eng, ccs, regions):
+@pytest.mark.parametrize("height,width,regions", [
+    (1024, 1536, None),
+    (1024, 1536, geo.Regions(2, 3, True)),
+    (1024, 1536, geo.Regions(2, 2, False, 1, 4)),
+    # nine regions of four shapes: corner, edge and interior regions share batches
+    (1536, 1536, geo.Regions(3, 3, False, 1, 4)),
+    (2048, 2048, geo.Regions(4, 4, True)),
+])
+def test_reconstruct_latent_with_index_map_weights_is_exact(eng, ccs, height, width, regions):
     """The oracle's closed-form pins run on the GPU: identity weights make every MFMA sum a
     single product plus exact zeros, so psi and y_hat are bit-exact."""
-    height, width = 1024, 1536
     lh, lw, zh, zw = _sizes(ccs, height, width)
     c = synth.LATENT_CHANNELS[ccs]
     p = _delta_params(c)

@@ -930,7 +930,8 @@ extern "C" int32_t zjai_hyper_decoder_forward(zjai_ctx* ctx, const zjai_net* net
         TensorP z = cx.alloc(1, c, zh, zw, m.dtype);
         {
             LaunchScope sc(cx, kname("k_i8_planar_to_nhwc", m.dtype), 0.0, (1.0 + dtype_size(m.dtype)) * zn);
-            ZJAI_HIP(launch_i8_planar_to_nhwc((const int8_t*)zdev, c, zh, zw, 0, 0, zh, zw, z->v, m.dtype, cx.stream));
+            ZJAI_HIP(launch_i8_planar_to_nhwc((const int8_t*)zdev, c, zh, zw, Windows{}, 1, zh, zw, z->v, m.dtype,
+                                              cx.stream));
         }
         TensorP t = hyper_decoder_forward(cx, m, z, out_h, out_w);
         const size_t pn = (size_t)4 * c * out_h * out_w;
@@ -962,7 +963,7 @@ extern "C" int32_t zjai_context_decompress(zjai_ctx* ctx, const zjai_net* net, c
         float* ydev = (float*)cx.pool.alloc(rn * 4);
         std::shared_ptr<void> keep2(ydev, [&cx](void* q) { cx.pool.release(q); });
         ZJAI_HIP(hipMemcpyAsync(rdev, residual, rn * 4, hipMemcpyHostToDevice, cx.stream));
-        latent_decompress(cx, m, rdev, w, (long long)h * w, h, w, ps, ydev);
+        latent_decompress(cx, m, rdev, w, (long long)h * w, Windows{}, h, w, ps, ydev);
         ZJAI_HIP(hipMemcpyAsync(y_hat, ydev, rn * 4, hipMemcpyDeviceToHost, cx.stream));
         ZJAI_HIP(hipStreamSynchronize(cx.stream));
     });

@@ -571,7 +571,7 @@ void secondary_forward(Context& ctx, const Net& net, const TensorP& y_luma, cons
 
 TensorP hyper_decoder_forward(Context& ctx, const Net& net, const TensorP& z, int out_h, int out_w) {
     if (net.kind != NET_LATENT) throw Error(ZJAI_E_INVALID_ARGUMENT, "hyper-decoder: not a latent model");
-    if (z->c != net.chs || z->n != 1 || z->dtype != net.dtype)
+    if (z->c != net.chs || z->dtype != net.dtype)
         throw Error(ZJAI_E_INVALID_ARGUMENT, "hyper-decoder: z_hat channels / precision differ from the model");
     Fwd f{ctx, net};
     TensorP x = f.conv("hyper_decoder.conv1", z);
@@ -592,17 +592,17 @@ TensorP hyper_decoder_forward(Context& ctx, const Net& net, const TensorP& z, in
 }
 
 void latent_decompress(Context& ctx, const Net& net, const float* res, long long res_row, long long res_plane,
-                       int H, int W, const TensorP& psi, float* y_hat) {
+                       const Windows& rwin, int H, int W, const TensorP& psi, float* y_hat) {
     if (net.kind != NET_LATENT) throw Error(ZJAI_E_INVALID_ARGUMENT, "context model: not a latent model");
-    const int C = net.chs, dt = net.dtype;
-    if (psi->dtype != dt || psi->n != 1) throw Error(ZJAI_E_INVALID_ARGUMENT, "context model: psi precision");
+    const int C = net.chs, dt = net.dtype, N = psi->n;
+    if (psi->dtype != dt) throw Error(ZJAI_E_INVALID_ARGUMENT, "context model: psi precision");
     if (H <= 0 || W <= 0) throw Error(ZJAI_E_INVALID_ARGUMENT, "context model: empty residual");
     if (!net.context) {
         // upshuffle_psi_par (src/model/mcm.rs:742-746) checks
         if (psi->c != 4 * C || 2 * psi->h < H || 2 * psi->w < W)
             throw Error(ZJAI_E_INVALID_ARGUMENT, "upshuffle_psi: shape mismatch");
-        LaunchScope sc(ctx, kname("k_upshuffle_psi", dt), 0.0, (double)C * H * W * (8.0 + dtype_size(dt)));
-        ZJAI_HIP(launch_upshuffle_psi(psi->v, dt, C, psi->h, psi->w, res, res_row, res_plane, H, W, y_hat,
+        LaunchScope sc(ctx, kname("k_upshuffle_psi", dt), 0.0, (double)N * C * H * W * (8.0 + dtype_size(dt)));
+        ZJAI_HIP(launch_upshuffle_psi(psi->v, dt, N, C, psi->h, psi->w, res, res_row, res_plane, rwin, H, W, y_hat,
                                       ctx.stream));
         return;
     }
@@ -613,7 +613,7 @@ void latent_decompress(Context& ctx, const Net& net, const float* res, long long
     static const int pos[4][2] = {{0, 0}, {1, 1}, {0, 1}, {1, 0}};
     Fwd f{ctx, net};
     // The reconstructed stages, concatenated along channels: stage s lands in [s C, (s + 1) C).
-    TensorP stages = ctx.alloc(1, 4 * C, hh, hw, dt);
+    TensorP stages = ctx.alloc(N, 4 * C, hh, hw, dt);
     const double es = dtype_size(dt);
     for (int s = 0; s < 4; ++s) {
         ctx.check_stop();
@@ -622,11 +622,11 @@ void latent_decompress(Context& ctx, const Net& net, const float* res, long long
         TensorP in = psi_s;
         if (s > 0) {
             TensorP t = f.conv(p + ".conv.0", channel_view(stages, 0, s * C));
-            TensorP joined = ctx.alloc(1, 2 * C, hh, hw, dt);
+            TensorP joined = ctx.alloc(N, 2 * C, hh, hw, dt);
             f.conv(p + ".conv.1", t, Epilogue{}, channel_view(joined, 0, C));
             {
-                LaunchScope sc(ctx, kname("k_copy", dt), 0.0, 2.0 * es * C * hh * hw);
-                ZJAI_HIP(launch_copy(psi_s->v, channel_view(joined, C, C)->v, dt, 1, C, hh, hw, ctx.stream));
+                LaunchScope sc(ctx, kname("k_copy", dt), 0.0, 2.0 * es * N * C * hh * hw);
+                ZJAI_HIP(launch_copy(psi_s->v, channel_view(joined, C, C)->v, dt, N, C, hh, hw, ctx.stream));
             }
             in = joined;
         }
@@ -637,9 +637,9 @@ void latent_decompress(Context& ctx, const Net& net, const float* res, long long
         a = f.conv(p + ".fusion_pred_net.conv2", a, er);
         TensorP st = channel_view(stages, s * C, C);
         f.conv(p + ".fusion_pred_net.conv3", a, Epilogue{}, st);
-        LaunchScope sc(ctx, kname("k_mcm_stage", dt), 0.0, (double)C * hh * hw * (2.0 * es + 8.0));
-        ZJAI_HIP(launch_mcm_stage(st->v, dt, C, hh, hw, res, res_row, res_plane, H, W, pos[s][0], pos[s][1], y_hat,
-                                  ctx.stream));
+        LaunchScope sc(ctx, kname("k_mcm_stage", dt), 0.0, (double)N * C * hh * hw * (2.0 * es + 8.0));
+        ZJAI_HIP(launch_mcm_stage(st->v, dt, N, C, hh, hw, res, res_row, res_plane, rwin, H, W, pos[s][0], pos[s][1],
+                                  y_hat, ctx.stream));
     }
 }
 

@@ -11,59 +11,69 @@ namespace {
 
 inline dim3 blocks_of(long long n) { return dim3((unsigned)((n + 255) / 256)); }
 
-// z_hat int8 planar [C][ZH][ZW], window at (x0, y0) of h x w -> NHWC view, exact in every storage
-// type (`Tensor<i8>` -> f32 -> `BTensor::from_planar`, src/model/hyper_decoder.rs:66-74).
+// z_hat int8 planar [C][ZH][ZW], item b's window at (win.x0[b], win.y0[b]) of h x w -> NHWC view,
+// exact in every storage type (`Tensor<i8>` -> f32 -> `BTensor::from_planar`,
+// src/model/hyper_decoder.rs:66-74).
 template <typename T>
-__global__ void __launch_bounds__(256) k_i8_planar_to_nhwc(const int8_t* z, int C, int ZH, int ZW, int y0,
-                                                           int x0, int h, int w, View dst) {
+__global__ void __launch_bounds__(256) k_i8_planar_to_nhwc(const int8_t* z, int C, int ZH, int ZW, Windows win,
+                                                           int N, int h, int w, View dst) {
     const int q = C / 4;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)h * w * q) return;
+    if (i >= (long long)N * h * w * q) return;
     const int cq = (int)(i % q);
-    const long long t = i / q;
-    const int x = (int)(t % w), y = (int)(t / w);
+    long long t = i / q;
+    const int x = (int)(t % w);
+    t /= w;
+    const int y = (int)(t % h), b = (int)(t / h);
     f32x4 v;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) v[k] = (float)z[((long long)(cq * 4 + k) * ZH + y0 + y) * ZW + x0 + x];
-    store4<T>(at_mut<T>(dst, 0, y, x, cq * 4), v);
+    for (int k = 0; k < 4; ++k)
+        v[k] = (float)z[((long long)(cq * 4 + k) * ZH + win.y0[b] + y) * ZW + win.x0[b] + x];
+    store4<T>(at_mut<T>(dst, b, y, x, cq * 4), v);
 }
 
 // One context-model stage (ContextModel::decompress_with, src/model/mcm.rs:203-236): the stage's
 // mean (NHWC, C channels, hh x hw half-resolution grid) becomes mean + residual where the
 // latent sample (2y + py, 2x + px) exists -- one f32 add, in place, so the next stages read it as
-// context -- and the same value lands in y_hat (planar [C][H][W]). Samples of the padded border
-// keep the bare mean and write nothing.
+// context -- and the same value lands in y_hat (planar [N][C][H][W]). Samples of the padded
+// border keep the bare mean and write nothing. Item b's residual window starts at
+// (rwin.x0[b], rwin.y0[b]) of a plane with the given row / plane strides.
 template <typename T>
-__global__ void __launch_bounds__(256) k_mcm_stage(View st, int C, int hh, int hw, const float* res,
-                                                   long long res_row, long long res_plane, int H, int W,
-                                                   int py, int px, float* y_hat) {
+__global__ void __launch_bounds__(256) k_mcm_stage(View st, int N, int C, int hh, int hw, const float* res,
+                                                   long long res_row, long long res_plane, Windows rwin, int H,
+                                                   int W, int py, int px, float* y_hat) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)hh * hw * C) return;
+    if (i >= (long long)N * hh * hw * C) return;
     const int c = (int)(i % C);
-    const long long t = i / C;
-    const int x = (int)(t % hw), y = (int)(t / hw);
+    long long t = i / C;
+    const int x = (int)(t % hw);
+    t /= hw;
+    const int y = (int)(t % hh), b = (int)(t / hh);
     const int sy = 2 * y + py, sx = 2 * x + px;
     if (sy >= H || sx >= W) return;
-    T* p = at_mut<T>(st, 0, y, x, c);
-    const float v = to_f32(*p) + res[(long long)c * res_plane + (long long)sy * res_row + sx];
+    T* p = at_mut<T>(st, b, y, x, c);
+    const float v = to_f32(*p) + res[(long long)c * res_plane + (long long)(rwin.y0[b] + sy) * res_row + rwin.x0[b] + sx];
     *p = from_f32<T>(v);
-    y_hat[((long long)c * H + sy) * W + sx] = v;
+    y_hat[(((long long)b * C + c) * H + sy) * W + sx] = v;
 }
 
 // A component without a context model (src/decoder/reconstruct.rs:191-202): the psi quarters
 // up-shuffled to latent resolution (`upshuffle_psi_par`, src/model/mcm.rs:742-764: stage
 // (y % 2, x % 2) -> quarter {0, 2, 3, 1}) plus the residual, one f32 add per sample.
 template <typename T>
-__global__ void __launch_bounds__(256) k_upshuffle_psi(View psi, int C, const float* res, long long res_row,
-                                                       long long res_plane, int H, int W, float* y_hat) {
+__global__ void __launch_bounds__(256) k_upshuffle_psi(View psi, int N, int C, const float* res, long long res_row,
+                                                       long long res_plane, Windows rwin, int H, int W,
+                                                       float* y_hat) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)C * H * W) return;
+    if (i >= (long long)N * C * H * W) return;
     const int x = (int)(i % W);
-    const long long t = i / W;
-    const int y = (int)(t % H), c = (int)(t / H);
+    long long t = i / W;
+    const int y = (int)(t % H);
+    t /= H;
+    const int c = (int)(t % C), b = (int)(t / C);
     const int quarter = (0x1320 >> (4 * ((y & 1) * 2 + (x & 1)))) & 0xf;  // {0, 2, 3, 1}
-    const float m = to_f32(*at<T>(psi, 0, y >> 1, x >> 1, quarter * C + c));
-    y_hat[i] = m + res[(long long)c * res_plane + (long long)y * res_row + x];
+    const float m = to_f32(*at<T>(psi, b, y >> 1, x >> 1, quarter * C + c));
+    y_hat[i] = m + res[(long long)c * res_plane + (long long)(rwin.y0[b] + y) * res_row + rwin.x0[b] + x];
 }
 
 // `assign_par` (src/decoder/reconstruct.rs:38-62) from an NHWC tile: dst[c][dy0 + y][dx0 + x] =
@@ -101,32 +111,36 @@ __global__ void __launch_bounds__(256) k_assign_planar(const float* src, int C, 
         default: return hipErrorInvalidValue;                                                \
     }
 
-hipError_t launch_i8_planar_to_nhwc(const int8_t* z, int C, int ZH, int ZW, int y0, int x0, int h, int w,
+hipError_t launch_i8_planar_to_nhwc(const int8_t* z, int C, int ZH, int ZW, const Windows& win, int N, int h, int w,
                                     View dst, int dtype, hipStream_t s) {
-    if (C % 4 || y0 < 0 || x0 < 0 || y0 + h > ZH || x0 + w > ZW) return hipErrorInvalidValue;
-    const long long n = (long long)h * w * (C / 4);
+    if (C % 4 || N < 1 || N > MAXB) return hipErrorInvalidValue;
+    for (int b = 0; b < N; ++b)
+        if (win.y0[b] < 0 || win.x0[b] < 0 || win.y0[b] + h > ZH || win.x0[b] + w > ZW) return hipErrorInvalidValue;
+    const long long n = (long long)N * h * w * (C / 4);
     if (n <= 0) return hipSuccess;
-    ZJAI_LATENT_DISPATCH(dtype, k_i8_planar_to_nhwc, <<<blocks_of(n), 256, 0, s>>>(z, C, ZH, ZW, y0, x0, h, w, dst))
+    ZJAI_LATENT_DISPATCH(dtype, k_i8_planar_to_nhwc, <<<blocks_of(n), 256, 0, s>>>(z, C, ZH, ZW, win, N, h, w, dst))
     return hipGetLastError();
 }
 
-hipError_t launch_mcm_stage(View st, int dtype, int C, int hh, int hw, const float* res, long long res_row,
-                            long long res_plane, int H, int W, int py, int px, float* y_hat, hipStream_t s) {
-    if (2 * hh < H || 2 * hw < W || py < 0 || py > 1 || px < 0 || px > 1) return hipErrorInvalidValue;
-    const long long n = (long long)hh * hw * C;
+hipError_t launch_mcm_stage(View st, int dtype, int N, int C, int hh, int hw, const float* res, long long res_row,
+                            long long res_plane, const Windows& rwin, int H, int W, int py, int px, float* y_hat,
+                            hipStream_t s) {
+    if (N < 1 || N > MAXB || 2 * hh < H || 2 * hw < W || py < 0 || py > 1 || px < 0 || px > 1)
+        return hipErrorInvalidValue;
+    const long long n = (long long)N * hh * hw * C;
     if (n <= 0) return hipSuccess;
-    ZJAI_LATENT_DISPATCH(dtype, k_mcm_stage,
-                         <<<blocks_of(n), 256, 0, s>>>(st, C, hh, hw, res, res_row, res_plane, H, W, py, px, y_hat))
+    ZJAI_LATENT_DISPATCH(dtype, k_mcm_stage, <<<blocks_of(n), 256, 0, s>>>(st, N, C, hh, hw, res, res_row, res_plane,
+                                                                           rwin, H, W, py, px, y_hat))
     return hipGetLastError();
 }
 
-hipError_t launch_upshuffle_psi(View psi, int dtype, int C, int ph, int pw, const float* res, long long res_row,
-                                long long res_plane, int H, int W, float* y_hat, hipStream_t s) {
-    if (2 * ph < H || 2 * pw < W) return hipErrorInvalidValue;
-    const long long n = (long long)C * H * W;
+hipError_t launch_upshuffle_psi(View psi, int dtype, int N, int C, int ph, int pw, const float* res, long long res_row,
+                                long long res_plane, const Windows& rwin, int H, int W, float* y_hat, hipStream_t s) {
+    if (N < 1 || N > MAXB || 2 * ph < H || 2 * pw < W) return hipErrorInvalidValue;
+    const long long n = (long long)N * C * H * W;
     if (n <= 0) return hipSuccess;
     ZJAI_LATENT_DISPATCH(dtype, k_upshuffle_psi,
-                         <<<blocks_of(n), 256, 0, s>>>(psi, C, res, res_row, res_plane, H, W, y_hat))
+                         <<<blocks_of(n), 256, 0, s>>>(psi, N, C, res, res_row, res_plane, rwin, H, W, y_hat))
     return hipGetLastError();
 }
 

@@ -106,17 +106,19 @@ hipError_t launch_attention_fold(const float* proj, const float* attn, int N, in
                                  int dtype, int nblk, void* wpk, long long w_bstride,
                                  hipStream_t s);
 
-// Latent reconstruction (src/decoder/reconstruct.rs:81-234), one item per launch:
-// int8 planar z_hat window -> NHWC view of the storage type;
-hipError_t launch_i8_planar_to_nhwc(const int8_t* z, int C, int ZH, int ZW, int y0, int x0, int h, int w,
+// Latent reconstruction (src/decoder/reconstruct.rs:81-234), N regions of one shape per launch:
+// int8 planar z_hat windows (per item origin) -> NHWC view of the storage type;
+hipError_t launch_i8_planar_to_nhwc(const int8_t* z, int C, int ZH, int ZW, const Windows& win, int N, int h, int w,
                                     View dst, int dtype, hipStream_t s);
-// context-model stage (py, px): st (hh x hw x C, the mean) += residual in place, y_hat planar
-// [C][H][W] written at the stage's samples; residual planar with the given row / plane strides;
-hipError_t launch_mcm_stage(View st, int dtype, int C, int hh, int hw, const float* res, long long res_row,
-                            long long res_plane, int H, int W, int py, int px, float* y_hat, hipStream_t s);
-// no context model: y_hat [C][H][W] = up-shuffled psi (ph x pw x 4C) + residual;
-hipError_t launch_upshuffle_psi(View psi, int dtype, int C, int ph, int pw, const float* res, long long res_row,
-                                long long res_plane, int H, int W, float* y_hat, hipStream_t s);
+// context-model stage (py, px): st (N x hh x hw x C, the means) += residual in place, y_hat
+// planar [N][C][H][W] written at the stage's samples; item b's residual window starts at
+// (rwin.x0[b], rwin.y0[b]) of planes with the given row / plane strides;
+hipError_t launch_mcm_stage(View st, int dtype, int N, int C, int hh, int hw, const float* res, long long res_row,
+                            long long res_plane, const Windows& rwin, int H, int W, int py, int px, float* y_hat,
+                            hipStream_t s);
+// no context model: y_hat [N][C][H][W] = up-shuffled psi (N x ph x pw x 4C) + residual;
+hipError_t launch_upshuffle_psi(View psi, int dtype, int N, int C, int ph, int pw, const float* res, long long res_row,
+                                long long res_plane, const Windows& rwin, int H, int W, float* y_hat, hipStream_t s);
 // region merges: a clamped rectangle of an NHWC tile (SH x SW) or of a planar f32 tile into a
 // planar f32 destination [C][DH][DW].
 hipError_t launch_assign_from_nhwc(View src, int dtype, int C, int SH, int SW, int oy, int ox, int h, int w,

@@ -4,6 +4,7 @@
 // on the conv kernels (graph.hip), the data movement on latent.hip's kernels.
 
 #include <algorithm>
+#include <map>
 
 #include "runtime.h"
 
@@ -121,51 +122,116 @@ void reconstruct_latent(Context& ctx, const Net& net, int height, int width, con
     ZJAI_HIP(hipMemsetAsync(psi.p, 0, pn * 4, ctx.stream));
     ZJAI_HIP(hipMemsetAsync(yhat.p, 0, rn * 4, ctx.stream));
 
+    // Regions of one shape run as one batch (up to MAXB) through each network; the results are
+    // merged region by region in raster order afterwards, so where extended regions overlap the
+    // later one wins, as in the reference.
+    auto batches = [&](auto key_of) {
+        std::vector<std::vector<int>> out;
+        std::map<std::vector<int>, int> slot;
+        for (int r = 0; r < n; ++r) {
+            const std::vector<int> k = key_of(r);
+            auto it = slot.find(k);
+            if (it == slot.end() || out[it->second].size() == (size_t)MAXB) {
+                slot[k] = (int)out.size();
+                out.push_back({});
+            }
+            out[slot[k]].push_back(r);
+        }
+        return out;
+    };
+    auto item = [](const TensorP& t, int b) {
+        View v = t->v;
+        v.p = (char*)v.p + (long long)b * v.bstride * dtype_size(t->dtype);
+        return v;
+    };
+
     // 1. psi per region (hyper-decoder on the region's z window), merged in raster order.
+    std::vector<int> oh(n), ow(n);
     for (int r = 0; r < n; ++r) {
-        ctx.check_stop();
         const RArea it = img.extended[r], zt = zg.extended[r];
         const int th = ccs == 0 ? it.h : ceil_div(it.h, 2), tw = ccs == 0 ? it.w : ceil_div(it.w, 2);
         const int divider = ccs == 0 ? 32 : 16;
-        const int out_h = 2 * zt.h - hyper_crop(th, divider), out_w = 2 * zt.w - hyper_crop(tw, divider);
-        if (out_h <= 0 || out_w <= 0) throw Error(ZJAI_E_INVALID_ARGUMENT, "reconstruct_latent: region geometry");
+        oh[r] = 2 * zt.h - hyper_crop(th, divider);
+        ow[r] = 2 * zt.w - hyper_crop(tw, divider);
+        if (oh[r] <= 0 || ow[r] <= 0) throw Error(ZJAI_E_INVALID_ARGUMENT, "reconstruct_latent: region geometry");
         if (zt.h <= 0 || zt.w <= 0 || zt.y + zt.h > zh || zt.x + zt.w > zw)
             throw Error(ZJAI_E_INVALID_ARGUMENT, "reconstruct_latent: z_hat window outside tensor");
-        TensorP z = ctx.alloc(1, C, zt.h, zt.w, dt);
-        {
-            LaunchScope sc(ctx, kname("k_i8_planar_to_nhwc", dt), 0.0, (1.0 + dtype_size(dt)) * C * zt.h * zt.w);
-            ZJAI_HIP(launch_i8_planar_to_nhwc(zdev.as<int8_t>(), C, zh, zw, zt.y, zt.x, zt.h, zt.w, z->v, dt,
-                                              ctx.stream));
+    }
+    std::vector<TensorP> psi_of(n);
+    std::vector<int> psi_item(n);
+    for (const auto& bt : batches([&](int r) {
+             const RArea zt = zg.extended[r];
+             return std::vector<int>{zt.h, zt.w, oh[r], ow[r]};
+         })) {
+        ctx.check_stop();
+        const int nb = (int)bt.size();
+        const RArea z0 = zg.extended[bt[0]];
+        Windows win{};
+        for (int i = 0; i < nb; ++i) {
+            win.x0[i] = zg.extended[bt[i]].x;
+            win.y0[i] = zg.extended[bt[i]].y;
         }
-        TensorP t = hyper_decoder_forward(ctx, net, z, out_h, out_w);
+        TensorP z = ctx.alloc(nb, C, z0.h, z0.w, dt);
+        {
+            LaunchScope sc(ctx, kname("k_i8_planar_to_nhwc", dt), 0.0, (1.0 + dtype_size(dt)) * nb * C * z0.h * z0.w);
+            ZJAI_HIP(launch_i8_planar_to_nhwc(zdev.as<int8_t>(), C, zh, zw, win, nb, z0.h, z0.w, z->v, dt, ctx.stream));
+        }
+        TensorP t = hyper_decoder_forward(ctx, net, z, oh[bt[0]], ow[bt[0]]);
+        for (int i = 0; i < nb; ++i) {
+            psi_of[bt[i]] = t;
+            psi_item[bt[i]] = i;
+        }
+    }
+    for (int r = 0; r < n; ++r) {
+        const TensorP& t = psi_of[r];
         const RArea core = pg.extended[r];
         const int h = std::max(0, std::min({core.h, t->h, ph - core.y}));
         const int w = std::max(0, std::min({core.w, t->w, pw - core.x}));
         LaunchScope sc(ctx, kname("k_assign_from_nhwc", dt), 0.0, (4.0 + dtype_size(dt)) * 4 * C * h * w);
-        ZJAI_HIP(launch_assign_from_nhwc(t->v, dt, 4 * C, t->h, t->w, 0, 0, h, w, psi.as<float>(), ph, pw, core.y,
-                                         core.x, ctx.stream));
+        ZJAI_HIP(launch_assign_from_nhwc(item(t, psi_item[r]), dt, 4 * C, t->h, t->w, 0, 0, h, w, psi.as<float>(), ph,
+                                         pw, core.y, core.x, ctx.stream));
     }
+    psi_of.clear();
 
     // 2. y_hat per region (context model on the region's residual and psi windows), merged in
     // raster order: independent regions keep their whole latent area, dependent ones drop one
     // latent sample on each interior side (HD_MCM_TILE_OVERLAP / 2 / 16, reconstruct.rs:30-34).
     for (int r = 0; r < n; ++r) {
-        ctx.check_stop();
-        const RArea lt = lg.extended[r], pt = pg.extended[r], it = img.extended[r];
+        const RArea lt = lg.extended[r], pt = pg.extended[r];
         if (lt.h <= 0 || lt.w <= 0 || lt.y + lt.h > H || lt.x + lt.w > W || pt.h <= 0 || pt.w <= 0 ||
             pt.y + pt.h > ph || pt.x + pt.w > pw)
             throw Error(ZJAI_E_INVALID_ARGUMENT, "reconstruct_latent: region window outside tensor");
-        TensorP ps = ctx.alloc(1, 4 * C, pt.h, pt.w, dt);
-        {
-            Windows win{};
-            win.x0[0] = pt.x;
-            win.y0[0] = pt.y;
-            LaunchScope sc(ctx, kname("k_planar_to_nhwc", dt), 0.0, (4.0 + dtype_size(dt)) * 4 * C * pt.h * pt.w);
-            ZJAI_HIP(launch_planar_to_nhwc(psi.as<float>(), 4 * C, ph, pw, win, 1, pt.h, pt.w, ps->v, dt, ctx.stream));
+    }
+    std::vector<std::shared_ptr<DevBuf>> ytile_of(n);
+    std::vector<int> y_item(n);
+    for (const auto& bt : batches([&](int r) {
+             const RArea lt = lg.extended[r], pt = pg.extended[r];
+             return std::vector<int>{lt.h, lt.w, pt.h, pt.w};
+         })) {
+        ctx.check_stop();
+        const int nb = (int)bt.size();
+        const RArea l0 = lg.extended[bt[0]], p0 = pg.extended[bt[0]];
+        Windows pwin{}, rwin{};
+        for (int i = 0; i < nb; ++i) {
+            pwin.x0[i] = pg.extended[bt[i]].x;
+            pwin.y0[i] = pg.extended[bt[i]].y;
+            rwin.x0[i] = lg.extended[bt[i]].x;
+            rwin.y0[i] = lg.extended[bt[i]].y;
         }
-        DevBuf ytile(ctx, (size_t)C * lt.h * lt.w * 4);
-        latent_decompress(ctx, net, rdev.as<float>() + (long long)lt.y * W + lt.x, W, (long long)H * W, lt.h, lt.w,
-                          ps, ytile.as<float>());
+        TensorP ps = ctx.alloc(nb, 4 * C, p0.h, p0.w, dt);
+        {
+            LaunchScope sc(ctx, kname("k_planar_to_nhwc", dt), 0.0, (4.0 + dtype_size(dt)) * nb * 4 * C * p0.h * p0.w);
+            ZJAI_HIP(launch_planar_to_nhwc(psi.as<float>(), 4 * C, ph, pw, pwin, nb, p0.h, p0.w, ps->v, dt, ctx.stream));
+        }
+        auto ytile = std::make_shared<DevBuf>(ctx, (size_t)nb * C * l0.h * l0.w * 4);
+        latent_decompress(ctx, net, rdev.as<float>(), W, (long long)H * W, rwin, l0.h, l0.w, ps, ytile->as<float>());
+        for (int i = 0; i < nb; ++i) {
+            ytile_of[bt[i]] = ytile;
+            y_item[bt[i]] = i;
+        }
+    }
+    for (int r = 0; r < n; ++r) {
+        const RArea lt = lg.extended[r], it = img.extended[r];
         RArea core = lt;
         int ox = 0, oy = 0;
         if (!rp.independent) {
@@ -180,9 +246,10 @@ void reconstruct_latent(Context& ctx, const Net& net, int height, int width, con
         }
         const int h = std::max(0, std::min({core.h, lt.h - oy, H - core.y}));
         const int w = std::max(0, std::min({core.w, lt.w - ox, W - core.x}));
+        const float* src = ytile_of[r]->as<float>() + (size_t)y_item[r] * C * lt.h * lt.w;
         LaunchScope sc(ctx, "k_assign_planar", 0.0, 8.0 * C * h * w);
-        ZJAI_HIP(launch_assign_planar(ytile.as<float>(), C, lt.h, lt.w, oy, ox, h, w, yhat.as<float>(), H, W, core.y,
-                                      core.x, ctx.stream));
+        ZJAI_HIP(launch_assign_planar(src, C, lt.h, lt.w, oy, ox, h, w, yhat.as<float>(), H, W, core.y, core.x,
+                                      ctx.stream));
     }
     ZJAI_HIP(hipMemcpyAsync(psi_out, psi.p, pn * 4, hipMemcpyDeviceToHost, ctx.stream));
     ZJAI_HIP(hipMemcpyAsync(y_out, yhat.p, rn * 4, hipMemcpyDeviceToHost, ctx.stream));

@@ -246,11 +246,12 @@ NetP build_latent_net(Context& ctx, int comp, int dtype, const std::map<std::str
 // (NHWC, 4C channels, out_h x out_w).
 TensorP hyper_decoder_forward(Context& ctx, const Net& net, const TensorP& z, int out_h, int out_w);
 // `ContextModel::decompress_with` (src/model/mcm.rs:171-240), or for a net without a context
-// model the up-shuffled psi plus the residual (src/decoder/reconstruct.rs:191-202): residual
-// planar f32 on the device ([C] planes of H x W with the given row / plane strides) and psi
-// (NHWC, 4C, ceil(H/2) x ceil(W/2)) -> y_hat planar f32 [C][H][W] on the device.
+// model the up-shuffled psi plus the residual (src/decoder/reconstruct.rs:191-202), for psi->n
+// regions of one shape at once: residual planar f32 on the device ([C] planes with the given row
+// / plane strides; item b's H x W window starts at (rwin.x0[b], rwin.y0[b])) and psi (NHWC, 4C,
+// ceil(H/2) x ceil(W/2) per item) -> y_hat planar f32 [N][C][H][W] on the device.
 void latent_decompress(Context& ctx, const Net& net, const float* res, long long res_row, long long res_plane,
-                       int H, int W, const TensorP& psi, float* y_hat);
+                       const Windows& rwin, int H, int W, const TensorP& psi, float* y_hat);
 
 // Region geometry (src/tools/regions.rs:47-150).
 enum RegionPlane : int { PLANE_LATENT = 0, PLANE_PSI = 1, PLANE_HYPER_LATENT = 2, PLANE_IMAGE = 3 };
