@@ -341,6 +341,89 @@ ZJAI_API int32_t zjai_reconstruct_latent(zjai_ctx* ctx, const zjai_net* net, int
                                          const float* residual, int32_t h, int32_t w, float* psi,
                                          float* y_hat);
 
+/* ------------------------------------------------------------------------- weight readers */
+
+/* Host only (no context, no device). Failures return ZJAI_E_MODEL (malformed file, missing or
+ * mistyped tensor), ZJAI_E_LIMIT (table sizes, small output buffers) or
+ * ZJAI_E_INVALID_ARGUMENT; zjai_last_error(NULL, ...) holds the message. */
+typedef struct zjai_checkpoint zjai_checkpoint;
+typedef struct zjai_bundle zjai_bundle;
+
+/* Element types by their ZJM1 codes (`dtype_code`, src/weights/packed.rs:62-75). */
+#define ZJAI_DTYPE_F64 0
+#define ZJAI_DTYPE_F32 1
+#define ZJAI_DTYPE_F16 2
+#define ZJAI_DTYPE_I64 3
+#define ZJAI_DTYPE_I32 4
+#define ZJAI_DTYPE_I16 5
+#define ZJAI_DTYPE_I8 6
+#define ZJAI_DTYPE_U8 7
+#define ZJAI_DTYPE_BOOL 8
+#define ZJAI_MAX_RANK 8
+
+/* `Checkpoint::parse` (src/weights/mod.rs:135-187): a packed ZJM1 file (by its magic) or a
+ * PyTorch `.pth` checkpoint (stored ZIP, `src/weights/zip.rs`, whose data.pkl runs through a
+ * data-only pickle interpreter, `src/weights/pickle.rs`: nothing in the file is executed).
+ * The bytes are copied; the caller may free them on return. */
+ZJAI_API int32_t zjai_checkpoint_parse(const void* data, size_t len, zjai_checkpoint** out);
+ZJAI_API int32_t zjai_checkpoint_destroy(zjai_checkpoint* ck);
+/* Top-level tensors (nested dict leaves as dotted names), integer entries and numeric lists
+ * (`tensor_names`, `ints`, `list`, src/weights/mod.rs:189-233); packed = 1 for ZJM1. */
+ZJAI_API int32_t zjai_checkpoint_counts(const zjai_checkpoint* ck, int32_t* tensors, int32_t* ints,
+                                        int32_t* lists, int32_t* packed);
+/* Name of tensor i (file order) into buf (NUL-terminated; ZJAI_E_LIMIT if cap is too small). */
+ZJAI_API int32_t zjai_checkpoint_tensor_name(const zjai_checkpoint* ck, int32_t i, char* buf, size_t cap);
+/* `Checkpoint::info` (src/weights/mod.rs:198-204): dtype, rank and up to ZJAI_MAX_RANK dims. */
+ZJAI_API int32_t zjai_checkpoint_info(const zjai_checkpoint* ck, const char* name, int32_t* dtype,
+                                      int32_t* rank, int64_t* shape);
+/* `Checkpoint::raw` (src/weights/mod.rs:330-340): contiguous little-endian row-major bytes of
+ * any dtype (strided views gathered); `bytes` must equal numel x element size. */
+ZJAI_API int32_t zjai_checkpoint_read(const zjai_checkpoint* ck, const char* name, void* out, size_t bytes);
+/* `Checkpoint::f32` (src/weights/mod.rs:342-378): an f32 tensor, or an f16 one (ZJB2 members)
+ * upcast exactly; `len` must equal numel. */
+ZJAI_API int32_t zjai_checkpoint_read_f32(const zjai_checkpoint* ck, const char* name, float* out, size_t len);
+/* Integer entry i (`epoch`, ...) and numeric list i (`clip_thres.E1B.MinList`): name into buf;
+ * for a list, *n = its length and up to `cap_values` values. */
+ZJAI_API int32_t zjai_checkpoint_int_at(const zjai_checkpoint* ck, int32_t i, char* buf, size_t cap,
+                                        int64_t* value);
+ZJAI_API int32_t zjai_checkpoint_list_at(const zjai_checkpoint* ck, int32_t i, char* buf, size_t cap,
+                                         double* values, size_t cap_values, size_t* n);
+/* `write_zjm` / `write_zjm_f16` (src/weights/packed.rs:166-225): the named tensors and all
+ * integer entries as a ZJM1 file; f16 != 0 stores f32 tensors (except `vr_vec.c`) as f16,
+ * round to nearest even. *len = the file size; out == NULL only queries it. */
+ZJAI_API int32_t zjai_checkpoint_write_zjm(const zjai_checkpoint* ck, const char* const* names, int32_t n,
+                                           int32_t f16, void* out, size_t cap, size_t* len);
+
+/* `PackedBundle::parse` / `add` (src/weights/packed.rs:299-345): ZJB1 / ZJB2 bundles of files
+ * addressed by their path relative to the model directory ("VM_common_int/Y_0.012.pth"); a
+ * path already present keeps its first copy. The bytes are copied. */
+ZJAI_API int32_t zjai_bundle_parse(const void* data, size_t len, zjai_bundle** out);
+ZJAI_API int32_t zjai_bundle_add(zjai_bundle* b, const void* data, size_t len);
+ZJAI_API int32_t zjai_bundle_destroy(zjai_bundle* b);
+/* `paths` (src/weights/packed.rs:347-351): count, then path i into buf. */
+ZJAI_API int32_t zjai_bundle_count(const zjai_bundle* b, int32_t* n);
+ZJAI_API int32_t zjai_bundle_path(const zjai_bundle* b, int32_t i, char* buf, size_t cap);
+/* `ModelSource::read` (src/weights/packed.rs:377-383): a file's bytes, borrowed until the bundle
+ * is destroyed (ZJAI_E_MODEL when absent). */
+ZJAI_API int32_t zjai_bundle_get(const zjai_bundle* b, const char* rel, const void** data, size_t* len);
+/* `notice` (src/weights/packed.rs:368-375): the first bundle's notice text; *len = its length. */
+ZJAI_API int32_t zjai_bundle_notice(const zjai_bundle* b, char* buf, size_t cap, size_t* len);
+/* `write_bundle` / `write_bundle_f16` (src/weights/packed.rs:235-334): n files as a ZJB1 (or,
+ * with f16 != 0, ZJB2) bundle. *len = the bundle size; out == NULL only queries it. */
+ZJAI_API int32_t zjai_bundle_write(const char* const* paths, const void* const* files, const size_t* sizes,
+                                   int32_t n, const char* notice, int32_t f16, void* out, size_t cap,
+                                   size_t* len);
+
+/* zjai_net_create / zjai_latent_model_create with the tensors of a parsed checkpoint
+ * (`SynthesisPrimary::load(ck, ...)`, src/model/synthesis.rs:242; `CommonModel::load`,
+ * src/model/common.rs:117-129): every f32 (or f16) tensor of the checkpoint is offered by name. */
+ZJAI_API int32_t zjai_net_create_from_checkpoint(zjai_ctx* ctx, int32_t op, int32_t component,
+                                                 int32_t precision, const zjai_checkpoint* ck,
+                                                 zjai_net** out);
+ZJAI_API int32_t zjai_latent_model_create_from_checkpoint(zjai_ctx* ctx, int32_t component,
+                                                          int32_t precision, const zjai_checkpoint* ck,
+                                                          zjai_net** out);
+
 #ifdef __cplusplus
 }
 #endif

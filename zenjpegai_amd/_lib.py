@@ -70,6 +70,7 @@ _pp = ctypes.POINTER(ctypes.c_void_p)
 _i32 = ctypes.c_int32
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i32p = ctypes.POINTER(ctypes.c_int32)
+_sz = ctypes.c_size_t
 
 # name -> argtypes (every entry point returns int32)
 PROTOTYPES = {
@@ -135,6 +136,30 @@ PROTOTYPES = {
                                 ctypes.c_size_t],
     "zjai_reconstruct_latent": [_vp, _vp, _i32, _i32, ctypes.POINTER(ZjaiRegions), _vp, _i32,
                                 _i32, _f32p, _i32, _i32, _f32p, _f32p],
+    # weight readers (host only)
+    "zjai_checkpoint_parse": [_vp, _sz, _pp],
+    "zjai_checkpoint_destroy": [_vp],
+    "zjai_checkpoint_counts": [_vp, _i32p, _i32p, _i32p, _i32p],
+    "zjai_checkpoint_tensor_name": [_vp, _i32, ctypes.c_char_p, _sz],
+    "zjai_checkpoint_info": [_vp, ctypes.c_char_p, _i32p, _i32p, ctypes.POINTER(ctypes.c_int64)],
+    "zjai_checkpoint_read": [_vp, ctypes.c_char_p, _vp, _sz],
+    "zjai_checkpoint_read_f32": [_vp, ctypes.c_char_p, _f32p, _sz],
+    "zjai_checkpoint_int_at": [_vp, _i32, ctypes.c_char_p, _sz, ctypes.POINTER(ctypes.c_int64)],
+    "zjai_checkpoint_list_at": [_vp, _i32, ctypes.c_char_p, _sz, ctypes.POINTER(ctypes.c_double),
+                                _sz, ctypes.POINTER(_sz)],
+    "zjai_checkpoint_write_zjm": [_vp, ctypes.POINTER(ctypes.c_char_p), _i32, _i32, _vp, _sz,
+                                  ctypes.POINTER(_sz)],
+    "zjai_bundle_parse": [_vp, _sz, _pp],
+    "zjai_bundle_add": [_vp, _vp, _sz],
+    "zjai_bundle_destroy": [_vp],
+    "zjai_bundle_count": [_vp, _i32p],
+    "zjai_bundle_path": [_vp, _i32, ctypes.c_char_p, _sz],
+    "zjai_bundle_get": [_vp, ctypes.c_char_p, _pp, ctypes.POINTER(_sz)],
+    "zjai_bundle_notice": [_vp, ctypes.c_char_p, _sz, ctypes.POINTER(_sz)],
+    "zjai_bundle_write": [ctypes.POINTER(ctypes.c_char_p), _pp, ctypes.POINTER(_sz), _i32,
+                          ctypes.c_char_p, _i32, _vp, _sz, ctypes.POINTER(_sz)],
+    "zjai_net_create_from_checkpoint": [_vp, _i32, _i32, _i32, _vp, _pp],
+    "zjai_latent_model_create_from_checkpoint": [_vp, _i32, _i32, _vp, _pp],
 }
 
 _lib = None

@@ -5,6 +5,7 @@
 #include <cstring>
 #include <mutex>
 
+#include "checkpoint.h"
 #include "runtime.h"
 
 using namespace zjai;
@@ -977,5 +978,239 @@ extern "C" int32_t zjai_reconstruct_latent(zjai_ctx* ctx, const zjai_net* net, i
         need(net->n->kind == NET_LATENT, "not a latent model");
         reconstruct_latent(ctx->c, *net->n, height, width, region_params(regions), z_hat, zh, zw, residual, h, w, psi,
                            y_hat);
+    });
+}
+
+// ------------------------------------------------------------------------- weight readers
+struct zjai_checkpoint {
+    std::unique_ptr<Checkpoint> ck;
+};
+struct zjai_bundle {
+    Bundle b;
+};
+
+namespace {
+
+// A NUL-terminated copy of `s` into buf (ZJAI_E_LIMIT when it does not fit).
+void copy_name(const std::string& s, char* buf, size_t cap) {
+    need(buf != nullptr, "null name buffer");
+    if (s.size() + 1 > cap) throw Error(ZJAI_E_LIMIT, "name buffer too small");
+    std::memcpy(buf, s.data(), s.size());
+    buf[s.size()] = 0;
+}
+
+const CkTensor& tensor_of(const zjai_checkpoint* ck, const char* name) {
+    need(ck != nullptr && name != nullptr, "null checkpoint or name");
+    const CkTensor* t = ck->ck->find(name);
+    if (!t) throw Error(ZJAI_E_MODEL, std::string("tensor `") + name + "` not found");
+    return *t;
+}
+
+// Every f32 / f16 tensor of a checkpoint as named f32 parameters; `hold` owns the data.
+std::map<std::string, Param> checkpoint_params(const Checkpoint& ck, std::vector<std::vector<float>>& hold) {
+    std::map<std::string, Param> P;
+    hold.reserve(ck.tensors().size());
+    for (const CkTensor& t : ck.tensors()) {
+        if (t.dtype != CK_F32 && t.dtype != CK_F16) continue;
+        if (P.count(t.name)) continue;  // the first of duplicate names, as a by-name lookup finds
+        Param p;
+        for (uint64_t d : t.shape) {
+            if (d > (uint64_t)INT32_MAX) throw Error(ZJAI_E_MODEL, "tensor `" + t.name + "`: dimension too large");
+            p.shape.push_back((int)d);
+        }
+        hold.push_back(ck.f32(t));
+        p.data = hold.back().data();
+        P[t.name] = p;
+    }
+    return P;
+}
+
+}  // namespace
+
+extern "C" int32_t zjai_checkpoint_parse(const void* data, size_t len, zjai_checkpoint** out) {
+    if (!out || (!data && len)) return ZJAI_E_INVALID_ARGUMENT;
+    *out = nullptr;
+    return guard(nullptr, [&] { *out = new zjai_checkpoint{Checkpoint::parse((const uint8_t*)data, len)}; });
+}
+
+extern "C" int32_t zjai_checkpoint_destroy(zjai_checkpoint* ck) {
+    delete ck;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_checkpoint_counts(const zjai_checkpoint* ck, int32_t* tensors, int32_t* ints, int32_t* lists,
+                                          int32_t* packed) {
+    if (!ck) return ZJAI_E_INVALID_ARGUMENT;
+    if (tensors) *tensors = (int32_t)ck->ck->tensors().size();
+    if (ints) *ints = (int32_t)ck->ck->ints().size();
+    if (lists) *lists = (int32_t)ck->ck->lists().size();
+    if (packed) *packed = ck->ck->packed() ? 1 : 0;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_checkpoint_tensor_name(const zjai_checkpoint* ck, int32_t i, char* buf, size_t cap) {
+    if (!ck || i < 0 || (size_t)i >= ck->ck->tensors().size()) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] { copy_name(ck->ck->tensors()[i].name, buf, cap); });
+}
+
+extern "C" int32_t zjai_checkpoint_info(const zjai_checkpoint* ck, const char* name, int32_t* dtype, int32_t* rank,
+                                        int64_t* shape) {
+    return guard(nullptr, [&] {
+        const CkTensor& t = tensor_of(ck, name);
+        if (t.shape.size() > ZJAI_MAX_RANK) throw Error(ZJAI_E_LIMIT, "tensor rank above 8");
+        if (dtype) *dtype = t.dtype;
+        if (rank) *rank = (int32_t)t.shape.size();
+        if (shape)
+            for (size_t k = 0; k < t.shape.size(); ++k) shape[k] = (int64_t)t.shape[k];
+    });
+}
+
+extern "C" int32_t zjai_checkpoint_read(const zjai_checkpoint* ck, const char* name, void* out, size_t bytes) {
+    return guard(nullptr, [&] {
+        const CkTensor& t = tensor_of(ck, name);
+        const std::vector<uint8_t> b = ck->ck->bytes(t);
+        if (b.size() != bytes) throw Error(ZJAI_E_INVALID_ARGUMENT, "output size differs from the tensor's bytes");
+        need(out != nullptr || bytes == 0, "null output");
+        if (bytes) std::memcpy(out, b.data(), bytes);
+    });
+}
+
+extern "C" int32_t zjai_checkpoint_read_f32(const zjai_checkpoint* ck, const char* name, float* out, size_t len) {
+    return guard(nullptr, [&] {
+        const CkTensor& t = tensor_of(ck, name);
+        const std::vector<float> v = ck->ck->f32(t);
+        if (v.size() != len) throw Error(ZJAI_E_INVALID_ARGUMENT, "output length differs from the tensor's size");
+        need(out != nullptr || len == 0, "null output");
+        if (len) std::memcpy(out, v.data(), len * 4);
+    });
+}
+
+extern "C" int32_t zjai_checkpoint_int_at(const zjai_checkpoint* ck, int32_t i, char* buf, size_t cap,
+                                          int64_t* value) {
+    if (!ck || i < 0 || (size_t)i >= ck->ck->ints().size()) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] {
+        const auto& e = ck->ck->ints()[i];
+        if (buf) copy_name(e.first, buf, cap);
+        if (value) *value = e.second;
+    });
+}
+
+extern "C" int32_t zjai_checkpoint_list_at(const zjai_checkpoint* ck, int32_t i, char* buf, size_t cap,
+                                           double* values, size_t cap_values, size_t* n) {
+    if (!ck || i < 0 || (size_t)i >= ck->ck->lists().size()) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] {
+        const auto& e = ck->ck->lists()[i];
+        if (buf) copy_name(e.first, buf, cap);
+        if (n) *n = e.second.size();
+        if (values) std::copy_n(e.second.begin(), std::min(cap_values, e.second.size()), values);
+    });
+}
+
+extern "C" int32_t zjai_checkpoint_write_zjm(const zjai_checkpoint* ck, const char* const* names, int32_t n,
+                                             int32_t f16, void* out, size_t cap, size_t* len) {
+    if (!ck || !len || n < 0 || (n && !names)) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] {
+        std::vector<std::string> nm;
+        for (int32_t i = 0; i < n; ++i) {
+            need(names[i] != nullptr, "null tensor name");
+            nm.push_back(names[i]);
+        }
+        const std::vector<uint8_t> f = write_zjm(*ck->ck, nm, f16 != 0);
+        *len = f.size();
+        if (!out) return;
+        if (cap < f.size()) throw Error(ZJAI_E_LIMIT, "output buffer too small");
+        std::memcpy(out, f.data(), f.size());
+    });
+}
+
+extern "C" int32_t zjai_bundle_parse(const void* data, size_t len, zjai_bundle** out) {
+    if (!out || (!data && len)) return ZJAI_E_INVALID_ARGUMENT;
+    *out = nullptr;
+    return guard(nullptr, [&] {
+        std::unique_ptr<zjai_bundle> b(new zjai_bundle());
+        b->b.add((const uint8_t*)data, len);
+        *out = b.release();
+    });
+}
+
+extern "C" int32_t zjai_bundle_add(zjai_bundle* b, const void* data, size_t len) {
+    if (!b || (!data && len)) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] { b->b.add((const uint8_t*)data, len); });
+}
+
+extern "C" int32_t zjai_bundle_destroy(zjai_bundle* b) {
+    delete b;
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_bundle_count(const zjai_bundle* b, int32_t* n) {
+    if (!b || !n) return ZJAI_E_INVALID_ARGUMENT;
+    *n = (int32_t)b->b.paths().size();
+    return ZJAI_OK;
+}
+
+extern "C" int32_t zjai_bundle_path(const zjai_bundle* b, int32_t i, char* buf, size_t cap) {
+    if (!b || i < 0) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] {
+        const std::vector<std::string> p = b->b.paths();
+        need((size_t)i < p.size(), "path index out of range");
+        copy_name(p[i], buf, cap);
+    });
+}
+
+extern "C" int32_t zjai_bundle_get(const zjai_bundle* b, const char* rel, const void** data, size_t* len) {
+    if (!b || !rel || !data || !len) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] {
+        const auto f = b->b.get(rel);
+        if (!f.first) throw Error(ZJAI_E_MODEL, std::string(rel) + ": not in the model bundle");
+        *data = f.first;
+        *len = f.second;
+    });
+}
+
+extern "C" int32_t zjai_bundle_notice(const zjai_bundle* b, char* buf, size_t cap, size_t* len) {
+    if (!b) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] {
+        const std::string s = b->b.notice();
+        if (len) *len = s.size();
+        if (buf) copy_name(s, buf, cap);
+    });
+}
+
+extern "C" int32_t zjai_bundle_write(const char* const* paths, const void* const* files, const size_t* sizes,
+                                     int32_t n, const char* notice, int32_t f16, void* out, size_t cap, size_t* len) {
+    if (!len || n < 0 || (n && (!paths || !files || !sizes))) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] {
+        std::vector<std::pair<std::string, std::vector<uint8_t>>> fs;
+        for (int32_t i = 0; i < n; ++i) {
+            need(paths[i] != nullptr && (files[i] != nullptr || sizes[i] == 0), "null file");
+            const uint8_t* p = (const uint8_t*)files[i];
+            fs.push_back({paths[i], std::vector<uint8_t>(p, p + sizes[i])});
+        }
+        const std::vector<uint8_t> f = write_bundle(fs, notice ? notice : "", f16 != 0);
+        *len = f.size();
+        if (!out) return;
+        if (cap < f.size()) throw Error(ZJAI_E_LIMIT, "output buffer too small");
+        std::memcpy(out, f.data(), f.size());
+    });
+}
+
+extern "C" int32_t zjai_net_create_from_checkpoint(zjai_ctx* ctx, int32_t op, int32_t component, int32_t precision,
+                                                   const zjai_checkpoint* ck, zjai_net** out) {
+    if (!ctx || !ck || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(precision >= DT_F32 && precision <= DT_BF16, "precision");
+        std::vector<std::vector<float>> hold;
+        *out = new zjai_net{build_net(ctx->c, op, component, precision, checkpoint_params(*ck->ck, hold))};
+    });
+}
+
+extern "C" int32_t zjai_latent_model_create_from_checkpoint(zjai_ctx* ctx, int32_t component, int32_t precision,
+                                                            const zjai_checkpoint* ck, zjai_net** out) {
+    if (!ctx || !ck || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(precision >= DT_F32 && precision <= DT_BF16, "precision");
+        std::vector<std::vector<float>> hold;
+        *out = new zjai_net{build_latent_net(ctx->c, component, precision, checkpoint_params(*ck->ck, hold))};
     });
 }

@@ -12,17 +12,11 @@
 #include <vector>
 
 #include "conv.h"
+#include "error.h"
 #include "ops.h"
 #include "../../include/zjai_hip.h"
 
 namespace zjai {
-
-// Error carrying one of the ZJAI_E_* status codes across the C++ internals; the C-ABI catches
-// it and returns the code (no exception crosses the ABI).
-struct Error : std::runtime_error {
-    int code;
-    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
-};
 
 #define ZJAI_HIP(call)                                                                        \
     do {                                                                                      \

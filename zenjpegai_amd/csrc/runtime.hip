@@ -1,6 +1,7 @@
 // Host runtime: device pool, tensors, weight packing and conv launches.
 
 #include "runtime.h"
+#include "checkpoint.h"
 
 #include <cmath>
 #include <cstring>
@@ -163,36 +164,6 @@ TensorP channel_view(const TensorP& t, int c0, int n) {
 }
 
 // ------------------------------------------------------------------------ weight conversion
-// f32 -> f16 bits, round to nearest even, the reference's integer algorithm
-// (src/weights/f16.rs:12-53).
-static uint16_t f32_to_f16_bits(float v) {
-    uint32_t b;
-    std::memcpy(&b, &v, 4);
-    const uint16_t sign = (uint16_t)((b >> 16) & 0x8000);
-    const int exp = (int)((b >> 23) & 0xff);
-    const uint32_t mant = b & 0x007fffff;
-    if (exp == 255) {
-        uint16_t payload = (uint16_t)((mant >> 13) | 0x200);
-        return (uint16_t)(sign | 0x7c00 | (mant ? payload : 0));
-    }
-    const int e = exp - 127 + 15;
-    if (e >= 31) return (uint16_t)(sign | 0x7c00);
-    if (e <= 0) {
-        if (e < -10) return sign;
-        const uint32_t m = mant | 0x00800000;
-        const uint32_t shift = (uint32_t)(14 - e);
-        const uint32_t dropped = m & ((1u << shift) - 1);
-        const uint32_t half = 1u << (shift - 1);
-        uint32_t r = m >> shift;
-        if (dropped > half || (dropped == half && (r & 1))) r += 1;
-        return (uint16_t)(sign | r);
-    }
-    const uint32_t dropped = mant & 0x1fff;
-    uint32_t r = mant >> 13;
-    if (dropped > 0x1000 || (dropped == 0x1000 && (r & 1))) r += 1;
-    return (uint16_t)(sign | (((uint32_t)e << 10) + r));
-}
-
 // f32 -> bf16 bits, round to nearest even (NaN kept quiet).
 static uint16_t f32_to_bf16_bits(float v) {
     uint32_t b;

@@ -11,6 +11,7 @@ import numpy as np
 from . import _lib
 from ._lib import HipError, check, lib
 from .nn import BTensor, Engine, _f32, _fp
+from .weights import Checkpoint
 
 
 def _descriptors(params: dict):
@@ -31,9 +32,13 @@ def _descriptors(params: dict):
     return n, c_names, c_ndims, c_dims, c_ptrs, keep
 
 
-def _net_create(eng: Engine, op: str, component: int, params: dict):
-    n, c_names, c_ndims, c_dims, c_ptrs, _keep = _descriptors(params)
+def _net_create(eng: Engine, op: str, component: int, params):
     h = ctypes.c_void_p()
+    if isinstance(params, Checkpoint):
+        check(lib().zjai_net_create_from_checkpoint(eng.handle, _lib.OPS[op], component, eng.dtype,
+                                                    params.handle, ctypes.byref(h)), eng.handle)
+        return h
+    n, c_names, c_ndims, c_dims, c_ptrs, _keep = _descriptors(params)
     check(lib().zjai_net_create(eng.handle, _lib.OPS[op], component, eng.dtype, n, c_names,
                                 c_ndims, c_dims, c_ptrs, ctypes.byref(h)), eng.handle)
     return h
@@ -50,7 +55,7 @@ class _Net:
     @classmethod
     def load(cls, params: dict, op: str, eng: Engine):
         """``SynthesisPrimary::load(ck, op, eng)`` / ``SynthesisSecondary::load``: ``params``
-        maps checkpoint names to arrays."""
+        is a ``weights.Checkpoint`` or maps checkpoint names to arrays."""
         return cls(eng, params, op)
 
     def out_size(self, h: int, w: int):
@@ -275,10 +280,15 @@ class LatentModel:
     def __init__(self, eng: Engine, params: dict, component: int):
         self.eng = eng
         self.component = component
-        n, c_names, c_ndims, c_dims, c_ptrs, _keep = _descriptors(params)
         self._h = ctypes.c_void_p()
-        check(lib().zjai_latent_model_create(eng.handle, component, eng.dtype, n, c_names, c_ndims,
-                                             c_dims, c_ptrs, ctypes.byref(self._h)), eng.handle)
+        if isinstance(params, Checkpoint):
+            check(lib().zjai_latent_model_create_from_checkpoint(
+                eng.handle, component, eng.dtype, params.handle, ctypes.byref(self._h)), eng.handle)
+        else:
+            n, c_names, c_ndims, c_dims, c_ptrs, _keep = _descriptors(params)
+            check(lib().zjai_latent_model_create(eng.handle, component, eng.dtype, n, c_names,
+                                                 c_ndims, c_dims, c_ptrs, ctypes.byref(self._h)),
+                  eng.handle)
         c, ctx = ctypes.c_int32(), ctypes.c_int32()
         check(lib().zjai_latent_model_info(self._h, ctypes.byref(c), ctypes.byref(ctx)))
         self.channels, self.has_context = c.value, bool(ctx.value)
