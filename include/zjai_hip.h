@@ -424,6 +424,27 @@ ZJAI_API int32_t zjai_latent_model_create_from_checkpoint(zjai_ctx* ctx, int32_t
                                                           int32_t precision, const zjai_checkpoint* ck,
                                                           zjai_net** out);
 
+/* ------------------------------------------------------------------ analysis transforms */
+
+/* `AnalysisPrimary::load` / `AnalysisSecondary::load` (src/model/analysis.rs:230-240, :282-290):
+ * the encoder's picture -> latent transforms for op BOP or HOP (SOP has none:
+ * ZJAI_E_INVALID_ARGUMENT) and component 0 (luma) / 1 (chroma), from named checkpoint tensors
+ * ("conv1".."conv5", "act1".."act3", HOP's "TAM" and "cab") and the optional 1-D lists
+ * "clip_thres.E{k}{B|H}.MinList" / ".MaxList". Destroy with zjai_net_destroy. */
+ZJAI_API int32_t zjai_analysis_create(zjai_ctx* ctx, int32_t op, int32_t component, int32_t precision,
+                                      int32_t n_tensors, const char* const* names, const int32_t* ndims,
+                                      const int32_t* dims, const float* const* data, zjai_net** out);
+ZJAI_API int32_t zjai_analysis_create_from_checkpoint(zjai_ctx* ctx, int32_t op, int32_t component,
+                                                      int32_t precision, const zjai_checkpoint* ck,
+                                                      zjai_net** out);
+/* `forward_clip` (src/model/analysis.rs:248-270, :297-310): picture planes f32 [c][h][w] in
+ * [0, 255] on the host -- c = 1 (luma) or c = 12 (half the luma resolution: luma
+ * pixel-unshuffled by 2, then U and V likewise) -> latent f32 [160][ceil(h/16)][ceil(w/16)]
+ * (component 0) or [96][ceil(h/8)][ceil(w/8)] (component 1) on the host (synchronises).
+ * clip != 0 applies the clip_thres lists after each conv. */
+ZJAI_API int32_t zjai_analysis_forward(zjai_ctx* ctx, const zjai_net* net, const float* x, int32_t c,
+                                       int32_t h, int32_t w, int32_t clip, float* y, size_t len);
+
 #ifdef __cplusplus
 }
 #endif

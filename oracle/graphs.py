@@ -374,3 +374,86 @@ def reconstruct_latent(p, ccs, height, width, regions, z_hat, residual, context=
         else:
             _assign(y_hat, lt, y, (0, 0))
     return psi, y_hat
+
+
+# ------------------------------------------------------------------------------ analysis
+# The encoder's analysis transforms (src/model/analysis.rs), composed of the pinned layers.
+
+def normalize(x):
+    """``normalize`` (src/model/analysis.rs:35-39): (x - 127.5) / 128 in f32."""
+    return ((x.astype(np.float32) - np.float32(127.5)) / np.float32(128.0)).astype(np.float32)
+
+
+def pad_amount(length, divider):
+    """``pad_amount`` (src/model/analysis.rs:43-46)."""
+    return 2 * _ceil(length, 2 * divider) - _ceil(length, divider)
+
+
+def replicate_pad(x, bottom, right):
+    """``replicate_pad`` (src/model/analysis.rs:48-70): F.pad(x, (0, right, 0, bottom),
+    mode="replicate")."""
+    if bottom == 0 and right == 0:
+        return x
+    return np.pad(x, ((0, 0), (0, bottom), (0, right)), mode="edge")
+
+
+def pad_for(x, h, w, divider):
+    """``pad_for`` (src/model/analysis.rs:72-81)."""
+    if x.shape[1:] != (_ceil(h, divider), _ceil(w, divider)):
+        raise ValueError("analysis transform: map size does not match the picture size")
+    return replicate_pad(x, pad_amount(h, divider), pad_amount(w, divider))
+
+
+def clip_channels(x, lo, hi):
+    """``clip_channels`` (src/model/load.rs:103-119): channel c < min(len(lo), len(hi)) clamped
+    to [lo[c], hi[c]]; NaN stays NaN."""
+    x = x.copy()
+    for c in range(min(len(lo), len(hi), x.shape[0])):
+        lo_c, hi_c = np.float32(lo[c]), np.float32(hi[c])
+        v = x[c]
+        v = np.where(v < lo_c, lo_c, v)
+        x[c] = np.where(v > hi_c, hi_c, v)
+    return x
+
+
+def _clip(p, op, stage, x, clip):
+    key = f"clip_thres.E{stage}{'H' if op == 'hop' else 'B'}"
+    if not clip or f"{key}.MinList" not in p or f"{key}.MaxList" not in p:
+        return x
+    return clip_channels(x, np.asarray(p[f"{key}.MinList"], np.float32).ravel(),
+                         np.asarray(p[f"{key}.MaxList"], np.float32).ravel())
+
+
+def _analysis_trunk(p, op, x, luma, clip):
+    """``Trunk::forward`` (src/model/analysis.rs:157-207)."""
+    _, h, w = x.shape
+    t = conv3x3(p, "conv1", pad_for(normalize(x), h, w, 1), stride=2)
+    t = res_au(p, "act1", _clip(p, op, 1, t, clip))
+    t = pad_for(t, h, w, 2)
+    if op == "hop":
+        t = tam(p, "TAM", t, luma)
+    t = res_au(p, "act2", _clip(p, op, 2, conv3x3(p, "conv2", t, stride=2), clip))
+    t = pad_for(t, h, w, 4)
+    if op == "hop":
+        t = cab(p, "cab", t)
+    return res_au(p, "act3", _clip(p, op, 3, conv3x3(p, "conv3", t, stride=2), clip))
+
+
+def analysis_primary(p, op, x, clip=False):
+    """``AnalysisPrimary::forward_clip`` (src/model/analysis.rs:248-270): [1, h, w] in [0, 255]
+    -> [160, ceil(h/16), ceil(w/16)]."""
+    if op not in ("bop", "hop"):
+        raise ValueError("there is no SOP analysis transform (use BOP)")
+    _, h, w = x.shape
+    t = pad_for(_analysis_trunk(p, op, x, True, clip), h, w, 8)
+    t = _clip(p, op, 4, conv3x3(p, "conv4", t, stride=2), clip)
+    return _clip(p, op, 5, conv1x1(p, "conv5", t), clip)
+
+
+def analysis_secondary(p, op, x, clip=False):
+    """``AnalysisSecondary::forward_clip`` (src/model/analysis.rs:297-310): [12, h, w] ->
+    [96, ceil(h/8), ceil(w/8)]."""
+    if op not in ("bop", "hop"):
+        raise ValueError("there is no SOP analysis transform (use BOP)")
+    t = _analysis_trunk(p, op, x, False, clip)
+    return _clip(p, op, 5, conv1x1(p, "conv5", t), clip)

@@ -160,6 +160,10 @@ PROTOTYPES = {
                           ctypes.c_char_p, _i32, _vp, _sz, ctypes.POINTER(_sz)],
     "zjai_net_create_from_checkpoint": [_vp, _i32, _i32, _i32, _vp, _pp],
     "zjai_latent_model_create_from_checkpoint": [_vp, _i32, _i32, _vp, _pp],
+    "zjai_analysis_create": [_vp, _i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_char_p), _i32p,
+                             _i32p, ctypes.POINTER(_f32p), _pp],
+    "zjai_analysis_create_from_checkpoint": [_vp, _i32, _i32, _i32, _vp, _pp],
+    "zjai_analysis_forward": [_vp, _vp, _f32p, _i32, _i32, _i32, _i32, _f32p, _sz],
 }
 
 _lib = None

@@ -1009,7 +1009,7 @@ const CkTensor& tensor_of(const zjai_checkpoint* ck, const char* name) {
 // Every f32 / f16 tensor of a checkpoint as named f32 parameters; `hold` owns the data.
 std::map<std::string, Param> checkpoint_params(const Checkpoint& ck, std::vector<std::vector<float>>& hold) {
     std::map<std::string, Param> P;
-    hold.reserve(ck.tensors().size());
+    hold.reserve(ck.tensors().size() + ck.lists().size());
     for (const CkTensor& t : ck.tensors()) {
         if (t.dtype != CK_F32 && t.dtype != CK_F16) continue;
         if (P.count(t.name)) continue;  // the first of duplicate names, as a by-name lookup finds
@@ -1021,6 +1021,15 @@ std::map<std::string, Param> checkpoint_params(const Checkpoint& ck, std::vector
         hold.push_back(ck.f32(t));
         p.data = hold.back().data();
         P[t.name] = p;
+    }
+    // numeric lists (`clip_thres.E1B.MinList`, ...) as 1-D f32 parameters (`x as f32`)
+    for (const auto& l : ck.lists()) {
+        if (P.count(l.first)) continue;
+        Param p;
+        p.shape = {(int)l.second.size()};
+        hold.emplace_back(l.second.begin(), l.second.end());
+        p.data = hold.back().data();
+        P[l.first] = p;
     }
     return P;
 }
@@ -1212,5 +1221,57 @@ extern "C" int32_t zjai_latent_model_create_from_checkpoint(zjai_ctx* ctx, int32
         need(precision >= DT_F32 && precision <= DT_BF16, "precision");
         std::vector<std::vector<float>> hold;
         *out = new zjai_net{build_latent_net(ctx->c, component, precision, checkpoint_params(*ck->ck, hold))};
+    });
+}
+
+// ------------------------------------------------------------------ analysis transforms
+extern "C" int32_t zjai_analysis_create(zjai_ctx* ctx, int32_t op, int32_t component, int32_t precision,
+                                        int32_t n_tensors, const char* const* names, const int32_t* ndims,
+                                        const int32_t* dims, const float* const* data, zjai_net** out) {
+    if (!ctx || !out || n_tensors < 0 || (n_tensors && (!names || !ndims || !dims || !data)))
+        return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(precision >= DT_F32 && precision <= DT_BF16, "precision");
+        *out = new zjai_net{
+            build_analysis_net(ctx->c, op, component, precision, params_of(n_tensors, names, ndims, dims, data))};
+    });
+}
+
+extern "C" int32_t zjai_analysis_create_from_checkpoint(zjai_ctx* ctx, int32_t op, int32_t component,
+                                                        int32_t precision, const zjai_checkpoint* ck,
+                                                        zjai_net** out) {
+    if (!ctx || !ck || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(precision >= DT_F32 && precision <= DT_BF16, "precision");
+        std::vector<std::vector<float>> hold;
+        *out = new zjai_net{build_analysis_net(ctx->c, op, component, precision, checkpoint_params(*ck->ck, hold))};
+    });
+}
+
+extern "C" int32_t zjai_analysis_forward(zjai_ctx* ctx, const zjai_net* net, const float* x, int32_t c, int32_t h,
+                                         int32_t w, int32_t clip, float* y, size_t len) {
+    if (!ctx || !net || !x || !y) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        const Net& m = *net->n;
+        need(m.kind == NET_ANALYSIS, "not an analysis transform");
+        need(c == m.in_ch, "analysis transform: input planes (1 luma, 12 chroma)");
+        need(h > 0 && w > 0, "analysis transform: empty picture");
+        const int d = m.comp == COMP_Y ? 16 : 8;
+        const size_t yn = (size_t)m.chs * ceil_div(h, d) * ceil_div(w, d);
+        need(len >= yn, "output buffer too small");
+        Context& cx = ctx->c;
+        const size_t xn = (size_t)c * h * w;
+        float* xdev = (float*)cx.pool.alloc(xn * 4);
+        std::shared_ptr<void> keep(xdev, [&cx](void* q) { cx.pool.release(q); });
+        ZJAI_HIP(hipMemcpyAsync(xdev, x, xn * 4, hipMemcpyHostToDevice, cx.stream));
+        TensorP t = analysis_forward(cx, m, xdev, h, w, clip != 0);
+        float* dev = (float*)cx.pool.alloc(yn * 4);
+        std::shared_ptr<void> keep2(dev, [&cx](void* q) { cx.pool.release(q); });
+        {
+            LaunchScope sc(cx, kname("k_nhwc_to_planar", m.dtype), 0.0, (4.0 + dtype_size(m.dtype)) * yn);
+            ZJAI_HIP(launch_nhwc_to_planar(t->v, m.dtype, 1, m.chs, t->h, t->w, dev, cx.stream));
+        }
+        ZJAI_HIP(hipMemcpyAsync(y, dev, yn * 4, hipMemcpyDeviceToHost, cx.stream));
+        ZJAI_HIP(hipStreamSynchronize(cx.stream));
     });
 }

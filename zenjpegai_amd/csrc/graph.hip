@@ -113,6 +113,40 @@ struct Builder {
         conv(p + ".ffn.dwconv", 2 * hidden, 2 * hidden, 3, 3, 1, 1, 2 * hidden, false);
         conv1x1(p + ".ffn.project_out", hidden, dim, false);
     }
+    // A 3x3 stride-2 conv over picture planes: input channels padded to a multiple of 8 with
+    // zero weights (the kernels read whole 16-byte channel vectors; the padded input channels
+    // are zeros too, so the extra products are exact zeros).
+    void conv_s2_planes(const std::string& pfx, int cin, int cout) {
+        const Param& w = get(pfx + ".weight", {cout, cin, 3, 3});
+        const float* b = bias(pfx, cout, true);
+        const int cp = round_up(cin, 8);
+        std::vector<float> wp((size_t)cout * cp * 9, 0.0f);
+        for (int o = 0; o < cout; ++o)
+            for (int i = 0; i < cin; ++i)
+                for (int k = 0; k < 9; ++k) wp[((size_t)o * cp + i) * 9 + k] = w.data[((size_t)o * cin + i) * 9 + k];
+        net.L[pfx] = make_conv(ctx, cp, cout, 3, 3, 2, 1, 1, 1, wp.data(), b, nullptr, net.dtype, false);
+    }
+    // `clip_bounds` (src/model/load.rs:94-101): optional [lo, hi] lists; the first n channels
+    // (the shorter list, at most the map's channels) are clipped.
+    void clip_bounds(const std::string& key, int stage, int chs) {
+        auto lo = P.find(key + ".MinList"), hi = P.find(key + ".MaxList");
+        if (lo == P.end() || hi == P.end()) return;
+        auto numel = [](const Param& q) {
+            long long n = 1;
+            for (int d : q.shape) n *= d;
+            return n;
+        };
+        const int n = (int)std::min<long long>({numel(lo->second), numel(hi->second), (long long)chs});
+        if (n <= 0) return;
+        if (!lo->second.data || !hi->second.data) throw Error(ZJAI_E_MODEL, key + ": no data");
+        for (auto* q : {&lo, &hi}) {
+            float* d = nullptr;
+            ZJAI_HIP(hipMalloc(&d, sizeof(float) * n));
+            ZJAI_HIP(hipMemcpy(d, (*q)->second.data, sizeof(float) * n, hipMemcpyHostToDevice));
+            net.vec[(*q)->first] = d;
+        }
+        net.clip_n[stage] = n;
+    }
     void tam(const std::string& pfx, int dim, bool ds) {
         if (ds) {
             conv(pfx + ".ds_conv", dim, dim, 3, 3, 2, 1, 1, true);
@@ -214,6 +248,45 @@ NetP build_latent_net(Context& ctx, int comp, int dtype, const std::map<std::str
             b.conv1x1(p + ".fusion_pred_net.conv2", c, c, false);
             b.conv1x1(p + ".fusion_pred_net.conv3", c, c, false);
         }
+    }
+    return net;
+}
+
+NetP build_analysis_net(Context& ctx, int op, int comp, int dtype, const std::map<std::string, Param>& params) {
+    if (comp < COMP_Y || comp > COMP_UV) throw Error(ZJAI_E_INVALID_ARGUMENT, "analysis transform: unknown component");
+    // check_op (src/model/analysis.rs:209-217)
+    if (op == OP_SOP) throw Error(ZJAI_E_INVALID_ARGUMENT, "there is no SOP analysis transform (use BOP)");
+    if (op != OP_BOP && op != OP_HOP) throw Error(ZJAI_E_INVALID_ARGUMENT, "analysis transform: unknown operating point");
+    auto net = std::make_shared<Net>();
+    net->kind = NET_ANALYSIS;
+    net->op = op;
+    net->comp = comp;
+    net->dtype = dtype;
+    net->chs = comp == COMP_Y ? 160 : 96;  // LATENT_CHANNELS (src/header.rs:31)
+    net->in_ch = comp == COMP_Y ? 1 : 12;
+    const int C = 128;  // hidden width (src/model/analysis.rs:32)
+    const bool hop = op == OP_HOP;
+    Builder b{ctx, *net, params};
+    // Trunk::load (src/model/analysis.rs:122-153)
+    b.conv_s2_planes("conv1", net->in_ch, C);
+    b.res_au("act1", C);
+    if (hop) b.tam("TAM", C, comp == COMP_Y);
+    b.conv("conv2", C, C, 3, 3, 2, 1, 1, true);
+    b.res_au("act2", C);
+    if (hop) b.cab("cab", C);
+    b.conv("conv3", C, C, 3, 3, 2, 1, 1, true);
+    b.res_au("act3", C);
+    if (comp == COMP_Y) {
+        b.conv("conv4", C, net->chs, 3, 3, 2, 1, 1, true);
+        b.conv1x1("conv5", net->chs, net->chs, false);
+    } else {
+        b.conv1x1("conv5", C, net->chs, false);
+    }
+    // clip_key (src/model/analysis.rs:111-119): clip_thres.E{stage}{B|H}
+    for (int k = 1; k <= 5; ++k) {
+        if (k == 4 && comp != COMP_Y) continue;
+        const int chs = k <= 3 ? C : net->chs;
+        b.clip_bounds("clip_thres.E" + std::to_string(k) + (hop ? "H" : "B"), k, chs);
     }
     return net;
 }
@@ -589,6 +662,70 @@ TensorP hyper_decoder_forward(Context& ctx, const Net& net, const TensorP& z, in
     x = f.conv("hyper_decoder.conv3", x, e);
     ctx.check_stop();
     return f.conv("hyper_decoder.conv4", x, e);
+}
+
+TensorP analysis_forward(Context& ctx, const Net& net, const float* x, int h, int w, bool clip) {
+    if (net.kind != NET_ANALYSIS) throw Error(ZJAI_E_INVALID_ARGUMENT, "not an analysis transform");
+    if (h <= 0 || w <= 0) throw Error(ZJAI_E_INVALID_ARGUMENT, "analysis transform: empty picture");
+    const int dt = net.dtype;
+    const double es = dtype_size(dt);
+    Fwd f{ctx, net};
+    // pad_amount (src/model/analysis.rs:43-46): one row / column when the map is odd.
+    auto pad_amount = [](int len, int d) { return 2 * ceil_div(len, 2 * d) - ceil_div(len, d); };
+    // pad_for (src/model/analysis.rs:72-81)
+    auto pad_for = [&](const TensorP& t, int d) -> TensorP {
+        if (t->h != ceil_div(h, d) || t->w != ceil_div(w, d))
+            throw Error(ZJAI_E_INVALID_ARGUMENT, "analysis transform: map size does not match the picture size");
+        const int ph = pad_amount(h, d), pw = pad_amount(w, d);
+        if (!ph && !pw) return t;
+        TensorP o = ctx.alloc(t->n, t->c, t->h + ph, t->w + pw, dt);
+        LaunchScope sc(ctx, kname("k_replicate_pad", dt), 0.0, 2.0 * es * o->n * o->c * o->h * o->w);
+        ZJAI_HIP(launch_replicate_pad(t->v, dt, t->n, t->c, t->h, t->w, o->v, o->h, o->w, ctx.stream));
+        return o;
+    };
+    // feature clipping after conv k (src/model/analysis.rs:169-203, :258-266)
+    auto clip_after = [&](const TensorP& t, int k) {
+        if (!clip || !net.clip_n[k]) return;
+        const std::string key = std::string("clip_thres.E") + std::to_string(k) + (net.op == OP_HOP ? "H" : "B");
+        LaunchScope sc(ctx, kname("k_clip_channels", dt), 0.0, 2.0 * es * t->n * net.clip_n[k] * t->h * t->w);
+        ZJAI_HIP(launch_clip_channels(t->v, dt, t->n, t->c, t->h, t->w, net.clip_n[k], net.vec.at(key + ".MinList"),
+                                      net.vec.at(key + ".MaxList"), ctx.stream));
+    };
+    // normalize + the first padding_layer, channels padded to the first conv's input width
+    const int cp = round_up(net.in_ch, 8);
+    TensorP in = ctx.alloc(1, cp, h + pad_amount(h, 1), w + pad_amount(w, 1), dt);
+    {
+        LaunchScope sc(ctx, kname("k_normalize_pad", dt), 0.0,
+                       4.0 * net.in_ch * h * w + es * cp * in->h * in->w);
+        ZJAI_HIP(launch_normalize_pad(x, net.in_ch, h, w, cp, in->h, in->w, in->v, dt, ctx.stream));
+    }
+    // Trunk::forward (src/model/analysis.rs:157-207)
+    TensorP t = f.conv("conv1", in);
+    in.reset();
+    clip_after(t, 1);
+    t = f.res_au("act1", t);
+    ctx.check_stop();
+    t = pad_for(t, 2);
+    if (net.op == OP_HOP) t = f.tam("TAM", t, net.comp == COMP_Y);
+    t = f.conv("conv2", t);
+    clip_after(t, 2);
+    t = f.res_au("act2", t);
+    ctx.check_stop();
+    t = pad_for(t, 4);
+    if (net.op == OP_HOP) t = f.cab("cab", t);
+    t = f.conv("conv3", t);
+    clip_after(t, 3);
+    t = f.res_au("act3", t);
+    ctx.check_stop();
+    if (net.comp == COMP_Y) {
+        // AnalysisPrimary::forward_clip (src/model/analysis.rs:248-270)
+        t = pad_for(t, 8);
+        t = f.conv("conv4", t);
+        clip_after(t, 4);
+    }
+    t = f.conv("conv5", t);
+    clip_after(t, 5);
+    return t;
 }
 
 void latent_decompress(Context& ctx, const Net& net, const float* res, long long res_row, long long res_plane,

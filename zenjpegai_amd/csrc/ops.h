@@ -126,4 +126,14 @@ hipError_t launch_assign_from_nhwc(View src, int dtype, int C, int SH, int SW, i
 hipError_t launch_assign_planar(const float* src, int C, int SH, int SW, int oy, int ox, int h, int w, float* dst,
                                 int DH, int DW, int dy0, int dx0, hipStream_t s);
 
+// Analysis transforms (src/model/analysis.rs): normalised planar picture planes -> NHWC with the
+// first replicate padding (Cp >= C channels, zeros beyond C); replicate padding NHWC -> NHWC;
+// per-channel clipping of channels [0, n) in place.
+hipError_t launch_normalize_pad(const float* x, int C, int H, int W, int Cp, int OH, int OW, View dst, int dtype,
+                                hipStream_t s);
+hipError_t launch_replicate_pad(View src, int dtype, int N, int C, int H, int W, View dst, int OH, int OW,
+                                hipStream_t s);
+hipError_t launch_clip_channels(View x, int dtype, int N, int C, int H, int W, int n, const float* lo,
+                                const float* hi, hipStream_t s);
+
 }  // namespace zjai

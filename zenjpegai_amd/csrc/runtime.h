@@ -207,13 +207,15 @@ struct Param {
     const float* data;
 };
 
-enum NetKind : int { NET_SYNTHESIS = 0, NET_LATENT = 1 };
+enum NetKind : int { NET_SYNTHESIS = 0, NET_LATENT = 1, NET_ANALYSIS = 2 };
 
 struct Net {
     int kind = NET_SYNTHESIS;
     int op = 0, comp = 0, dtype = DT_F32;
     int chs = 0;           // latent nets: latent channels (160 luma, 96 chroma)
     bool context = false;  // latent nets: a multi-stage context model is present
+    int in_ch = 0;         // analysis nets: picture planes in (1 luma, 12 chroma)
+    int clip_n[6] = {};    // analysis nets: channels clipped after conv k (0: no clip_thres)
     std::map<std::string, LayerP> L;
     std::map<std::string, float*> vec;  // device f32 vectors (layer norm, temperature)
     ~Net();
@@ -246,6 +248,13 @@ TensorP hyper_decoder_forward(Context& ctx, const Net& net, const TensorP& z, in
 // ceil(H/2) x ceil(W/2) per item) -> y_hat planar f32 [N][C][H][W] on the device.
 void latent_decompress(Context& ctx, const Net& net, const float* res, long long res_row, long long res_plane,
                        const Windows& rwin, int H, int W, const TensorP& psi, float* y_hat);
+
+// ------------------------------------------------------------------- analysis transforms
+// `AnalysisPrimary::load` / `AnalysisSecondary::load` (src/model/analysis.rs:230-290), BOP or HOP.
+NetP build_analysis_net(Context& ctx, int op, int comp, int dtype, const std::map<std::string, Param>& params);
+// `forward_clip` (src/model/analysis.rs:157-207, :248-310): planar f32 picture planes on the
+// device ([in_ch][h][w] in [0, 255]) -> the latent (NHWC, chs channels, h / 16 or h / 8).
+TensorP analysis_forward(Context& ctx, const Net& net, const float* x, int h, int w, bool clip);
 
 // Region geometry (src/tools/regions.rs:47-150).
 enum RegionPlane : int { PLANE_LATENT = 0, PLANE_PSI = 1, PLANE_HYPER_LATENT = 2, PLANE_IMAGE = 3 };

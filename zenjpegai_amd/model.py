@@ -342,3 +342,56 @@ class LatentModel:
                 self._h = None
         except Exception:
             pass
+
+
+class _Analysis:
+    """``AnalysisPrimary`` / ``AnalysisSecondary`` (src/model/analysis.rs:219-311): picture
+    planes in [0, 255] -> the latent ``y``. ``op`` is bop or hop (there is no SOP analysis
+    transform)."""
+    component = 0
+
+    def __init__(self, eng: Engine, params, op: str):
+        self.eng = eng
+        self.op = op
+        self._h = ctypes.c_void_p()
+        if isinstance(params, Checkpoint):
+            check(lib().zjai_analysis_create_from_checkpoint(eng.handle, _lib.OPS[op], self.component,
+                                                             eng.dtype, params.handle,
+                                                             ctypes.byref(self._h)), eng.handle)
+        else:
+            n, c_names, c_ndims, c_dims, c_ptrs, _keep = _descriptors(params)
+            check(lib().zjai_analysis_create(eng.handle, _lib.OPS[op], self.component, eng.dtype, n,
+                                             c_names, c_ndims, c_dims, c_ptrs, ctypes.byref(self._h)),
+                  eng.handle)
+
+    @classmethod
+    def load(cls, params, op: str, eng: Engine):
+        """``AnalysisPrimary::load(ck, op, eng)``: ``params`` is a ``weights.Checkpoint`` or maps
+        checkpoint names to arrays."""
+        return cls(eng, params, op)
+
+    def forward(self, eng: Engine, x: np.ndarray, clip: bool = False) -> np.ndarray:
+        """``forward`` / ``forward_clip``: planar ``[c, h, w]`` -> ``[chs, h / d, w / d]``."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        c, h, w = x.shape
+        d, chs = (16, 160) if self.component == 0 else (8, 96)
+        out = np.empty((chs, -(-h // d), -(-w // d)), np.float32)
+        check(lib().zjai_analysis_forward(eng.handle, self._h, _fp(x), c, h, w, int(clip), _fp(out),
+                                          out.size), eng.handle)
+        return out
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib().zjai_net_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+
+class AnalysisPrimary(_Analysis):
+    component = 0
+
+
+class AnalysisSecondary(_Analysis):
+    component = 1

@@ -277,3 +277,58 @@ def hyper_latent(seed: int, name: str, c: int, h: int, w: int, b: float = 1.5) -
 def residual(seed: int, name: str, c: int, h: int, w: int, b: float = 0.5) -> np.ndarray:
     """A dequantised residual ``[c, h, w]``: continuous Laplace(0, b) samples."""
     return laplace(seed, name, (c, h, w), b)
+
+
+# ---------------------------------------------------------------------------------------------
+# Analysis transforms (encoder side, src/model/analysis.rs).
+# ---------------------------------------------------------------------------------------------
+
+ANALYSIS_HIDDEN = 128  # src/model/analysis.rs:32
+
+
+def analysis_param_specs(op: str, component: str):
+    """``[(name, shape, kind)]`` of ``AnalysisPrimary`` / ``AnalysisSecondary``
+    (src/model/analysis.rs:122-153, :230-290) for ``op`` in bop/hop; ResAU groups of 16
+    channels, as the synthesis ResAUs."""
+    c = ANALYSIS_HIDDEN
+    luma = component == "y"
+    t: list = []
+    _conv3(t, "conv1", 1 if luma else 12, c)
+    _res_au(t, "act1", c, c // 16)
+    if op == "hop":
+        _tam(t, "TAM", c, luma)
+    _conv3(t, "conv2", c, c)
+    _res_au(t, "act2", c, c // 16)
+    if op == "hop":
+        _cab(t, "cab", c)
+    _conv3(t, "conv3", c, c)
+    _res_au(t, "act3", c, c // 16)
+    if luma:
+        _conv3(t, "conv4", c, LATENT_CHANNELS[0])
+        _conv1(t, "conv5", LATENT_CHANNELS[0], LATENT_CHANNELS[0], False)
+    else:
+        _conv1(t, "conv5", c, LATENT_CHANNELS[1], False)
+    return t
+
+
+def random_analysis_params(op: str, component: str, seed: int = 1, gain: float = 1.0) -> dict:
+    """He-normal random-init parameters of one analysis transform, keyed by checkpoint name."""
+    params = {}
+    for name, shape, kind in analysis_param_specs(op, component):
+        tag = f"analysis/{op}/{component}/{name}"
+        if kind == "conv":
+            params[name] = normal(seed, tag, shape, gain * np.sqrt(2.0 / (shape[1] * shape[2] * shape[3])))
+        elif kind == "convt":
+            params[name] = normal(seed, tag, shape, gain * np.sqrt(2.0 / (shape[0] * (shape[2] / 2.0) ** 2)))
+        elif kind == "bias":
+            params[name] = normal(seed, tag, shape, 0.01)
+        elif kind == "ones":
+            params[name] = np.ones(shape, np.float32)
+        else:
+            params[name] = np.zeros(shape, np.float32)
+    return params
+
+
+def picture(seed: int, name: str, c: int, h: int, w: int) -> np.ndarray:
+    """Picture planes ``[c, h, w]`` in [0, 255] (uniform samples, whole numbers)."""
+    return np.floor(uniform(seed, name, (c, h, w), 0.0, 256.0)).clip(0, 255).astype(np.float32)
