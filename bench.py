@@ -188,6 +188,42 @@ def latent_stage_cpu(inputs):
     return out
 
 
+def analysis_stage(prec, reps=3):
+    """The encoder's analysis transforms (src/model/analysis.rs) on the config-5 picture: HOP
+    primary on the 3840x2160 luma plane and HOP secondary on the 12 half-resolution planes, one
+    ``zjai_analysis_forward`` call each. Reports the summed kernel time (HIP events, best of
+    ``reps``), the wall time (host transfers included), the algorithmic FLOPs and the picture's
+    Mpixel/s over the kernel time of both."""
+    from zenjpegai_amd import model, nn, synth
+    eng = nn.Engine(0, prec)
+    out, total = {}, 0.0
+    for comp, cls, planes, h, w in (("y", model.AnalysisPrimary, 1, 2160, 3840),
+                                    ("uv", model.AnalysisSecondary, 12, 1080, 1920)):
+        net = cls.load(synth.random_analysis_params("hop", comp, seed=1), "hop", eng)
+        x = synth.picture(1, f"cfg5/analysis/{comp}", planes, h, w)
+        net.forward(eng, x)
+        best_k, best_w, flops = None, None, 0.0
+        for _ in range(reps):
+            eng.profile_begin()
+            t0 = time.perf_counter()
+            net.forward(eng, x)
+            wall = (time.perf_counter() - t0) * 1e3
+            recs = eng.profile_end()
+            k = sum(r[3] for r in recs)
+            flops = sum(r[1] for r in recs)
+            best_k = k if best_k is None else min(best_k, k)
+            best_w = wall if best_w is None else min(best_w, wall)
+        out[f"{comp}_kernel_ms"] = round(best_k, 3)
+        out[f"{comp}_wall_ms"] = round(best_w, 3)
+        out[f"{comp}_gflop"] = round(flops / 1e9, 1)
+        out[f"{comp}_tflops"] = round(flops / (best_k / 1e3) / 1e12, 1)
+        total += best_k
+        del net
+    out["mpix_s"] = round(3840 * 2160 / (total / 1e3) / 1e6, 1)
+    eng.close()
+    return out
+
+
 def layer_configs(prec, reps=10):
     """BASELINE configs 1-3 as single-layer runs at their full sizes: kernel time per run (HIP
     events around each launch) and conv TFLOP/s (all taps counted)."""
@@ -395,6 +431,9 @@ def main():
             log(f"[bench] RGB output stage: {extra['rgb_output_stage_cfg5']}")
             extra["latent_reconstruction_cfg5"], latent_inputs = latent_stage(args.precision)
             log(f"[bench] latent reconstruction: {extra['latent_reconstruction_cfg5']}")
+            for prec in (args.precision, "bf16"):
+                extra[f"analysis_hop_cfg5_{prec}"] = analysis_stage(prec)
+                log(f"[bench] analysis transforms {prec}: {extra[f'analysis_hop_cfg5_{prec}']}")
         for prec in ("f32", "bf16"):
             extra.update(layer_configs(prec))
         log("[bench] configs 1-3: " + ", ".join(f"{k}={v}" for k, v in extra.items() if k.startswith("cfg") and "tflops" in k))
