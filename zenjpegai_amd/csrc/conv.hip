@@ -870,7 +870,12 @@ k_convT_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
     __shared__ float s_w[4 * 4 * CKN * COUT];
     const int gw = (p.OW + 1) / 2, gh = (p.OH + 1) / 2;
     const int gx = (gw + TXN - 1) / TXN, gy = (gh + TYN - 1) / TYN;
-    int bid = (int)blockIdx.x;
+    // XCD-aware order: workgroups go to the 8 XCDs round-robin, so workgroup q takes tile
+    // (q % 8) * (gridDim.x / 8) + q / 8 and each XCD runs one contiguous band of tile rows,
+    // whose shared halo rows then meet in its L2. The grid is a multiple of 8; extra
+    // workgroups exit (uniformly, before any barrier).
+    int bid = (int)((blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8);
+    if (bid >= gx * gy * p.N) return;
     const int tx = bid % gx;
     bid /= gx;
     const int ty = bid % gy, bi = bid / gy;
@@ -955,7 +960,7 @@ k_convT_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
 template <typename T>
 static hipError_t go_narrow(int coutp, const ConvParams& p, const float* wn, int cin, hipStream_t s) {
     const int gw = (p.OW + 1) / 2, gh = (p.OH + 1) / 2;
-    const long long blocks = (long long)((gw + 63) / 64) * ((gh + 3) / 4) * p.N;
+    const long long blocks = ((long long)((gw + 63) / 64) * ((gh + 3) / 4) * p.N + 7) / 8 * 8;
     if (blocks <= 0 || blocks > (1ll << 30) || p.N < 1 || p.N > MAXB) return hipErrorInvalidValue;
     const dim3 g((unsigned)blocks);
     switch (coutp) {

@@ -167,7 +167,12 @@ __global__ void __launch_bounds__(256) k_depthwise3x3(View src, View dst, int N,
     const int cout = gated ? elu_half : C;
     const int nvec = (cout + V - 1) / V, vpw = gated ? 32 : 64, nvw = (nvec + vpw - 1) / vpw;
     const int lane = threadIdx.x & 63;
-    const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    // XCD-aware order: the hardware deals workgroups to the 8 XCDs round-robin, so workgroup p
+    // takes logical block (p % 8) * (gridDim.x / 8) + p / 8 and each XCD works through one
+    // contiguous run of column groups, whose overlapping input columns then meet in its L2.
+    const long long nb8 = gridDim.x / 8;
+    const long long blk = (blockIdx.x % 8) * nb8 + blockIdx.x / 8;
+    const long long wave = (blk * blockDim.x + threadIdx.x) >> 6;
     const int gx = (w + X - 1) / X, gr = (h + DW_R - 1) / DW_R;
     if (wave >= (long long)N * gr * gx * nvw) return;  // whole waves only
     const int cw = (int)(wave % nvw);
@@ -505,7 +510,8 @@ hipError_t launch_depthwise3x3(View src, View dst, int dtype, int N, int C, int 
     const long long waves = (long long)N * ((h + DW_R - 1) / DW_R) * ((w + X - 1) / X) *
                             (((cout + V - 1) / V + vpw - 1) / vpw);
     if (waves == 0) return hipSuccess;
-    const long long blocks = (waves + 3) / 4;
+    // a multiple of 8 workgroups for the kernel's XCD-aware block order (the extra ones exit)
+    const long long blocks = ((waves + 3) / 4 + 7) / 8 * 8;
     if (blocks > (1ll << 31) - 1) return hipErrorInvalidValue;
     ZJAI_DISPATCH(dtype, k_depthwise3x3, <<<dim3((unsigned)blocks), 256, 0, s>>>(src, dst, N, C, h, w, weight, bias, elu_half))
     return hipGetLastError();
