@@ -346,8 +346,8 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only; the synthesis tiles would shard "
-              "across GPUs with no collective (see DESIGN.md), but no multi-GPU figure is "
-              "produced.", file=sys.stderr)
+              "across GPUs with no collective (each GPU runs whole tiles and writes its core "
+              "rectangles), but no multi-GPU figure is produced.", file=sys.stderr)
         sys.exit(2)
 
     from zenjpegai_amd import nn
