@@ -165,6 +165,21 @@ def test_pickle_globals_are_never_called():
     assert ck.tensor_names() == [] and ck.ints() == [("epoch", 7)]
 
 
+def test_deeply_nested_and_cyclic_pickles_parse_without_recursion():
+    """Values live in an arena: a list nested 400k deep (MARK x n, LIST x n) and a list that
+    contains itself (via the memo) neither overflow the stack nor leak when released."""
+    n = 400_000
+    nested = b"\x80\x02}q\x00X\x01\x00\x00\x00a" + b"(" * n + b"l" * n + b"sX\x05\x00\x00\x00epochK\x03s."
+    cyclic = b"\x80\x02}q\x00X\x01\x00\x00\x00b]q\x01h\x01as."
+    for pkl in (nested, cyclic):
+        out = io.BytesIO()
+        with zipfile.ZipFile(out, "w") as z:
+            z.writestr("a/data.pkl", pkl)
+        ck = Checkpoint.parse(out.getvalue())
+        assert ck.tensor_names() == []
+    assert ck.ints() == []
+
+
 def test_pickle_rejects_unknown_opcodes_and_truncation():
     for pkl in (b"\x80\x02}q\x00Z.", b"\x80\x02}q\x00(X\xff\xff\xff\x7f", b"\x80\x02(t", b"\x80\x09}."):
         out = io.BytesIO()
