@@ -327,6 +327,12 @@ __global__ void __launch_bounds__(256) k_layer_norm(View src, View dst, int N, i
 // MFMA (M = q channels, N = k channels, K = 4 positions per instruction); the chunk partials
 // are reduced in f64 by the softmax kernel.
 constexpr int ATT_POS = 256;
+// Position groups loaded per trip of the Gram loop: 4 for f32 (68 -> 52 us on config 5's TAM
+// maps); the 16-bit loads measured slower batched (58 -> 65 us) and keep one group per trip.
+template <typename T>
+constexpr int att_u() {
+    return sizeof(T) == 4 ? 4 : 1;
+}
 
 int attention_gram_chunks(int h, int w) { return (h * w + ATT_POS - 1) / ATT_POS; }
 
@@ -348,27 +354,39 @@ __global__ void __launch_bounds__(256) k_attention_gram(View qkv, int dim, int h
             dq[a] = dk[a] = z;
             g[a][0] = g[a][1] = z;
         }
-        for (int p = p0; p < p1; p += 4) {
-            const int pos = p + kq;
-            float aq[2] = {0.0f, 0.0f}, ak[2] = {0.0f, 0.0f};
-            if (pos < p1) {
-                const int y = pos / w, x = pos - y * w;
-                const T* px = base + (long long)y * qkv.row + (long long)x * qkv.cs + hd * c + m;
+        // ATT_U groups of 4 positions per trip: all their loads issue before the first MFMA, so
+        // the loads of a trip overlap; the MFMAs then run group by group in position order.
+        constexpr int ATT_U = att_u<T>();
+        for (int p = p0; p < p1; p += 4 * ATT_U) {
+            float aq[ATT_U][2], ak[ATT_U][2];
 #pragma unroll
-                for (int bb = 0; bb < 2; ++bb)
-                    if (bb * 16 + m < c) {
-                        aq[bb] = to_f32(px[bb * 16]);
-                        ak[bb] = to_f32(px[dim + bb * 16]);
-                    }
+            for (int u = 0; u < ATT_U; ++u) {
+                aq[u][0] = aq[u][1] = ak[u][0] = ak[u][1] = 0.0f;
+                const int pos = p + 4 * u + kq;
+                if (pos < p1) {
+                    const int y = pos / w, x = pos - y * w;
+                    const T* px = base + (long long)y * qkv.row + (long long)x * qkv.cs + hd * c + m;
+#pragma unroll
+                    for (int bb = 0; bb < 2; ++bb)
+                        if (bb * 16 + m < c) {
+                            aq[u][bb] = to_f32(px[bb * 16]);
+                            ak[u][bb] = to_f32(px[dim + bb * 16]);
+                        }
+                }
             }
 #pragma unroll
-            for (int bi = 0; bi < 2; ++bi) {
-                if (bi >= nb) continue;
+            for (int u = 0; u < ATT_U; ++u) {
+                if (p + 4 * u >= p1) break;  // uniform: the groups of the one-position-at-a-time loop
 #pragma unroll
-                for (int bj = 0; bj < 2; ++bj)
-                    if (bj < nb) g[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[bi], ak[bj], g[bi][bj], 0, 0, 0);
-                dq[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[bi], aq[bi], dq[bi], 0, 0, 0);
-                dk[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(ak[bi], ak[bi], dk[bi], 0, 0, 0);
+                for (int bi = 0; bi < 2; ++bi) {
+                    if (bi >= nb) continue;
+#pragma unroll
+                    for (int bj = 0; bj < 2; ++bj)
+                        if (bj < nb)
+                            g[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[u][bi], ak[u][bj], g[bi][bj], 0, 0, 0);
+                    dq[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[u][bi], aq[u][bi], dq[bi], 0, 0, 0);
+                    dk[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(ak[u][bi], ak[u][bi], dk[bi], 0, 0, 0);
+                }
             }
         }
         // Lane l holds D[4 * (l / 16) + i][l % 16] of each 16x16 tile.
