@@ -410,26 +410,49 @@ __global__ void __launch_bounds__(256) k_attention_gram(View qkv, int dim, int h
     }
 }
 
-// One wave per attention row (item b, head hd, query i): reduce the chunk partials in f64,
+// One workgroup per attention row (item b, head hd, query i): reduce the chunk partials in f64,
 // normalise (F.normalize, eps 1e-12), scale by the temperature, softmax with the Cephes exp and
 // an f64 sum in index order (src/nn/fast/math.rs:558-577).
-__global__ void __launch_bounds__(64) k_attention_softmax(const float* partial, int nchunk, int dim,
-                                                          int heads, const float* temperature,
-                                                          float* attn) {
+__global__ void __launch_bounds__(256) k_attention_softmax(const float* partial, int nchunk, int dim,
+                                                           int heads, const float* temperature,
+                                                           float* attn) {
+    // The chunk sums run in ATT_SL slices of 32 lanes (slice t takes chunks t, t + ATT_SL, ...,
+    // in order), then the slices are added in slice order: a fixed order, so the result does not
+    // depend on scheduling, and ATT_SL times the loads in flight of a single 32-lane pass.
+    constexpr int ATT_SL = 8;
+    __shared__ double s_red[ATT_SL][2][32];
+    __shared__ double s_rq[ATT_SL];
     __shared__ double s_qq;
     __shared__ float s_e[64];
     const int row = blockIdx.x, b = blockIdx.y, c = dim / heads, hd = row / c, i = row - hd * c;
-    const int E = c * c + 2 * c, lane = threadIdx.x;
+    const int E = c * c + 2 * c, tid = threadIdx.x, sl = tid >> 5, j = tid & 31;
     double sqk = 0.0, skk = 0.0, sqq = 0.0;
-    if (lane < c) {
-        for (int k = 0; k < nchunk; ++k) {
+    if (j < c) {
+        for (int k = sl; k < nchunk; k += ATT_SL) {
             const float* pb = partial + (((long long)b * nchunk + k) * heads + hd) * E;
-            sqk += (double)pb[i * c + lane];
-            skk += (double)pb[c * c + c + lane];
-            if (lane == 0) sqq += (double)pb[c * c + i];
+            sqk += (double)pb[i * c + j];
+            skk += (double)pb[c * c + c + j];
+            if (j == 0) sqq += (double)pb[c * c + i];
         }
     }
-    if (lane == 0) s_qq = sqq;
+    s_red[sl][0][j] = sqk;
+    s_red[sl][1][j] = skk;
+    if (j == 0) s_rq[sl] = sqq;
+    __syncthreads();
+    const int lane = tid;  // the rest runs on threads 0..63 (columns j < c)
+    sqk = 0.0;
+    skk = 0.0;
+    if (lane < c) {
+        for (int t = 0; t < ATT_SL; ++t) {
+            sqk += s_red[t][0][lane];
+            skk += s_red[t][1][lane];
+        }
+    }
+    if (lane == 0) {
+        double q = 0.0;
+        for (int t = 0; t < ATT_SL; ++t) q += s_rq[t];
+        s_qq = q;
+    }
     __syncthreads();
     float nq = (float)sqrt(s_qq);
     nq = nq > 1e-12f ? nq : 1e-12f;
@@ -439,15 +462,15 @@ __global__ void __launch_bounds__(64) k_attention_softmax(const float* partial, 
         nk = nk > 1e-12f ? nk : 1e-12f;
         a = (float)(sqk / ((double)nq * (double)nk)) * temperature[hd];
     }
-    s_e[lane] = a;
+    if (lane < 64) s_e[lane] = a;
     __syncthreads();
     float mx = -INFINITY;
-    for (int j = 0; j < c; ++j) mx = fmaxf(mx, s_e[j]);
+    for (int jj = 0; jj < c; ++jj) mx = fmaxf(mx, s_e[jj]);
     __syncthreads();
     if (lane < c) s_e[lane] = cephes_exp(a - mx);
     __syncthreads();
     double sum = 0.0;
-    for (int j = 0; j < c; ++j) sum += (double)s_e[j];
+    for (int jj = 0; jj < c; ++jj) sum += (double)s_e[jj];
     if (lane < c) attn[((long long)b * dim + row) * c + lane] = s_e[lane] / (float)sum;
 }
 
@@ -560,8 +583,8 @@ hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads,
 
 hipError_t launch_attention_softmax(const float* partial, int N, int nchunk, int dim, int heads,
                                     const float* temperature, float* attn, hipStream_t s) {
-    if (dim / heads > 64) return hipErrorInvalidValue;
-    k_attention_softmax<<<dim3(dim, N), 64, 0, s>>>(partial, nchunk, dim, heads, temperature, attn);
+    if (heads <= 0 || dim % heads || dim / heads > 32) return hipErrorInvalidValue;
+    k_attention_softmax<<<dim3(dim, N), 256, 0, s>>>(partial, nchunk, dim, heads, temperature, attn);
     return hipGetLastError();
 }
 
