@@ -208,12 +208,13 @@ def secondary(p, op, y_hat_luma, y_hat_chroma, h, w, denorm=True):
 
 
 def synthesize(py, puv, op, y_hat, uv_hat, height, width, tiles, sv=1, sh=1, out_h=None,
-               out_w=None):
+               out_w=None, denorm=True):
     """``synthesize_luma_into`` + ``synthesize_chroma_into`` (src/decoder/reconstruct.rs:379-464):
     per tile, window the latents, run the nets, copy tile cores into the planes (chroma keeps the
     rows/cols at multiples of ``sv``/``sh``). ``tiles`` are ``geometry.SynthesisTile``.
     Returns ``(rec_y [out_h, out_w], rec_u, rec_v [ceil(out_h/sv), ceil(out_w/sw)])`` float32;
-    ``puv`` None skips chroma."""
+    ``puv`` None skips chroma. ``denorm=False`` keeps the nets' values before ``denormalize``
+    (which is elementwise, so ``denormalize`` of these planes gives the default result)."""
     out_h = height if out_h is None else out_h
     out_w = width if out_w is None else out_w
     rec_y = np.zeros((out_h, out_w), np.float32)
@@ -224,14 +225,14 @@ def synthesize(py, puv, op, y_hat, uv_hat, height, width, tiles, sv=1, sh=1, out
         img, lat, core = t.image, t.latent, t.core
         ox, oy = t.core_offset
         by = np.ascontiguousarray(y_hat[:, lat.y:lat.y + lat.height, lat.x:lat.x + lat.width])
-        ty = primary(py, op, by, img.height, img.width)[0]
+        ty = primary(py, op, by, img.height, img.width, denorm)[0]
         rows = min(core.height, max(out_h - core.y, 0))
         cols = min(core.width, max(out_w - core.x, 0))
         rec_y[core.y:core.y + rows, core.x:core.x + cols] = ty[oy:oy + rows, ox:ox + cols]
         if puv is None:
             continue
         buv = np.ascontiguousarray(uv_hat[:, lat.y:lat.y + lat.height, lat.x:lat.x + lat.width])
-        tuv = secondary(puv, op, by, buv, img.height, img.width)
+        tuv = secondary(puv, op, by, buv, img.height, img.width, denorm)
         for c, dst in enumerate((rec_u, rec_v)):
             y0 = _ceil(core.y, sv) * sv
             x0 = _ceil(core.x, sh) * sh

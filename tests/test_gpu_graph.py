@@ -233,22 +233,32 @@ def test_picture_10bit_and_float(engines):
         assert float(np.max(np.abs(g - wv))) <= 0.05
 
 
-def test_config4_sop_1mp_untiled_8bit(engines):
+@pytest.mark.parametrize("gain", [1.0, 0.5])
+def test_config4_sop_1mp_untiled_8bit(engines, gain):
     """BASELINE config 4 at full size: latent 1x160x64x64 round(Laplace(0,1.5)), SOP luma with
-    He-normal weights, 1024x1024 output quantised to 8 bit, untiled."""
+    He-normal weights, 1024x1024 output quantised to 8 bit, untiled. He x 0.5: the north-star
+    gate (one step, 0.05 %). He gain 1 (the BASELINE spec): every sample saturates and the
+    oracle disagrees with itself by up to ~20 steps when its weights move by one ulp
+    (test_conditioning.py); the GPU is held to the 0.05 % fraction and to 3x that spread."""
+    from test_conditioning import nudge
     eng = engines["f32"]
-    p = synth.random_params("sop", "y", seed=4)
+    p = synth.random_params("sop", "y", seed=4, gain=gain)
     y = synth.latent(4, "cfg4/y", 160, 64, 64)
     tiles = model.synthesis_tiles(1024, 1024, 64, 64, None)
     got, _, _ = model.synthesize(eng, model.SynthesisPrimary.load(p, "sop", eng), None, y, None,
                                  1024, 1024, tiles, bit_depth=8)
-    ref = og.primary(p, "sop", y, 1024, 1024)[0]
-    want = oracle.quantize_plane(ref, 8)
+    with og.fast_convs():
+        want = oracle.quantize_plane(og.primary(p, "sop", y, 1024, 1024)[0], 8)
+        spread = oracle.quantize_plane(og.primary(nudge(p), "sop", y, 1024, 1024)[0], 8)
     d = np.abs(got.astype(np.int32) - want.astype(np.int32))
-    scale = float(np.max(np.abs(og.primary(p, "sop", y, 1024, 1024, denorm=False))))
-    # He-normal weights: the conditioning bound in 8-bit steps (see the module docstring).
-    assert d.max() <= max(1, int(np.ceil(2e-5 * scale * 128))), (int(d.max()), scale)
-    assert np.count_nonzero(d) <= 5e-4 * d.size, int(np.count_nonzero(d))
+    ds = np.abs(spread.astype(np.int32) - want.astype(np.int32))
+    print(f"config 4 He gain {gain}: GPU vs oracle max step {int(d.max())}, "
+          f"{np.count_nonzero(d)} of {d.size} differ; oracle vs oracle(+-1 ulp weights) max step "
+          f"{int(ds.max())}, {np.count_nonzero(ds)} differ")
+    if gain < 1.0:
+        assert d.max() <= 1 and np.count_nonzero(d) <= 5e-4 * d.size
+    else:
+        assert np.count_nonzero(d) <= max(5e-4 * d.size, 3 * np.count_nonzero(ds))
 
 
 def test_repeated_runs_are_bit_identical(engines):
@@ -276,3 +286,20 @@ def test_cancellation_between_layers(engines):
         eng.set_stop(False)
     eng.sync()
     assert net.forward(eng, t, 64, 64).shape == (1, 64, 64)
+
+
+def test_picture_rejects_a_tile_latent_window_that_is_not_its_image_size(engines):
+    """A tile's latent window must be ceil(image / 16) (latent_extent, src/tools/tiles.rs:22-24):
+    tiles of one image size are batched, and a batch reads every item with the first one's
+    window size."""
+    eng = engines["f32"]
+    op, h, w = "sop", 256, 384
+    lh, lw = h // 16, w // 16
+    tiles = model.synthesis_tiles(h, w, lh, lw, (128, 32))
+    t = tiles[0]
+    bad = model.SynthesisTile(t.image, model.Area(t.latent.x, t.latent.y, t.latent.width - 1,
+                                                  t.latent.height), t.core, t.core_offset)
+    prim = model.SynthesisPrimary.load(synth.random_params(op, "y", seed=2, gain=0.5), op, eng)
+    with pytest.raises(model.HipError) as e:
+        model.Picture(eng, prim, None, lh, lw, h, w, [bad] + tiles[1:])
+    assert e.value.kind == "InvalidArgument"

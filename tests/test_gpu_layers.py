@@ -107,16 +107,19 @@ def _he(name, shape, fan_in, seed=11):
 
 @pytest.mark.parametrize("prec", ["f32", "f16", "bf16"])
 def test_config1_conv3x3_128(engines, prec):
-    """BASELINE config 1 (Conv2d 3x3 s1 p1 128->128, U[-1,1] input, He weights, N(0,0.01)
-    bias) on a 64x64 crop of its input size."""
+    """BASELINE config 1 at full size (Conv2d 3x3 s1 p1 128->128 on 1x128x256x256, U[-1,1]
+    input, He weights, N(0,0.01) bias); the oracle runs on the nn::fast restatement, which is
+    bit-identical to the reference loops."""
     eng = engines[prec]
-    x = synth.uniform(1, "cfg1/x", (128, 64, 64), -1, 1)
+    x = synth.uniform(1, "cfg1/x", (128, 256, 256), -1, 1)
     w = _he("cfg1/w", (128, 128, 3, 3), 1152)
     b = synth.normal(1, "cfg1/b", (128,), 0.01)
     y = nn.ConvLayer(nn.Conv2d(128, 128, (3, 3), 1, (1, 1), 1, w, b), eng).forward(
         eng, nn.BTensor.from_planar(eng, x)).to_planar()
-    want = oracle.conv2d(x, w, b, 1, (1, 1))
-    assert rel_err(y, want) <= TOL[prec]
+    want = oracle.conv2d(x, w, b, 1, (1, 1), fast=True)
+    err = rel_err(y, want)
+    print(f"config 1 {prec}: max |gpu - oracle| / max|oracle| = {err:.2e}")
+    assert err <= TOL[prec]
 
 
 @pytest.mark.parametrize("prec", ["f32", "bf16"])
@@ -135,10 +138,10 @@ def test_config2_convt4_leaky(engines, prec):
 
 
 def config3_oracle(x, p):
-    t = oracle.conv2d(x, p["c1w"], p["c1b"], 1, (1, 1))
+    t = oracle.conv2d(x, p["c1w"], p["c1b"], 1, (1, 1), fast=True)
     t = oracle.leaky_relu(t)
-    t = oracle.add(oracle.conv2d(t, p["c2w"], p["c2b"], 1, (1, 1)), x)
-    g = oracle.sigmoid(oracle.conv2d(x, p["gw"], p["gb"], 1, (0, 0)))
+    t = oracle.add(oracle.conv2d(t, p["c2w"], p["c2b"], 1, (1, 1), fast=True), x)
+    g = oracle.sigmoid(oracle.conv2d(x, p["gw"], p["gb"], 1, (0, 0), fast=True))
     return oracle.mul(t, g)
 
 
@@ -164,13 +167,15 @@ def config3_gpu(eng, x, p):
 
 @pytest.mark.parametrize("prec", ["f32", "bf16"])
 def test_config3_residual_sigmoid_gated_block(engines, prec):
-    """BASELINE config 3 (t = conv3x3(leaky(conv3x3(x))) + x; out = t * sigmoid(conv1x1(x)))
-    at 192 channels on a 48x48 crop."""
+    """BASELINE config 3 at full size (t = conv3x3(leaky(conv3x3(x))) + x;
+    out = t * sigmoid(conv1x1(x)), 192 channels, 1x192x128x128, U[-2,2] input)."""
     eng = engines[prec]
-    x = synth.uniform(3, "cfg3/x", (192, 48, 48), -2, 2)
+    x = synth.uniform(3, "cfg3/x", (192, 128, 128), -2, 2)
     p = config3_params()
     y = config3_gpu(eng, x, p).to_planar()
-    assert rel_err(y, config3_oracle(x, p)) <= TOL[prec] * 3
+    err = rel_err(y, config3_oracle(x, p))
+    print(f"config 3 {prec}: max |gpu - oracle| / max|oracle| = {err:.2e}")
+    assert err <= TOL[prec] * 3
 
 
 def test_fused_epilogues_match_op_sequences(engines):

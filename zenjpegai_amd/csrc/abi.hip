@@ -2,6 +2,8 @@
 // driver. No exception or abort crosses this boundary.
 
 #include <algorithm>
+#include <array>
+#include <map>
 #include <cstring>
 #include <mutex>
 
@@ -669,6 +671,9 @@ extern "C" int32_t zjai_picture_create(zjai_ctx* ctx, const zjai_net* net_y, con
                      t.latent_x + t.latent_w <= lw && t.latent_y + t.latent_h <= lh,
                  "tile latent window outside the latent");
             need(t.image_w > 0 && t.image_h > 0 && t.core_w > 0 && t.core_h > 0, "tile sizes");
+            // latent_extent (src/tools/tiles.rs:22-24): a tile's latent window is ceil(len / 16).
+            need(t.latent_h == ceil_div(t.image_h, 16) && t.latent_w == ceil_div(t.image_w, 16),
+                 "tile latent window is not ceil(image size / 16)");
             int oh, ow;
             primary_out_size(p->net_y->op, t.image_h, t.image_w, &oh, &ow);
             need(t.core_off_y >= 0 && t.core_off_x >= 0 && t.core_off_y + t.core_h <= oh &&
@@ -676,8 +681,12 @@ extern "C" int32_t zjai_picture_create(zjai_ctx* ctx, const zjai_net* net_y, con
                  "synthesis tile smaller than its core");
             need(t.core_x >= 0 && t.core_y >= 0, "tile core position");
         }
-        std::map<std::pair<int, int>, std::vector<int>> by_size;
-        for (int i = 0; i < n_tiles; ++i) by_size[{p->tiles[i].image_h, p->tiles[i].image_w}].push_back(i);
+        // One batch shares every layer shape: key on the image and the latent window size.
+        std::map<std::array<int, 4>, std::vector<int>> by_size;
+        for (int i = 0; i < n_tiles; ++i) {
+            const zjai_tile& t = p->tiles[i];
+            by_size[{t.image_h, t.image_w, t.latent_h, t.latent_w}].push_back(i);
+        }
         for (auto& kv : by_size)
             for (size_t i = 0; i < kv.second.size(); i += MAXB)
                 p->batches.emplace_back(kv.second.begin() + i,

@@ -503,7 +503,9 @@ static inline dim3 grid_for(long long n) { return dim3((unsigned)((n + 255) / 25
 
 hipError_t launch_planar_to_nhwc(const float* src, int C, int LH, int LW, const Windows& win, int N,
                                  int h, int w, View dst, int dtype, hipStream_t s) {
-    if (N < 1 || N > MAXB) return hipErrorInvalidValue;
+    if (C % 4 || N < 1 || N > MAXB) return hipErrorInvalidValue;
+    for (int b = 0; b < N; ++b)
+        if (win.y0[b] < 0 || win.x0[b] < 0 || win.y0[b] + h > LH || win.x0[b] + w > LW) return hipErrorInvalidValue;
     const long long n = (long long)N * h * w * (C / 4);
     if (n == 0) return hipSuccess;
     ZJAI_DISPATCH(dtype, k_planar_to_nhwc, <<<grid_for(n), 256, 0, s>>>(src, C, LH, LW, win, N, h, w, dst))
