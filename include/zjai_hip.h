@@ -195,6 +195,22 @@ ZJAI_API int32_t zjai_layer_norm_channels(zjai_ctx* ctx, const zjai_tensor* x, c
 /* `math::channel_attention` (src/nn/fast/math.rs:512): qkv [3*dim] channels -> [dim]. */
 ZJAI_API int32_t zjai_channel_attention(zjai_ctx* ctx, const zjai_tensor* qkv, int32_t heads,
                                const float* temperature, zjai_tensor** out);
+/* Allocation-free channel attention. It has no counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same result as zjai_channel_attention, bit for bit. qkv and
+ * out are caller-owned device buffers, 16-byte aligned, NHWC dense in `precision`: qkv
+ * [h][w][channels] (channels = 3 * dim: q, k, v), out [h][w][dim]; temperature is a device array
+ * of `heads` floats. The work is enqueued on the context's stream (zjai_sync waits for it) and
+ * allocates nothing: its scratch (Gram partial sums, attention matrix, folded weight) is one
+ * static device array of ZJAI_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends and
+ * shared by every call on that GPU, so calls that overlap on one GPU (contexts on different
+ * streams) race. A map that needs more scratch (with dim 128 and 4 heads: more than ~240k
+ * positions) returns ZJAI_E_LIMIT before anything is launched. */
+#define ZJAI_NOALLOC_SCRATCH_BYTES (16u << 20)
+ZJAI_API int32_t zjai_channel_attention_noalloc(zjai_ctx* ctx, const void* qkv, int32_t channels,
+                                                int32_t h, int32_t w, int32_t heads,
+                                                const float* temperature, int32_t precision,
+                                                void* out);
 
 /* ------------------------------------------------------------------------ synthesis nets */
 

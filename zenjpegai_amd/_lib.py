@@ -108,6 +108,7 @@ PROTOTYPES = {
     "zjai_pixel_shuffle": [_vp, _vp, _i32, _pp],
     "zjai_layer_norm_channels": [_vp, _vp, _f32p, _f32p, _pp],
     "zjai_channel_attention": [_vp, _vp, _i32, _f32p, _pp],
+    "zjai_channel_attention_noalloc": [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _i32, _vp],
     "zjai_net_create": [_vp, _i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_char_p), _i32p,
                         _i32p, ctypes.POINTER(_f32p), _pp],
     "zjai_net_destroy": [_vp],

@@ -75,6 +75,38 @@ TensorP planar_upload(Context& c, const float* data, int ch, int h, int w, int d
 
 }  // namespace
 
+// ---------------------------------------------------------------- allocation-free scratch
+// Scratch of zjai_channel_attention_noalloc: each GPU holds its own copy of this array until the
+// process ends. In host code `scratch` is a host-side stand-in, not device memory: the array's
+// address on a device comes from hipGetSymbolAddress (scratch_setup, called by zjai_ctx_create
+// with that device current) and only that address is passed to kernels.
+static __device__ __align__(256) unsigned char scratch[ZJAI_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int SCRATCH_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[SCRATCH_DEVICES] = {};
+
+void scratch_setup(int device) {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (device < 0 || device >= SCRATCH_DEVICES) throw Error(ZJAI_E_UNSUPPORTED, "device index beyond the scratch table");
+    if (g_scratch_dev[device]) return;
+    void* p = nullptr;
+    ZJAI_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) throw Error(ZJAI_E_DEVICE, "hipGetSymbolAddress: no address for the scratch array");
+    g_scratch_dev[device] = p;
+}
+
+unsigned char* scratch_of(int device) {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    return device >= 0 && device < SCRATCH_DEVICES ? (unsigned char*)g_scratch_dev[device] : nullptr;
+}
+
+size_t round_up256(size_t n) { return (n + 255) / 256 * 256; }
+
+}  // namespace
+
 // ------------------------------------------------------------------------------- context
 extern "C" int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out) {
     if (!out) return ZJAI_E_INVALID_ARGUMENT;
@@ -94,6 +126,7 @@ extern "C" int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** ou
         if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
             throw Error(ZJAI_E_UNSUPPORTED, std::string("kernels are built for gfx950, device is ") + prop.gcnArchName);
         ZJAI_HIP(hipSetDevice(device));
+        scratch_setup(device);
         ctx->c.device = device;
         ctx->c.flags = flags;
         ZJAI_HIP(hipStreamCreateWithFlags(&ctx->c.stream, hipStreamNonBlocking));
@@ -408,6 +441,85 @@ extern "C" int32_t zjai_channel_attention(zjai_ctx* ctx, const zjai_tensor* qkv,
         TensorP y = conv_forward(ctx->c, *L, channel_view(qkv->t, 2 * dim, dim), e);
         ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
         *out = new zjai_tensor{y};
+    });
+}
+
+extern "C" int32_t zjai_channel_attention_noalloc(zjai_ctx* ctx, const void* qkv, int32_t channels,
+                                                  int32_t h, int32_t w, int32_t heads,
+                                                  const float* temperature, int32_t precision,
+                                                  void* out) {
+    if (!ctx || !qkv || !temperature || !out) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(precision >= DT_F32 && precision <= DT_BF16, "precision");
+        need(h > 0 && w > 0, "attention: empty map");
+        need(heads > 0 && channels > 0 && channels % (3 * heads) == 0, "attention: channel / head counts");
+        const int dim = channels / 3, c = dim / heads;
+        need(dim % 8 == 0, "attention: dim must be a multiple of 8");
+        need(c >= 1 && c <= 32, "attention: at most 32 channels per head");
+        need((((uintptr_t)qkv | (uintptr_t)out) & 15) == 0 && ((uintptr_t)temperature & 3) == 0,
+             "attention: buffers not aligned (16 bytes; temperature 4)");
+        // The dim x dim 1x1 projection (the identity) the attention is folded into, in the
+        // packing make_conv gives it: [chunk][nblk][16][CK] of the storage type.
+        const int es = dtype_size(precision), CK = 64 / es;
+        const TileCfg cfg = conv_tile_cfg(dim, CK_1x1, precision);
+        const int nblk = round_up(ceil_div(dim, 16), cfg.wc * cfg.cf), nchunks = ceil_div(dim, CK);
+        const size_t w_bytes = (size_t)nchunks * nblk * 16 * CK * es;
+        // Scratch layout: Gram partials [nchunk][heads][c*c + 2c] f32 | attn [dim][c] f32 | weight.
+        const int nchunk = attention_gram_chunks(h, w);
+        const size_t part_bytes = (size_t)nchunk * heads * (c * c + 2 * c) * 4;
+        const size_t attn_off = round_up256(part_bytes), w_off = round_up256(attn_off + (size_t)dim * c * 4);
+        if (w_off + w_bytes > ZJAI_NOALLOC_SCRATCH_BYTES)
+            throw Error(ZJAI_E_LIMIT, "attention: the map needs more than the allocation-free scratch");
+        unsigned char* base = scratch_of(ctx->c.device);
+        if (!base) throw Error(ZJAI_E_DEVICE, "allocation-free scratch not set up for this device");
+        float* partial = (float*)base;
+        float* attn = (float*)(base + attn_off);
+        void* wfold = base + w_off;
+        Context& C = ctx->c;
+        const View vq{const_cast<void*>(qkv), (long long)w * channels, (long long)h * w * channels, channels, 0};
+        // Padded rows / columns of the folded weight must read zero, and the scratch keeps the
+        // last call's contents.
+        if (nblk * 16 != dim || nchunks * CK != dim) {
+            LaunchScope sc(C, "k_zero_u32", 0.0, (double)w_bytes);
+            ZJAI_HIP(launch_zero(wfold, w_bytes, C.stream));
+        }
+        const double n = (double)h * w, total = (double)heads * (c * c + 2 * c);
+        {
+            LaunchScope sc(C, kname("k_attention_gram", precision), 2.0 * total * n, es * 2.0 * dim * n + 4.0 * nchunk * total);
+            ZJAI_HIP(launch_attention_gram(vq, precision, 1, dim, heads, h, w, partial, C.stream));
+        }
+        {
+            LaunchScope sc(C, "k_attention_softmax", 0.0, 4.0 * nchunk * total);
+            ZJAI_HIP(launch_attention_softmax(partial, 1, nchunk, dim, heads, temperature, attn, C.stream));
+        }
+        {
+            LaunchScope sc(C, kname("k_attention_fold", precision), 2.0 * dim * dim * c, 4.0 * dim * c + (double)w_bytes);
+            ZJAI_HIP(launch_attention_fold(nullptr, attn, 1, dim, heads, precision, nblk, wfold,
+                                           (long long)(w_bytes / es), C.stream));
+        }
+        // attn . v: the folded weight as a 1x1 conv over the v channels (conv_forward's launch).
+        ConvParams p{};
+        p.x = View{const_cast<void*>(qkv), (long long)w * channels, (long long)h * w * channels, channels, 2 * dim};
+        p.H = h;
+        p.W = w;
+        p.N = 1;
+        p.OH = h;
+        p.OW = w;
+        p.y = View{out, (long long)w * dim, (long long)h * w * dim, dim, 0};
+        p.w = wfold;
+        p.w_bstride = (long long)(w_bytes / es);
+        p.bias = nullptr;
+        p.cin_g = dim;
+        p.cout_g = dim;
+        p.groups = 1;
+        p.nchunks = nchunks;
+        p.nblk_g = nblk;
+        p.ntiles = nblk / (cfg.wc * cfg.cf);
+        p.ps = 1;
+        p.out_mode = OUT_NHWC;
+        p.sv = p.sh = 1;
+        LaunchScope sc(C, conv_kernel_name(CK_1x1, precision, cfg), 2.0 * n * dim * dim, es * 2.0 * n * dim + (double)w_bytes);
+        ZJAI_HIP(launch_conv(CK_1x1, precision, cfg, p, C.stream));
     });
 }
 

@@ -105,6 +105,8 @@ hipError_t launch_attention_softmax(const float* partial, int N, int nchunk, int
 hipError_t launch_attention_fold(const float* proj, const float* attn, int N, int dim, int heads,
                                  int dtype, int nblk, void* wpk, long long w_bstride,
                                  hipStream_t s);
+// Zero `bytes` (a multiple of 4, 4-byte aligned) at p with a kernel.
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
 
 // Latent reconstruction (src/decoder/reconstruct.rs:81-234), N regions of one shape per launch:
 // int8 planar z_hat windows (per item origin) -> NHWC view of the storage type;

@@ -476,7 +476,8 @@ __global__ void __launch_bounds__(256) k_attention_softmax(const float* partial,
 
 // Folds the output projection into the attention: wfold[o][hd*c + j] =
 // sum_i proj[o][hd*c + i] * attn[hd*c + i][j] (f64 accumulate), stored straight into the packed
-// 1x1 conv layout [chunk][nblk][16][CK] of the storage type, one weight per batch item.
+// 1x1 conv layout [chunk][nblk][16][CK] of the storage type, one weight per batch item. A null
+// proj is the identity (the same products, 1 or 0 times attn).
 template <typename T>
 __global__ void k_attention_fold(const float* proj, const float* attn, int dim, int heads, int nblk,
                                  int CK, T* wpk, long long w_bstride) {
@@ -485,13 +486,31 @@ __global__ void k_attention_fold(const float* proj, const float* attn, int dim, 
     const int c = dim / heads, o = e / dim, col = e - o * dim, hd = col / c, j = col - hd * c;
     const float* at_b = attn + (long long)b * dim * c;
     double s = 0.0;
-    for (int i = 0; i < c; ++i) s += (double)proj[o * dim + hd * c + i] * (double)at_b[(hd * c + i) * c + j];
+    for (int i = 0; i < c; ++i) {
+        const float pw = proj ? proj[o * dim + hd * c + i] : (o == hd * c + i ? 1.0f : 0.0f);
+        s += (double)pw * (double)at_b[(hd * c + i) * c + j];
+    }
     const int ch = col / CK, kk = col - ch * CK;
     wpk[(long long)b * w_bstride + (((long long)ch * nblk + o / 16) * 16 + o % 16) * CK + kk] = from_f32<T>((float)s);
 }
 
+// Zero fill with vector stores (instead of hipMemsetAsync, which callers capturing the stream
+// into a HIP graph cannot rely on).
+__global__ void k_zero_u32(uint32_t* p, long long n) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
 // ------------------------------------------------------------------------------- launchers
 static inline dim3 grid_for(long long n) { return dim3((unsigned)((n + 255) / 256)); }
+
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s) {
+    if (bytes % 4 || ((uintptr_t)p & 3)) return hipErrorInvalidValue;
+    const long long n = (long long)(bytes / 4);
+    if (n == 0) return hipSuccess;
+    k_zero_u32<<<grid_for(n), 256, 0, s>>>((uint32_t*)p, n);
+    return hipGetLastError();
+}
 
 #define ZJAI_DISPATCH(dtype, KERNEL, ...)                                                     \
     switch (dtype) {                                                                         \

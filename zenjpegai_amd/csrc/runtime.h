@@ -152,6 +152,9 @@ struct Layer {
 };
 using LayerP = std::shared_ptr<Layer>;
 
+// Tile shape the implicit-GEMM kernels use for a layer with cout_g outputs per group.
+TileCfg conv_tile_cfg(int cout_g, int kind, int dtype);
+
 LayerP make_conv(Context& ctx, int cin, int cout, int kh, int kw, int stride, int pad_h,
                  int pad_w, int groups, const float* weight, const float* bias,
                  const int extra[4], int dtype, bool keep_f32);

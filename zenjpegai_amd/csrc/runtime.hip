@@ -250,7 +250,7 @@ void Layer::out_size(int h, int w, int* oh, int* ow) const {
 // 3x3 layers take the 8-wave 64-channel x 16-row tile (two waves per SIMD from one workgroup hide
 // each other's LDS and barrier waits: +2-3 % on the config-5 picture in every precision); fp32
 // 1x1 layers with >= 256 outputs the 8-wave 128-channel x 8-row tile (+2 % in fp32).
-static TileCfg pick_cfg(int cout_g, int kind, int dtype) {
+TileCfg conv_tile_cfg(int cout_g, int kind, int dtype) {
     if (cout_g <= 16) return TileCfg{1, 4, 1, 2};
     if (cout_g <= 32) return TileCfg{1, 4, 2, 2};
     if (kind == CK_3x3) return TileCfg{2, 4, 2, 4};
@@ -293,7 +293,7 @@ LayerP make_conv(Context& ctx, int cin, int cout, int kh, int kw, int stride, in
     else throw Error(ZJAI_E_UNSUPPORTED, "conv2d: kernel geometry without a HIP kernel");
     const int vec = 16 / dtype_size(dtype);
     if (cin_g % vec) throw Error(ZJAI_E_UNSUPPORTED, "conv2d: channels per group not vector aligned");
-    L->cfg = pick_cfg(cout_g, L->kind, dtype);
+    L->cfg = conv_tile_cfg(cout_g, L->kind, dtype);
     const int NB = L->cfg.wc * L->cfg.cf;
     const int CK = 64 / dtype_size(dtype);
     const int T = kh * kw;
@@ -356,7 +356,7 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
     }
     const int vec = 16 / dtype_size(dtype);
     if (cin % vec) throw Error(ZJAI_E_UNSUPPORTED, "conv_transpose2d: channels not vector aligned");
-    L->cfg = pick_cfg(cout, CK_T3, dtype);
+    L->cfg = conv_tile_cfg(cout, CK_T3, dtype);
     const int NB = L->cfg.wc * L->cfg.cf;
     const int CK = 64 / dtype_size(dtype);
     L->nblk_g = round_up(ceil_div(cout, 16), NB);
