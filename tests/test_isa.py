@@ -8,7 +8,9 @@ Why: on MI355X an MFMA chain that renames its accumulator back to back -- ``v_mf
 states for it. In-place chains (destination = srcC) are fine back to back, and renamed chains
 six or more instructions apart (the fused transformer kernels have such) pass the GPU
 bit-identity tests. Register pressure in a kernel variant is what makes the compiler rename, so
-this guard runs on every build of every kernel."""
+this guard runs on every build of every kernel. The threshold is the smallest distance with GPU
+evidence (six): distances four and five are neither measured nor covered by a documented wait
+state, so they are rejected too."""
 
 import os
 import re
@@ -21,7 +23,7 @@ import pytest
 from zenjpegai_amd import _lib
 
 LLVM = "/opt/rocm/llvm/bin"
-MIN_RENAMED_DISTANCE = 4
+MIN_RENAMED_DISTANCE = 6
 MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
 TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 

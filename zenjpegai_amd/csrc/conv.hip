@@ -18,35 +18,14 @@
 // so the halo is the 3x3 one and only the tap table differs.
 
 #include "conv.h"
+#include "mfma.h"
 
 #include <type_traits>
 
 namespace zjai {
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-template <typename T> struct Mma;
-template <> struct Mma<float> {
-    static __device__ __forceinline__ void run(f32x4& acc, u32x4 a, u32x4 b) {
-        const f32x4 av = __builtin_bit_cast(f32x4, a), bv = __builtin_bit_cast(f32x4, b);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[0], bv[0], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[1], bv[1], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[2], bv[2], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[3], bv[3], acc, 0, 0, 0);
-    }
-};
-template <> struct Mma<_Float16> {
-    static __device__ __forceinline__ void run(f32x4& acc, u32x4 a, u32x4 b) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                     __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
-    }
-};
-template <> struct Mma<__bf16> {
-    static __device__ __forceinline__ void run(f32x4& acc, u32x4 a, u32x4 b) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                      __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
-    }
-};
+// The 16x16 fragment of mfma.h (Mma16): 4 x 16x16x4 f32 steps or one 16x16x32 16-bit step.
+template <typename T> using Mma = Mma16<T>;
 
 // clamp(v, 0, 6) on a 16-byte vector of the storage type (ResAU's relu6 on load).
 template <typename T> __device__ __forceinline__ u32x4 relu6_vec(u32x4 v);

@@ -410,9 +410,12 @@ __global__ void __launch_bounds__(256) k_attention_gram(View qkv, int dim, int h
     }
 }
 
-// One workgroup per attention row (item b, head hd, query i): reduce the chunk partials in f64,
-// normalise (F.normalize, eps 1e-12), scale by the temperature, softmax with the Cephes exp and
-// an f64 sum in index order (src/nn/fast/math.rs:558-577).
+// One workgroup per attention row (item b, head hd, query i): reduce the chunk partials in f64
+// (in the fixed slice order described below, not position order), then divide the raw q . k
+// dot by max(|q|, 1e-12) * max(|k|, 1e-12) -- the reference normalises q and k before the dot
+// (F.normalize, src/nn/fast/math.rs:538-545), so the two agree to rounding, not bit for bit --,
+// scale by the temperature and take the softmax with the Cephes exp and an f64 sum in index
+// order (math.rs:558-577).
 __global__ void __launch_bounds__(256) k_attention_softmax(const float* partial, int nchunk, int dim,
                                                            int heads, const float* temperature,
                                                            float* attn) {
