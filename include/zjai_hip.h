@@ -74,8 +74,8 @@ typedef struct zjai_picture zjai_picture;
 /* ------------------------------------------------------------------ context / diagnostics */
 
 /* Replaces `Engine` construction (src/nn/fast/mod.rs:128-172) for the HIP backend: binds a
- * device and creates its stream. flags: 0 or an OR of ZJAI_CTX_UNFUSED_BLOCKS and
- * ZJAI_CTX_PHASE_SPLIT_CONVT (other bits are rejected). */
+ * device and creates its stream. flags: 0 or an OR of ZJAI_CTX_UNFUSED_BLOCKS,
+ * ZJAI_CTX_PHASE_SPLIT_CONVT and ZJAI_CTX_MFMA16_CONV3X3 (other bits are rejected). */
 /* Run the transformer blocks (src/model/attention.rs:328-372) as the reference's separate ops --
  * layer norm, 1x1, depthwise (+ ELU gate), 1x1 -- instead of the fused kernels the 16-bit
  * precisions use by default for `prep_data` (LN + 1x1 + depthwise) and for the feed-forward half
@@ -85,6 +85,9 @@ typedef struct zjai_picture zjai_picture;
  * output phase per workgroup instead of all four phases per workgroup (same results bit for bit;
  * for A/B runs and the parity test that proves it). */
 #define ZJAI_CTX_PHASE_SPLIT_CONVT 0x2u
+/* Run the dense stride-1 3x3 convolutions of the 16-bit precisions on the 16x16x32 MFMA kernel
+ * instead of the 32x32x16 one (for A/B runs and the test that compares the two). */
+#define ZJAI_CTX_MFMA16_CONV3X3 0x4u
 ZJAI_API int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out);
 ZJAI_API int32_t zjai_ctx_destroy(zjai_ctx* ctx);
 /* Copies the last failure message (NUL-terminated, truncated to len). Works with ctx == NULL

@@ -26,6 +26,11 @@ def engines():
     return {p: nn.Engine(0, p) for p in ("f32", "f16", "bf16")}
 
 
+@pytest.fixture(scope="module")
+def igemm_engines():
+    return {p: nn.Engine(0, p, flags=_lib.CTX_MFMA16_CONV3X3) for p in ("f16", "bf16")}
+
+
 def rel_err(got, want):
     want = np.asarray(want, np.float64)
     return float(np.max(np.abs(np.asarray(got, np.float64) - want)) / max(np.max(np.abs(want)), 1e-30))
@@ -120,6 +125,53 @@ def test_config1_conv3x3_128(engines, prec):
     err = rel_err(y, want)
     print(f"config 1 {prec}: max |gpu - oracle| / max|oracle| = {err:.2e}")
     assert err <= TOL[prec]
+
+
+DENSE16_CASES = [  # cin, cout, h, w, fused epilogue (the first four take the 8-channel store)
+    (64, 64, 37, 53, "none"), (128, 128, 45, 70, "relu+add"), (128, 256, 33, 40, "leaky+gate"),
+    (64, 128, 20, 24, "mul"), (128, 128, 29, 31, "sigmoid*r"), (64, 64, 20, 24, "cab")]
+
+
+@pytest.mark.parametrize("prec", ["f16", "bf16"])
+@pytest.mark.parametrize("cin,cout,h,w,op", DENSE16_CASES)
+def test_dense_16bit_conv3x3_kernels_agree(engines, igemm_engines, prec, cin, cout, h, w, op):
+    """The two 16-bit dense 3x3 kernels (conv3x3_m32, 32x32x16 MFMA with the whole channel
+    halo resident, and conv_igemm, 16x16x32, chosen by ZJAI_CTX_MFMA16_CONV3X3) each meet the
+    oracle at the precision's tolerance for every fused epilogue, on ragged sizes; the profiler
+    names the kernel that ran."""
+    x = synth.normal(6, f"d16/x{cin}", (cin, h, w), 1.0)
+    r = synth.normal(6, f"d16/r{cout}", (cout, h, w), 1.0)
+    wt = _he(f"d16/w{cin}{cout}", (cout, cin, 3, 3), cin * 9)
+    b = synth.normal(6, f"d16/b{cout}", (cout,), 0.05)
+    base = oracle.conv2d(x, wt, b, 1, (1, 1), fast=True)
+    want, kw = {
+        "none": (lambda: base, {}),
+        "relu+add": (lambda: oracle.add(oracle.relu(base), r), dict(act=_lib.ACT_RELU, res=_lib.RES_ADD)),
+        "leaky+gate": (lambda: oracle.gate(r, oracle.leaky_relu(base)),
+                       dict(act=_lib.ACT_LEAKY_RELU, res=_lib.RES_GATE)),
+        "mul": (lambda: oracle.mul(r, base), dict(res=_lib.RES_MUL)),
+        "sigmoid*r": (lambda: oracle.mul(r, oracle.sigmoid(base)), dict(act=_lib.ACT_SIGMOID, res=_lib.RES_MUL)),
+        "cab": (lambda: oracle.add(oracle.mul(r, oracle.sigmoid(base)), x), dict(res=_lib.RES_CAB)),
+    }[op]
+    want = want()
+    got = {}
+    for flags, kernel in ((0, "conv3x3_m32"), (_lib.CTX_MFMA16_CONV3X3, "conv_igemm")):
+        eng = engines[prec] if flags == 0 else igemm_engines[prec]
+        layer = nn.ConvLayer(nn.Conv2d(cin, cout, (3, 3), 1, (1, 1), 1, wt, b), eng)
+        xt, rt = nn.BTensor.from_planar(eng, x), nn.BTensor.from_planar(eng, r)
+        if "res" in kw:
+            kw = dict(kw, r1=rt, r2=xt) if op == "cab" else dict(kw, r1=rt)
+        eng.sync()
+        eng.profile_begin()
+        y = layer.forward_fused(eng, xt, **kw)
+        names = [rec[0] for rec in eng.profile_end()]
+        assert any(n.startswith(kernel) for n in names), names
+        got[kernel] = y.to_planar()
+        err = rel_err(got[kernel], want)
+        print(f"{prec} {cin}->{cout} {h}x{w} {op} {kernel}: {err:.2e}")
+        assert err <= TOL[prec], (kernel, err)
+        kw = {k: v for k, v in kw.items() if k not in ("r1", "r2")}
+    assert rel_err(got["conv3x3_m32"], got["conv_igemm"]) <= TOL[prec]
 
 
 @pytest.mark.parametrize("prec", ["f32", "bf16"])

@@ -35,6 +35,7 @@ ACT_NONE, ACT_RELU, ACT_LEAKY_RELU, ACT_SIGMOID = 0, 1, 2, 3
 RES_NONE, RES_ADD, RES_GATE, RES_CAB, RES_MUL = 0, 1, 2, 3, 4
 CTX_UNFUSED_BLOCKS = 0x1  # zjai_ctx_create flags
 CTX_PHASE_SPLIT_CONVT = 0x2
+CTX_MFMA16_CONV3X3 = 0x4
 RESIZE_BICUBIC, RESIZE_BILINEAR = 0, 1
 PLANE_LATENT, PLANE_PSI, PLANE_HYPER_LATENT, PLANE_IMAGE = 0, 1, 2, 3
 

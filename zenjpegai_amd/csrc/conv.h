@@ -77,6 +77,13 @@ hipError_t launch_conv_tr_merged(int dtype, const ConvParams& p, hipStream_t s);
 constexpr int TR_MERGED_TAPS = 9;
 constexpr int TR_MERGED_NB = 4;
 
+// Dense stride-1 3x3 convolution in f16 / bf16 on 32x32x16 MFMAs (conv32.hip): mt (128 or 64)
+// output channels x 256 positions per workgroup, tiles tw (32 or 16) columns wide; p.w is the
+// packing [cin / 16][cout / mt][9][2][mt][8] of the storage type, p.cin_g 64 or 128,
+// groups 1, NHWC output without pixel shuffle, no relu6 on load.
+hipError_t launch_conv3x3_m32(int dtype, int mt, int tw, const ConvParams& p, hipStream_t s);
+int conv3x3_m32_width(int OH, int OW);
+
 // Stride-2 transposed conv with cout <= 8 on the vector ALUs (coutp = cout rounded up to 1, 2, 4
 // or 8); wn is [phase][tap][cin][coutp] f32. Uses p's input view, output geometry, tap tables,
 // bias and epilogue fields.

@@ -234,6 +234,7 @@ Layer::~Layer() {
     if (w_f32) (void)hipFree(w_f32);
     if (wn) (void)hipFree(wn);
     if (wpk_m) (void)hipFree(wpk_m);
+    if (wpk32) (void)hipFree(wpk32);
 }
 
 void Layer::out_size(int h, int w, int* oh, int* ow) const {
@@ -312,6 +313,20 @@ LayerP make_conv(Context& ctx, int cin, int cout, int kh, int kw, int stride, in
                         pk[dst] = weight[(((size_t)(g * cout_g + ocl) * cin_g + icl) * kh + ky) * kw + kx];
                     }
     L->wpk = upload_as(ctx, pk, dtype, &L->wpk_bytes);
+    if (dtype != DT_F32 && L->kind == CK_3x3 && groups == 1 && (cin == 64 || cin == 128) && cout % 64 == 0 && no_extra &&
+        pad_h == 1 && pad_w == 1) {
+        // conv3x3_m32's packing: [cin / 16][cout / mt][tap][channel half][mt][8].
+        const int mt = cout % 128 == 0 ? 128 : 64, nmt = cout / mt;
+        std::vector<float> p32((size_t)cin * cout * 9);
+        for (int oc = 0; oc < cout; ++oc)
+            for (int ic = 0; ic < cin; ++ic)
+                for (int t = 0; t < 9; ++t)
+                    p32[(((((size_t)(ic / 16) * nmt + oc / mt) * 9 + t) * 2 + (ic % 16) / 8) * mt + oc % mt) * 8 +
+                        ic % 8] = weight[((size_t)oc * cin + ic) * 9 + t];
+        size_t bytes = 0;
+        L->wpk32 = upload_as(ctx, p32, dtype, &bytes);
+        L->mt32 = mt;
+    }
     if (bias) L->bias = upload_f32(bias, cout);
     if (keep_f32 && L->kind == CK_1x1 && groups == 1) L->w_f32 = upload_f32(weight, (size_t)cout * cin);
     return L;
@@ -559,6 +574,16 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
         LaunchScope sc(ctx, std::string("conv_tr_merged<") + ty[L.dtype] + ">", 2.0 * macs,
                        bytes - (double)L.wpk_bytes + (double)L.wpk_m_bytes);
         ZJAI_HIP(launch_conv_tr_merged(L.dtype, p, ctx.stream));
+        return y;
+    }
+    if (L.wpk32 && !e.w_batch && !plane && ps == 1 && !e.relu6_in && !(ctx.top().flags & ZJAI_CTX_MFMA16_CONV3X3)) {
+        static const char* ty[] = {"float", "_Float16", "__bf16"};
+        const int tw = conv3x3_m32_width(OH, OW);
+        p.w = L.wpk32;
+        char name[64];
+        snprintf(name, sizeof name, "conv3x3_m32<%s, %d, %d>", ty[L.dtype], L.mt32, tw);
+        LaunchScope sc(ctx, name, 2.0 * macs, bytes);
+        ZJAI_HIP(launch_conv3x3_m32(L.dtype, L.mt32, tw, p, ctx.stream));
         return y;
     }
     LaunchScope sc(ctx, conv_kernel_name(L.kind, L.dtype, L.cfg), 2.0 * macs, bytes);
