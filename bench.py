@@ -39,7 +39,8 @@ sys.path.insert(0, ROOT)
 METRIC = "synthesis decode Mpixel/s at 1MP & 4MP; conv TFLOP/s + % MFMA peak (1 GPU)"
 PEAK_TFLOPS = {"f32": 157.3, "f16": 2500.0, "bf16": 2500.0}
 PEAK_HBM_GBS = 8000.0
-CONV_KERNELS = ("conv_igemm", "conv_dma_f32")  # the MFMA convolution kernels (conv.hip)
+# The MFMA convolution kernels (conv.hip, conv32.hip, conv1x1.hip).
+CONV_KERNELS = ("conv_igemm", "conv_dma_f32", "conv_tr_merged", "conv3x3_m32", "conv1x1_ring")
 
 
 def log(msg):

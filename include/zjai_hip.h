@@ -75,7 +75,8 @@ typedef struct zjai_picture zjai_picture;
 
 /* Replaces `Engine` construction (src/nn/fast/mod.rs:128-172) for the HIP backend: binds a
  * device and creates its stream. flags: 0 or an OR of ZJAI_CTX_UNFUSED_BLOCKS,
- * ZJAI_CTX_PHASE_SPLIT_CONVT and ZJAI_CTX_MFMA16_CONV3X3 (other bits are rejected). */
+ * ZJAI_CTX_PHASE_SPLIT_CONVT, ZJAI_CTX_MFMA16_CONV3X3 and ZJAI_CTX_IGEMM_CONV1X1 (other bits are
+ * rejected). */
 /* Run the transformer blocks (src/model/attention.rs:328-372) as the reference's separate ops --
  * layer norm, 1x1, depthwise (+ ELU gate), 1x1 -- instead of the fused kernels the 16-bit
  * precisions use by default for `prep_data` (LN + 1x1 + depthwise) and for the feed-forward half
@@ -88,6 +89,9 @@ typedef struct zjai_picture zjai_picture;
 /* Run the dense stride-1 3x3 convolutions of the 16-bit precisions on the 16x16x32 MFMA kernel
  * instead of the 32x32x16 one (for A/B runs and the test that compares the two). */
 #define ZJAI_CTX_MFMA16_CONV3X3 0x4u
+/* Run the 1x1 convolutions on the implicit-GEMM conv kernel instead of the dedicated 1x1 GEMM
+ * kernel (same results bit for bit; for A/B runs and the test that proves it). */
+#define ZJAI_CTX_IGEMM_CONV1X1 0x8u
 ZJAI_API int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out);
 ZJAI_API int32_t zjai_ctx_destroy(zjai_ctx* ctx);
 /* Copies the last failure message (NUL-terminated, truncated to len). Works with ctx == NULL

@@ -174,6 +174,54 @@ def test_dense_16bit_conv3x3_kernels_agree(engines, igemm_engines, prec, cin, co
     assert rel_err(got["conv3x3_m32"], got["conv_igemm"]) <= TOL[prec]
 
 
+CONV1X1_CASES = [  # cin, cout, h, w, epilogue, crop (input as a cropped view)
+    (128, 1024, 23, 37, "none", False), (512, 128, 19, 21, "add", False), (64, 192, 17, 40, "gate", True),
+    (64, 64, 9, 14, "sigmoid*r", False), (128, 512, 13, 11, "ps2", False), (256, 64, 30, 30, "relu", True)]
+
+
+@pytest.mark.parametrize("prec", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("cin,cout,h,w,op,crop", CONV1X1_CASES)
+def test_conv1x1_kernels_are_bit_identical(engines, prec, cin, cout, h, w, op, crop):
+    """The dedicated 1x1 GEMM kernel (conv1x1_ring: row-major position tiles, a ring of direct-LDS
+    chunk loads) and the implicit-GEMM kernel (ZJAI_CTX_IGEMM_CONV1X1) give the same bits for
+    every epilogue, ragged position counts and cropped input views; both meet the oracle."""
+    x = synth.normal(7, f"c11/x{cin}", (cin, h + 3, w + 5) if crop else (cin, h, w), 1.0)
+    r = synth.normal(7, f"c11/r{cout}", (cout, h, w), 1.0)
+    wt = _he(f"c11/w{cin}{cout}", (cout, cin, 1, 1), cin)
+    b = synth.normal(7, f"c11/b{cout}", (cout,), 0.05)
+    xc = x[:, :h, :w]
+    base = oracle.conv2d(xc, wt, b, 1, (0, 0))
+    want, kw = {
+        "none": (lambda: base, {}),
+        "add": (lambda: oracle.add(base, r), dict(res=_lib.RES_ADD)),
+        "gate": (lambda: oracle.gate(r, base), dict(res=_lib.RES_GATE)),
+        "sigmoid*r": (lambda: oracle.mul(r, oracle.sigmoid(base)), dict(act=_lib.ACT_SIGMOID, res=_lib.RES_MUL)),
+        "ps2": (lambda: oracle.pixel_shuffle(base, 2), dict(pixel_shuffle=2)),
+        "relu": (lambda: oracle.relu(base), dict(act=_lib.ACT_RELU)),
+    }[op]
+    want = want()
+    eng1 = nn.Engine(0, prec, flags=_lib.CTX_IGEMM_CONV1X1)
+    got = []
+    ring = "conv1x1_ring"
+    for eng, kernel in ((engines[prec], ring), (eng1, "conv_")):
+        layer = nn.ConvLayer(nn.Conv2d(cin, cout, (1, 1), 1, (0, 0), 1, wt, b), eng)
+        xt = nn.BTensor.from_planar(eng, x)
+        if crop:
+            xt = xt.crop(h, w)
+        args = dict(kw, r1=nn.BTensor.from_planar(eng, r)) if "res" in kw else kw
+        eng.sync()
+        eng.profile_begin()
+        y = layer.forward_fused(eng, xt, **args)
+        names = [rec[0] for rec in eng.profile_end()]
+        assert any(n.startswith(kernel) for n in names), names
+        got.append(y.to_planar())
+        err = rel_err(got[-1], want)
+        print(f"{prec} {cin}->{cout} {h}x{w} {op} {kernel}: {err:.2e}")
+        assert err <= TOL[prec], (kernel, err)
+    eng1.close()
+    np.testing.assert_array_equal(got[0], got[1])
+
+
 @pytest.mark.parametrize("prec", ["f32", "bf16"])
 def test_config2_convt4_leaky(engines, prec):
     """BASELINE config 2 at full size: ConvT k4 s2 p1 192->128, 64^2 -> 128^2, then

@@ -36,6 +36,7 @@ RES_NONE, RES_ADD, RES_GATE, RES_CAB, RES_MUL = 0, 1, 2, 3, 4
 CTX_UNFUSED_BLOCKS = 0x1  # zjai_ctx_create flags
 CTX_PHASE_SPLIT_CONVT = 0x2
 CTX_MFMA16_CONV3X3 = 0x4
+CTX_IGEMM_CONV1X1 = 0x8
 RESIZE_BICUBIC, RESIZE_BILINEAR = 0, 1
 PLANE_LATENT, PLANE_PSI, PLANE_HYPER_LATENT, PLANE_IMAGE = 0, 1, 2, 3
 

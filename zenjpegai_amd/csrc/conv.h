@@ -84,6 +84,14 @@ constexpr int TR_MERGED_NB = 4;
 hipError_t launch_conv3x3_m32(int dtype, int mt, int tw, const ConvParams& p, hipStream_t s);
 int conv3x3_m32_width(int OH, int OW);
 
+// 1x1 layers (stride 1, no padding, one group) as a GEMM over row-major positions with a
+// ring of direct-LDS chunk loads (conv1x1.hip); p.w is the implicit-GEMM packing, p.cout_g a
+// multiple of 64, 16-byte aligned input views, no relu6 on load. Results are bit-identical to
+// launch_conv on the same layer. conv1x1_ring_ok: whether p qualifies.
+hipError_t launch_conv1x1_ring(int dtype, const ConvParams& p, hipStream_t s);
+bool conv1x1_ring_ok(const ConvParams& p, int dtype);
+int conv1x1_ring_nb(const ConvParams& p);
+
 // Stride-2 transposed conv with cout <= 8 on the vector ALUs (coutp = cout rounded up to 1, 2, 4
 // or 8); wn is [phase][tap][cin][coutp] f32. Uses p's input view, output geometry, tap tables,
 // bias and epilogue fields.

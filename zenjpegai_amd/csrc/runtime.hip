@@ -586,6 +586,14 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
         ZJAI_HIP(launch_conv3x3_m32(L.dtype, L.mt32, tw, p, ctx.stream));
         return y;
     }
+    if (L.kind == CK_1x1 && !(ctx.top().flags & ZJAI_CTX_IGEMM_CONV1X1) && conv1x1_ring_ok(p, L.dtype)) {
+        static const char* ty[] = {"float", "_Float16", "__bf16"};
+        char name[64];
+        snprintf(name, sizeof name, "conv1x1_ring<%s, %d>", ty[L.dtype], conv1x1_ring_nb(p) * 16);
+        LaunchScope sc(ctx, name, 2.0 * macs, bytes);
+        ZJAI_HIP(launch_conv1x1_ring(L.dtype, p, ctx.stream));
+        return y;
+    }
     LaunchScope sc(ctx, conv_kernel_name(L.kind, L.dtype, L.cfg), 2.0 * macs, bytes);
     ZJAI_HIP(launch_conv(L.kind, L.dtype, L.cfg, p, ctx.stream));
     return y;
