@@ -333,8 +333,8 @@ def test_conv_transpose_odd_sizes(engines, k, op):
     assert rel_err(y, oracle.conv_transpose2d(x, w, b, 2, 1, op)) <= 1e-4
 
 
-@pytest.mark.parametrize("cout", [1, 3, 8])
-@pytest.mark.parametrize("k,op", [(3, 1), (4, 0)])
+@pytest.mark.parametrize("cout", [1, 2, 3, 8])
+@pytest.mark.parametrize("k,op", [(3, 1), (3, 0), (4, 0)])
 def test_narrow_conv_transpose_is_bit_exact(engines, cout, k, op):
     """Transposed convs with at most 8 outputs (the last synthesis layers) run on the vector ALUs
     in the reference's (input channel, tap) FMA order: in fp32 they equal the oracle bit for bit,
@@ -352,6 +352,38 @@ def test_narrow_conv_transpose_is_bit_exact(engines, cout, k, op):
     # relu6 on load (ResAU's input clamp) goes through the same kernel.
     y6 = layer.forward_fused(eng, xt, relu6_input=True).to_planar()
     assert np.array_equal(y6, oracle.conv_transpose2d(oracle.relu6(x), w, b, 2, 1, op))
+
+
+def _round_storage(a, prec):
+    """IEEE round-to-nearest-even of f32 values to the 16-bit storage type, back in f32."""
+    a = np.ascontiguousarray(a, np.float32)
+    if prec == "f16":
+        return a.astype(np.float16).astype(np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("prec", ["f16", "bf16"])
+@pytest.mark.parametrize("cout,op", [(1, 1), (2, 0)])
+def test_narrow_conv_transpose_3x3_16bit_is_exact(engines, prec, cout, op):
+    """The 3x3 narrow transposed conv (k_convT3_narrow) in a 16-bit precision computes in f32 on
+    the stored (rounded) inputs and weights in the reference's FMA order, so its output is the
+    oracle's f32 result on those rounded operands, rounded once to the storage type -- bit for
+    bit. 128 input channels (two 128-byte chunks in 16-bit), a map not a multiple of the tile."""
+    eng = engines[prec]
+    x = synth.normal(11, "t3/x", (128, 19, 45), 1.0)
+    w = synth.normal(11, f"t3/w{cout}", (128, cout, 3, 3), 0.1)
+    b = synth.normal(11, f"t3/b{cout}", (cout,), 0.1)
+    layer = nn.ConvTransposeLayer(nn.ConvTranspose2d(128, cout, 3, 2, 1, op, w, b), eng)
+    eng.sync()
+    eng.profile_begin()
+    y = layer.forward(eng, nn.BTensor.from_planar(eng, x)).to_planar()
+    names = [r[0] for r in eng.profile_end()]
+    assert any(n.startswith("k_convT3_narrow") for n in names), names
+    want = _round_storage(oracle.conv_transpose2d(_round_storage(x, prec), _round_storage(w, prec), b, 2, 1, op),
+                          prec)
+    assert np.array_equal(y, want)
 
 
 @pytest.mark.parametrize("prec", ["f16", "bf16"])

@@ -93,8 +93,10 @@ bool conv1x1_ring_ok(const ConvParams& p, int dtype);
 int conv1x1_ring_nb(const ConvParams& p);
 
 // Stride-2 transposed conv with cout <= 8 on the vector ALUs (coutp = cout rounded up to 1, 2, 4
-// or 8); wn is [phase][tap][cin][coutp] f32. Uses p's input view, output geometry, tap tables,
+// or 8); wn is [cin][phase][tap][coutp] f32. Uses p's input view, output geometry, tap tables,
 // bias and epilogue fields.
+// convT_narrow_k3: whether launch_convT_narrow takes the 3x3 / padding-1 kernel for p.
+bool convT_narrow_k3(int dtype, const ConvParams& p, int cin);
 hipError_t launch_convT_narrow(int dtype, int coutp, const ConvParams& p, const float* wn, int cin,
                                hipStream_t s);
 

@@ -738,7 +738,7 @@ hipError_t launch_conv_tr_merged(int dtype, const ConvParams& p0, hipStream_t s)
 // reference's convT order (src/nn/reference.rs:155-236), so in f32 the result equals the oracle
 // bit for bit. Per chunk of 16 input channels a workgroup stages its (TYN + 2) x (TXN + 2) input
 // halo in LDS channel-major, so consecutive threads read consecutive words.
-// wn: [phase][tap][cin][COUT] f32 (weights already rounded to the storage type).
+// wn: [cin][phase][tap][COUT] f32 (weights already rounded to the storage type).
 template <typename T, int COUT>
 __global__ void __launch_bounds__(256)
 k_convT_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
@@ -801,7 +801,7 @@ k_convT_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
         }
         for (int u = tid; u < 4 * 4 * CKN * COUT; u += 256) {
             const int oc = u % COUT, k = (u / COUT) % CKN, pt = u / (COUT * CKN);
-            s_w[u] = c0 + k < cin ? wn[((long long)pt * cin + c0 + k) * COUT + oc] : 0.0f;
+            s_w[u] = c0 + k < cin ? wn[((long long)(c0 + k) * 16 + pt) * COUT + oc] : 0.0f;
         }
         __syncthreads();
         const int kn = min(CKN, cin - c0);
@@ -835,6 +835,188 @@ k_convT_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
     }
 }
 
+// The same layer for the 3x3 kernel with padding 1 (the synthesis nets' conv3x3_t): its taps
+// are fixed, phase (py, px) reading input (y' + a, x' + b) for a <= py, b <= px, so a position
+// needs only the 2 x 2 input neighbourhood (y', x') .. (y' + 1, x' + 1). A workgroup of 256
+// threads takes 8 x 32 positions; per chunk of 128 bytes of input channels (32 f32 or 64
+// f16 / bf16) the 9 x 33 input halo goes global -> LDS with direct loads (whole 128-byte
+// channel runs per pixel, each fetched once; halo overhead 1.16x), double-buffered (two
+// workgroups per CU keep four chunks in flight), 16-byte
+// slots XOR-swizzled by pixel so that each thread's 16-byte neighbour reads are free of bank
+// conflicts. Weights come through scalar loads ([cin][phase][tap][COUT], uniform). Against the
+// generic kernel on HOP luma's 128 -> 1 layer (862 x 862 positions): f32 153 vs 270 us, bf16
+// 122 vs 226 us. FMA order
+// per output is the generic kernel's (input channel ascending, then the phase's taps in
+// (ky, kx) order), so the results are identical to it bit for bit.
+__device__ u32x4 g_zero_unitsT[4];  // 64 zero bytes: the source of halo pixels off the map
+
+typedef __attribute__((address_space(3))) void* lds_addr_t_t;
+
+template <typename T>
+__device__ __forceinline__ void unpack16(u32x4 u, float (&v)[16 / sizeof(T)]) {
+    if constexpr (sizeof(T) == 4) {
+        const f32x4 f = __builtin_bit_cast(f32x4, u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = f[i];
+    } else {
+        typedef T t8 __attribute__((ext_vector_type(8)));
+        const t8 h = __builtin_bit_cast(t8, u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (float)h[i];
+    }
+}
+
+template <typename T, int COUT>
+__global__ void __launch_bounds__(256)
+k_convT3_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
+    constexpr int TY = 8, TX = 32, HX = TX + 1, HY = TY + 1, HPIX = HX * HY;
+    constexpr int VEC = 16 / (int)sizeof(T);
+    constexpr int HALO_U = HPIX * 8;                  // [pixel][8 swizzled 16-byte slots]
+    constexpr int HN = (HALO_U + 255) / 256;
+    __shared__ u32x4 s_halo[2 * HALO_U];
+    const int gw = (p.OW + 1) / 2, gh = (p.OH + 1) / 2;
+    const int gx = (gw + TX - 1) / TX, gy = (gh + TY - 1) / TY;
+    // XCD-aware order (k_convT_narrow's): each XCD takes one contiguous band of tiles.
+    int bid = (int)((blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8);
+    if (bid >= gx * gy * p.N) return;
+    const int tx = bid % gx;
+    bid /= gx;
+    const int ty = bid % gy, bi = bid / gy;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = tid / TX, c = tid % TX;
+    const int y0 = ty * TY, x0 = tx * TX;
+    const T* xg = (const T*)p.x.p + (long long)bi * p.x.bstride + p.x.c_off;
+
+    float acc[4][COUT];
+#pragma unroll
+    for (int ph = 0; ph < 4; ++ph)
+#pragma unroll
+        for (int oc = 0; oc < COUT; ++oc) acc[ph][oc] = (p.bias && oc < p.cout_g) ? p.bias[oc] : 0.0f;
+
+    // Halo unit U = pixel * 8 + slot holds the pixel's 16-byte unit slot ^ ((pixel / 2) % 8).
+    long long hoff[HN];
+#pragma unroll
+    for (int i = 0; i < HN; ++i) {
+        const int U = wave * 64 + i * 256 + lane, pix = U >> 3, slot = U & 7;
+        const int hy = pix / HX, hx = pix - hy * HX;
+        const int iy = y0 + hy, ix = x0 + hx;
+        hoff[i] = (U < HALO_U && iy < p.H && ix < p.W)
+                      ? (long long)iy * p.x.row + (long long)ix * p.x.cs + (slot ^ ((pix >> 1) & 7)) * VEC
+                      : -1;
+    }
+    auto issue = [&](int chunk, int buf) __attribute__((always_inline)) {
+        const long long c0 = (long long)chunk * 8 * VEC;
+#pragma unroll
+        for (int i = 0; i < HN; ++i) {
+            const int ub = wave * 64 + i * 256;
+            if (ub >= HALO_U) break;
+            if (ub + lane < HALO_U) {
+                const void* src = hoff[i] >= 0 ? (const void*)(xg + hoff[i] + c0) : (const void*)g_zero_unitsT;
+                __builtin_amdgcn_global_load_lds(src, (lds_addr_t_t)(s_halo + buf * HALO_U + ub), 16, 0, 0);
+            }
+        }
+    };
+    int npix[4];  // neighbours (y' + a, x' + b), index 2a + b
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) npix[2 * a + b] = (r + a) * HX + c + b;
+
+    const int nch = cin / (8 * VEC);
+    issue(0, 0);
+    for (int ch = 0; ch < nch; ++ch) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of chunk ch are in LDS
+        __syncthreads();                     // ... and every other wave's
+        if (ch + 1 < nch) issue(ch + 1, (ch + 1) & 1);
+        const u32x4* hb = s_halo + (ch & 1) * HALO_U;
+#pragma unroll 2
+        for (int q = 0; q < 8; ++q) {
+            float x[4][VEC];
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                const int pix = npix[n];
+                unpack16<T>(hb[pix * 8 + (q ^ ((pix >> 1) & 7))], x[n]);
+                if (p.relu6_in) {
+#pragma unroll
+                    for (int i = 0; i < VEC; ++i) {
+                        float e = x[n][i];
+                        e = e < 0.0f ? 0.0f : e;
+                        x[n][i] = e > 6.0f ? 6.0f : e;
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+                const float* w = wn + (long long)((ch * 8 + q) * VEC + i) * 16 * COUT;
+                // Phase taps in (ky, kx) order: (0,0): x00; (0,1): x01, x00; (1,0): x10, x00;
+                // (1,1): x11, x10, x01, x00.
+#pragma unroll
+                for (int oc = 0; oc < COUT; ++oc) {
+                    acc[0][oc] = fmaf(w[0 * COUT + oc], x[0][i], acc[0][oc]);
+                    acc[1][oc] = fmaf(w[4 * COUT + oc], x[1][i], acc[1][oc]);
+                    acc[1][oc] = fmaf(w[5 * COUT + oc], x[0][i], acc[1][oc]);
+                    acc[2][oc] = fmaf(w[8 * COUT + oc], x[2][i], acc[2][oc]);
+                    acc[2][oc] = fmaf(w[9 * COUT + oc], x[0][i], acc[2][oc]);
+                    acc[3][oc] = fmaf(w[12 * COUT + oc], x[3][i], acc[3][oc]);
+                    acc[3][oc] = fmaf(w[13 * COUT + oc], x[2][i], acc[3][oc]);
+                    acc[3][oc] = fmaf(w[14 * COUT + oc], x[1][i], acc[3][oc]);
+                    acc[3][oc] = fmaf(w[15 * COUT + oc], x[0][i], acc[3][oc]);
+                }
+            }
+        }
+    }
+    const int yq = y0 + r, xq = x0 + c;
+#pragma unroll
+    for (int ph = 0; ph < 4; ++ph) {
+        const int oy = 2 * yq + (ph >> 1), ox = 2 * xq + (ph & 1);
+        if (oy >= p.OH || ox >= p.OW) continue;
+#pragma unroll
+        for (int oc0 = 0; oc0 < COUT; oc0 += 4) {
+            if (oc0 >= p.cout_g) break;
+            f32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = oc0 + i < COUT ? acc[ph][min(oc0 + i, COUT - 1)] : 0.0f;
+            epilogue_store<T>(p, bi, oy, ox, oc0, min(4, p.cout_g - oc0), v);
+        }
+    }
+}
+
+// Whether a layer's tap tables are the 3x3 / padding 1 ones k_convT3_narrow hard-codes
+// (halo offsets 1 = input row y', 2 = y' + 1).
+static bool taps_are_k3p1(const ConvParams& p) {
+    static const int nt[4] = {1, 2, 2, 4};
+    static const int dy[4][4] = {{1}, {1, 1}, {2, 1}, {2, 2, 1, 1}};
+    static const int dx[4][4] = {{1}, {2, 1}, {1, 1}, {2, 1, 2, 1}};
+    for (int ph = 0; ph < 4; ++ph) {
+        if (p.ntaps[ph] != nt[ph]) return false;
+        for (int t = 0; t < nt[ph]; ++t)
+            if (p.tap_dy[ph][t] != dy[ph][t] || p.tap_dx[ph][t] != dx[ph][t]) return false;
+    }
+    return true;
+}
+
+template <typename T>
+static hipError_t go_narrow3(int coutp, const ConvParams& p, const float* wn, int cin, hipStream_t s) {
+    const int gw = (p.OW + 1) / 2, gh = (p.OH + 1) / 2;
+    const long long blocks = ((long long)((gw + 31) / 32) * ((gh + 7) / 8) * p.N + 7) / 8 * 8;
+    if (blocks <= 0 || blocks > (1ll << 30) || p.N < 1 || p.N > MAXB) return hipErrorInvalidValue;
+    const dim3 g((unsigned)blocks);
+    switch (coutp) {
+        case 1: hipLaunchKernelGGL((k_convT3_narrow<T, 1>), g, dim3(256), 0, s, p, wn, cin); break;
+        case 2: hipLaunchKernelGGL((k_convT3_narrow<T, 2>), g, dim3(256), 0, s, p, wn, cin); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// One or two outputs only: wider layers spend their time in the FMAs, where the generic
+// kernel's LDS-broadcast weights beat scalar loads of 9 x coutp weights per input channel.
+bool convT_narrow_k3(int dtype, const ConvParams& p, int cin) {
+    const int vec = dtype == DT_F32 ? 4 : 8;
+    return p.cout_g <= 2 && taps_are_k3p1(p) && cin % (8 * vec) == 0 && p.x.cs % vec == 0 &&
+           p.x.c_off % vec == 0 && p.x.row % vec == 0 && p.x.bstride % vec == 0;
+}
+
 template <typename T>
 static hipError_t go_narrow(int coutp, const ConvParams& p, const float* wn, int cin, hipStream_t s) {
     const int gw = (p.OW + 1) / 2, gh = (p.OH + 1) / 2;
@@ -853,6 +1035,14 @@ static hipError_t go_narrow(int coutp, const ConvParams& p, const float* wn, int
 
 hipError_t launch_convT_narrow(int dtype, int coutp, const ConvParams& p, const float* wn, int cin,
                                hipStream_t s) {
+    if (convT_narrow_k3(dtype, p, cin)) {
+        switch (dtype) {
+            case DT_F32: return go_narrow3<float>(coutp, p, wn, cin, s);
+            case DT_F16: return go_narrow3<_Float16>(coutp, p, wn, cin, s);
+            case DT_BF16: return go_narrow3<__bf16>(coutp, p, wn, cin, s);
+        }
+        return hipErrorInvalidValue;
+    }
     switch (dtype) {
         case DT_F32: return go_narrow<float>(coutp, p, wn, cin, s);
         case DT_F16: return go_narrow<_Float16>(coutp, p, wn, cin, s);

@@ -415,7 +415,7 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
     }
     if (cout <= 8) {
         // Narrow layers run on the vector ALUs (launch_convT_narrow) from an f32 copy of the
-        // storage-rounded weights, [phase][tap][cin][coutp].
+        // storage-rounded weights, [cin][phase][tap][coutp].
         L->coutp = cout <= 1 ? 1 : cout <= 2 ? 2 : cout <= 4 ? 4 : 8;
         std::vector<float> wn((size_t)16 * cin * L->coutp, 0.0f);
         for (int ph = 0; ph < 4; ++ph) {
@@ -426,7 +426,7 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
                     const int ky = ky_list[py][a], kx = ky_list[px][b];
                     for (int ic = 0; ic < cin; ++ic)
                         for (int oc = 0; oc < cout; ++oc)
-                            wn[((size_t)(ph * 4 + t) * cin + ic) * L->coutp + oc] =
+                            wn[((size_t)ic * 16 + ph * 4 + t) * L->coutp + oc] =
                                 storage_value(weight[(((size_t)ic * cout + oc) * k + ky) * k + kx], dtype);
                 }
         }
@@ -561,7 +561,8 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
     if (L.wn && !e.w_batch) {
         static const char* ty[] = {"float", "_Float16", "__bf16"};
         char name[64];
-        snprintf(name, sizeof name, "k_convT_narrow<%s, %d>", ty[L.dtype], L.coutp);
+        snprintf(name, sizeof name, "%s<%s, %d>", convT_narrow_k3(L.dtype, p, L.cin) ? "k_convT3_narrow" : "k_convT_narrow",
+                 ty[L.dtype], L.coutp);
         LaunchScope sc(ctx, name, 2.0 * macs, bytes);
         ZJAI_HIP(launch_convT_narrow(L.dtype, L.coutp, p, L.wn, L.cin, ctx.stream));
         return y;
