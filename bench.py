@@ -8,9 +8,11 @@ latents already resident in HBM (``Picture.run``: every tile on one HIP stream, 
 written by the last layers' epilogues).
 
 ``value`` is the fp32-MFMA parity path (the reference computes in f32). Extra lines in ``extra``:
-the same picture on the f16 / bf16 paths, BASELINE config 4 (SOP luma 1024x1024, 8-bit), a 4 MP
-HOP picture (2048x2048, 1 MP header tiles) and BASELINE configs 1-3 as single layers (kernel time
-and TFLOP/s, f32 and bf16).
+the host-to-host rate of the same picture (latent upload, synthesis, download of the 10-bit
+planes; ``host_to_host``), the device time of the last timed step, the same picture on the f16 /
+bf16 paths with the PSNR of their 10-bit planes against the f32 path's, BASELINE config 4 (SOP
+luma 1024x1024, 8-bit), a 4 MP HOP picture (2048x2048, 1 MP header tiles) and BASELINE configs 1-3
+as single layers (kernel time and TFLOP/s, f32 and bf16).
 
 ``roofline``: one profiled step (HIP events around every launch, all on one stream); the
 dominant kernel is the one with the largest summed time; bound by its arithmetic intensity
@@ -20,7 +22,9 @@ from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes summarised in ``profiles/`` (n
 
 ``cpu_baseline``: the reference's CPU engine ``nn::fast`` restated in C++ (``oracle/fast_cpu.cpp``,
 bit-identical to the oracle) timed on a bounded sample of the same workload -- the config-5 tiles
-in order for about 20 s, luma + chroma -- on this host's cores.
+in order for about 20 s, luma + chroma -- on this host's cores; plus the first tile on one thread,
+the restatement's GMAC/s on a dense 3x3 160 -> 160 layer (one thread and all, beside the
+reference's published one-thread figure) and the host CPU as lscpu reports it.
 """
 
 from __future__ import annotations
@@ -47,8 +51,9 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_workload(name, eng, lanes=1, bits=None):
-    """``bits``: output bit depth override (0 = float planes)."""
+def make_workload(name, eng, lanes=1, bits=None, gain=1.0):
+    """``bits``: output bit depth override (0 = float planes); ``gain``: He-std scale of the
+    random weights (1 = the benchmarked nets)."""
     from zenjpegai_amd import model, synth
     bits_override = bits
     if name == "cfg5":
@@ -70,12 +75,12 @@ def make_workload(name, eng, lanes=1, bits=None):
         uv = False
     else:
         raise SystemExit(f"unknown workload {name}")
-    py = synth.random_params(op, "y", seed=1)
+    py = synth.random_params(op, "y", seed=1, gain=gain)
     y = synth.latent(1, f"{name}/y", 160, lh, lw)
     prim = model.SynthesisPrimary.load(py, op, eng)
     sec, uvl, puv = None, None, None
     if uv:
-        puv = synth.random_params(op, "uv", seed=1)
+        puv = synth.random_params(op, "uv", seed=1, gain=gain)
         sec = model.SynthesisSecondary.load(puv, op, eng)
         uvl = synth.latent(1, f"{name}/uv", 96, lh, lw)
     if bits_override is not None:
@@ -95,6 +100,34 @@ def time_steps(eng, pic, steps, warmup):
         pic.run()
     eng.sync()
     return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def host_to_host(pic, info, reps):
+    """One picture from latents on the host to quantised planes on the host: upload of y_hat and
+    uv_hat (host -> HBM), the synthesis, download of the Y, U and V planes (HBM -> host), all
+    synchronous, averaged over ``reps`` pictures after one warm-up."""
+    pic.upload(info["y"], info["uvl"])
+    pic.run()
+    pic.download()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        pic.upload(info["y"], info["uvl"])
+        pic.run()
+        pic.download()
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    return {"ms_per_picture": round(ms, 3), "mpix_s": round(info["h"] * info["w"] / (ms / 1e3) / 1e6, 3)}
+
+
+def plane_psnr(ref, got, bits):
+    """PSNR (dB) of each output plane against the f32 path's, at the planes' bit depth."""
+    peak = float((1 << bits) - 1) if bits else 255.0
+    out = {}
+    for name, a, b in zip("yuv", ref, got):
+        if a is None:
+            continue
+        mse = float(np.mean((a.astype(np.float64) - b.astype(np.float64)) ** 2))
+        out[name] = round(10.0 * np.log10(peak * peak / mse), 2) if mse > 0 else None
+    return out
 
 
 def profile_step(eng, pic):
@@ -285,13 +318,49 @@ def read_traffic(kernel, workload, precision):
     return None
 
 
-def cpu_baseline(info, budget_s=20.0):
-    """The CPU column: the reference's ``nn::fast`` engine restated in C++ (``oracle/fast_cpu.cpp``:
-    NCHWc blocks, packed weights, im2col rows, AVX-512 24x16 FMA register tiles, OpenMP over
-    rows; the rest of the graph on the oracle's C++ loops), run over the config-5 tiles in order
-    until ``budget_s`` is spent. Rate = displayed (core) pixels of the finished tiles / time, the
-    unit of ``value``."""
+def cpu_host():
+    """The host CPU as lscpu reports it: model, sockets, physical cores and logical CPUs (all on
+    the machine), and the CPUs this process may use."""
+    model, sockets, cores = None, set(), set()
+    try:
+        phys = None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                    sockets.add(v)
+                elif k == "core id":
+                    cores.add((phys, v))
+    except OSError:
+        pass
+    return {"model": model, "sockets": len(sockets) or None, "physical_cores": len(cores) or None,
+            "logical_cpus": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0))}
+
+
+def cpu_conv_anchor(threads, reps=3):
+    """GMAC/s of the nn::fast restatement on a dense 3x3 160 -> 160 layer at 107 x 107 positions
+    (the reference's per-core anchor: res_conv3x3_160_160@1/16, 97.3 G ops/s on one thread of its
+    AVX-512 tier, benchmarks/conv_kernels_2026-09-17.log:88-91)."""
     import oracle
+    from zenjpegai_amd import synth
+    oracle.set_cpu_threads(threads)
+    x = synth.normal(1, "cpu/x", (160, 107, 107), 1.0)
+    w = synth.normal(1, "cpu/w", (160, 160, 3, 3), 0.02)
+    oracle.conv2d(x, w, None, 1, (1, 1), fast=True)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        oracle.conv2d(x, w, None, 1, (1, 1), fast=True)
+    dt = (time.perf_counter() - t0) / reps
+    return round(107 * 107 * 160 * 160 * 9 / dt / 1e9, 1)
+
+
+def cpu_tiles(info, budget_s, max_tiles=None):
+    """Config-5 tiles in order through the CPU restatement until ``budget_s`` is spent: (tiles
+    done, core pixels, seconds)."""
     import oracle.graphs as og
     done, pix, t0 = 0, 0, time.perf_counter()
     with og.fast_convs():
@@ -304,16 +373,39 @@ def cpu_baseline(info, budget_s=20.0):
                 og.secondary(info["puv"], info["op"], y, uv, t.image.height, t.image.width)
             done += 1
             pix += min(t.core.width, max(info["w"] - t.core.x, 0)) * min(t.core.height, max(info["h"] - t.core.y, 0))
-            if time.perf_counter() - t0 >= budget_s:
+            if time.perf_counter() - t0 >= budget_s or (max_tiles and done >= max_tiles):
                 break
-    dt = time.perf_counter() - t0
+    return done, pix, time.perf_counter() - t0
+
+
+def cpu_baseline(info, budget_s=20.0):
+    """The CPU column: the reference's ``nn::fast`` engine restated in C++ (``oracle/fast_cpu.cpp``:
+    NCHWc blocks, packed weights, im2col rows, AVX-512 24x16 FMA register tiles, OpenMP over
+    rows; the rest of the graph on the oracle's C++ loops), run over the config-5 tiles in order
+    until ``budget_s`` is spent. Rate = displayed (core) pixels of the finished tiles / time, the
+    unit of ``value``."""
+    import oracle
+    threads = oracle.cpu_threads()
+    done, pix, dt = cpu_tiles(info, budget_s)
+    # One thread on the first tile (the per-core rate), then the threads restored.
+    oracle.set_cpu_threads(1)
+    d1, p1, t1 = cpu_tiles(info, 0.0, max_tiles=1)
+    gmac1 = cpu_conv_anchor(1)
+    oracle.set_cpu_threads(threads)
+    gmac = cpu_conv_anchor(threads)
     tier = oracle.lib().fc_block_size()
-    return {"value": round(pix / dt / 1e6, 4), "unit": "Mpixel/s", "cores": oracle.lib().fc_threads(),
+    return {"value": round(pix / dt / 1e6, 4), "unit": "Mpixel/s", "cores": threads,
             "kind": "port",
             "sample": (f"{done} of {len(info['tile_list'])} tiles of the config-5 picture (HOP Y+UV, "
                        f"{pix / 1e6:.2f} MP of cores) through a C++ restatement of the reference's "
-                       f"nn::fast engine ({'AVX-512' if tier == 16 else 'AVX2'} tier), {dt:.1f} s"),
-            "seconds": round(dt, 2)}
+                       f"nn::fast engine ({'AVX-512' if tier == 16 else 'AVX2'} tier; convolutions "
+                       f"blocked / row-vectorised, the other ops OpenMP loops), {dt:.1f} s"),
+            "seconds": round(dt, 2),
+            "one_thread": {"value": round(p1 / t1 / 1e6, 4), "unit": "Mpixel/s",
+                           "sample": f"tile 0 ({p1 / 1e6:.3f} MP of core), {t1:.1f} s"},
+            "conv3x3_160_gmac_s": {"threads_1": gmac1, f"threads_{threads}": gmac,
+                                   "reference_threads_1": 97.3},
+            "host": cpu_host()}
 
 
 def main():
@@ -358,9 +450,13 @@ def main():
     pic, info = make_workload(args.workload, eng, args.lanes)
     log(f"[bench] {info['tiles']} tiles; warmup {args.warmup}, timing {args.steps} steps")
     ms = time_steps(eng, pic, args.steps, args.warmup)
+    last_step_device_ms = eng.stats()["last_run_ms"]
     pixels = info["h"] * info["w"]
     value = pixels / (ms / 1e3) / 1e6
     log(f"[bench] {ms:.2f} ms/step -> {value:.2f} Mpixel/s")
+    h2h = host_to_host(pic, info, args.steps)
+    log(f"[bench] host to host: {h2h}")
+    planes_ref = pic.download() if args.precision == "f32" else None
     prof = profile_step(eng, pic)
     total_ms = sum(d["ms"] for d in prof.values())
     conv = {k: d for k, d in prof.items() if k.startswith(CONV_KERNELS)}
@@ -391,7 +487,8 @@ def main():
 
     latent_inputs = None
     extra = {
-        "device_ms_per_step": round(eng.stats()["last_run_ms"], 3),
+        "last_timed_step_device_ms": round(last_step_device_ms, 3),
+        "host_to_host": h2h,
         "profiled_kernel_ms": round(total_ms, 3),
         "conv_tflops": round(conv_flops / (conv_ms / 1e3) / 1e12, 3) if conv_ms else None,
         "conv_frac_of_peak": round(conv_flops / (conv_ms / 1e3) / 1e12 / PEAK_TFLOPS[args.precision], 4) if conv_ms else None,
@@ -410,8 +507,25 @@ def main():
             cf, cm = sum(d["flops"] for d in cv.values()), sum(d["ms"] for d in cv.values())
             extra[f"{args.workload}_{prec}_mpix_s"] = round(pixels / (ms2 / 1e3) / 1e6, 3)
             extra[f"{args.workload}_{prec}_conv_tflops"] = round(cf / (cm / 1e3) / 1e12, 3)
+            if planes_ref is not None:
+                extra[f"{args.workload}_{prec}_psnr_db_vs_f32"] = plane_psnr(planes_ref, p2.download(), info["bits"])
             log(f"[bench] {prec}: {ms2:.2f} ms/step")
             del p2, e2
+        if args.precision == "f32" and args.workload == "cfg5":
+            # The same picture on better-conditioned weights (He x 0.5): the gain-1 nets reach
+            # activations of ~1e5, beyond f16's range and bf16's 8-bit mantissa.
+            ref_e = nn.Engine(0, "f32")
+            ref_p, _ = make_workload(args.workload, ref_e, args.lanes, gain=0.5)
+            ref_p.run()
+            ref_planes = ref_p.download()
+            del ref_p, ref_e
+            for prec in ("bf16", "f16"):
+                e5 = nn.Engine(0, prec)
+                p5, _ = make_workload(args.workload, e5, args.lanes, gain=0.5)
+                p5.run()
+                extra[f"{args.workload}_{prec}_psnr_db_vs_f32_he_x0.5"] = plane_psnr(ref_planes, p5.download(), info["bits"])
+                del p5, e5
+            log("[bench] PSNR vs f32: " + ", ".join(f"{k}={v}" for k, v in extra.items() if "psnr" in k))
         if args.workload != "cfg4":
             e3 = nn.Engine(0, args.precision)
             p3, i3 = make_workload("cfg4", e3, args.lanes)

@@ -75,6 +75,8 @@ def lib():
         L.fc_threads.restype = ctypes.c_int
         L.fc_force_tier.restype = ctypes.c_int
         L.fc_force_tier.argtypes = [ctypes.c_int]
+        L.fc_set_threads.restype = ctypes.c_int
+        L.fc_set_threads.argtypes = [ctypes.c_int]
         for name in ("or_resize_bicubic", "or_resize_bilinear"):
             getattr(L, name).argtypes = [_f32p] + [ctypes.c_int] * 5 + [_f32p]
             getattr(L, name).restype = ctypes.c_int
@@ -306,3 +308,13 @@ def force_cpu_tier(v: int) -> None:
     """Pins the ``nn::fast`` restatement to its AVX2 (8) or AVX-512 (16) tier; 0 = automatic."""
     if lib().fc_force_tier(v):
         raise OracleError(f"CPU tier {v} is not available on this host")
+
+
+def set_cpu_threads(n: int) -> None:
+    """Sets the OpenMP threads of the CPU restatements (``fast_cpu.cpp`` and ``oracle.cpp``)."""
+    if lib().fc_set_threads(int(n)):
+        raise OracleError(f"thread count {n}")
+
+
+def cpu_threads() -> int:
+    return lib().fc_threads()

@@ -22,14 +22,15 @@
 // Tiers as in the reference: AVX-512 V = 16, B = 24 (conv.rs:381-386); AVX2 V = 8, B = 12
 // (conv.rs:388-393), chosen at run time.
 //
-// Grouped convolutions whose group size is not a multiple of V and depthwise layers are not
-// packed by the reference either (they go to its fallback / depthwise kernels); here they run
-// the oracle loops (or_conv2d), which have the same result.
+// Grouped convolutions whose group size is not a multiple of V are not packed by the reference
+// either (they go to its fallback kernel); here they run the oracle loops (or_conv2d), which have
+// the same result. Depthwise layers run a row-vectorised kernel with the oracle's sum order.
 
 #include <immintrin.h>
 #include <omp.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <vector>
@@ -186,10 +187,52 @@ int fc_block_size(void) { return tier_v(); }
 // Threads the OpenMP loops use.
 int fc_threads(void) { return omp_get_max_threads(); }
 
+// Sets the threads of later OpenMP loops (this library's and oracle.cpp's); n >= 1.
+int fc_set_threads(int n) {
+    if (n < 1) return -1;
+    omp_set_num_threads(n);
+    return 0;
+}
+
 // Forces the AVX2 tier (v = 8), the AVX-512 tier (16, only where supported) or automatic (0).
 int fc_force_tier(int v) {
     if (v != 0 && v != 8 && !(v == 16 && __builtin_cpu_supports("avx512f"))) return -1;
     g_forced_v = v;
+    return 0;
+}
+
+// Depthwise convolution (one input and one output channel per group, stride 1), planar: per
+// channel the zero-padded plane, then per tap (ky, kx ascending) one fused multiply-add over a
+// whole output row -- per output bias, then the taps in order, the oracle's sum -- vectorised
+// along the row by the compiler; OpenMP over channels (the reference's depthwise kernel,
+// src/nn/fast/depthwise.rs, likewise walks rows of one channel).
+static int depthwise(const float* x, int c, int h, int w, const float* weight, const float* bias, int kh,
+                     int kw, int pt, int pl, int pb, int pr, float* y) {
+    const int ph = h + pt + pb, pw = w + pl + pr;
+    if (ph < kh || pw < kw) return -1;
+    const int oh = ph - kh + 1, ow = pw - kw + 1;
+#pragma omp parallel
+    {
+        std::vector<float> pad((size_t)ph * pw);
+#pragma omp for schedule(dynamic, 1)
+        for (int ch = 0; ch < c; ++ch) {
+            std::fill(pad.begin(), pad.end(), 0.0f);
+            for (int r = 0; r < h; ++r)
+                std::memcpy(pad.data() + (size_t)(r + pt) * pw + pl, x + ((size_t)ch * h + r) * w, sizeof(float) * w);
+            const float* k = weight + (size_t)ch * kh * kw;
+            const float b = bias ? bias[ch] : 0.0f;
+            for (int oy = 0; oy < oh; ++oy) {
+                float* o = y + ((size_t)ch * oh + oy) * ow;
+                for (int ox = 0; ox < ow; ++ox) o[ox] = b;
+                for (int ky = 0; ky < kh; ++ky)
+                    for (int kx = 0; kx < kw; ++kx) {
+                        const float wt = k[ky * kw + kx];
+                        const float* in = pad.data() + (size_t)(oy + ky) * pw + kx;
+                        for (int ox = 0; ox < ow; ++ox) o[ox] = std::fma(wt, in[ox], o[ox]);
+                    }
+            }
+        }
+    }
     return 0;
 }
 
@@ -199,6 +242,9 @@ int fc_conv2d(const float* x, int c, int h, int w, const float* weight, const fl
     const int V = tier_v();
     if (groups <= 0 || c % groups || out_ch % groups || stride <= 0 || kh <= 0 || kw <= 0) return -1;
     const int icg = c / groups, ocg = out_ch / groups, nt = kh * kw;
+    if (groups == c && groups == out_ch && stride == 1)
+        return depthwise(x, c, h, w, weight, bias, kh, kw, pad_h + (extra ? extra[0] : 0), pad_w + (extra ? extra[1] : 0),
+                         pad_h + (extra ? extra[2] : 0), pad_w + (extra ? extra[3] : 0), y);
     if (nt > MAXT || stride > 2 || (groups > 1 && (icg % V || ocg % V)))
         return or_conv2d(x, c, h, w, weight, bias, out_ch, kh, kw, stride, pad_h, pad_w, groups, extra, y);
     const int pt = pad_h + (extra ? extra[0] : 0), pl = pad_w + (extra ? extra[1] : 0);

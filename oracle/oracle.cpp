@@ -15,6 +15,7 @@
 //
 // Tensors are planar [c][h][w] float32 (the reference's `Tensor<f32>`, `src/tensor.rs:12`).
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -135,6 +136,7 @@ int or_conv_transpose2d(const float* x, int c, int h, int w, const float* weight
 int or_pixel_shuffle(const float* x, int c, int h, int w, int r, float* y) {
     if (r <= 0 || c % (r * r)) return -1;
     const int oc_n = c / (r * r);
+#pragma omp parallel for schedule(static)
     for (int oc = 0; oc < oc_n; ++oc)
         for (int dy = 0; dy < r; ++dy)
             for (int dx = 0; dx < r; ++dx) {
@@ -148,12 +150,17 @@ int or_pixel_shuffle(const float* x, int c, int h, int w, int r, float* y) {
 
 // ---------------------------------------------------------------------------------------------
 // Elementwise operations (src/nn/reference.rs:339-350, src/nn/fast/layers.rs:174-229,
-// src/model/hyper_encoder.rs:21-30, src/model/synthesis.rs:187-192).
+// src/model/hyper_encoder.rs:21-30, src/model/synthesis.rs:187-192). Each element is computed
+// on its own, so the OpenMP split over elements changes no result.
 // ---------------------------------------------------------------------------------------------
 // f32::max(x, 0): a NaN input gives 0.
-void or_relu(float* x, long n) { for (long i = 0; i < n; ++i) x[i] = std::fmax(x[i], 0.0f); }
+void or_relu(float* x, long n) {
+#pragma omp parallel for simd schedule(static)
+    for (long i = 0; i < n; ++i) x[i] = std::fmax(x[i], 0.0f);
+}
 // f32::clamp(0, 6): NaN stays NaN.
 void or_relu6(float* x, long n) {
+#pragma omp parallel for schedule(static)
     for (long i = 0; i < n; ++i) {
         float v = x[i];
         if (v < 0.0f) v = 0.0f;
@@ -161,16 +168,27 @@ void or_relu6(float* x, long n) {
         x[i] = v;
     }
 }
-void or_add(float* dst, const float* src, long n) { for (long i = 0; i < n; ++i) dst[i] += src[i]; }
+void or_add(float* dst, const float* src, long n) {
+#pragma omp parallel for simd schedule(static)
+    for (long i = 0; i < n; ++i) dst[i] += src[i];
+}
 // `x *= 1 + mask`: an add then a multiply, never fused (layers.rs:195-201).
 void or_gate(float* x, const float* mask, long n) {
+#pragma omp parallel for simd schedule(static)
     for (long i = 0; i < n; ++i) { const float g = 1.0f + mask[i]; x[i] = x[i] * g; }
 }
 // `if v < 0 { v *= 0.01 }` (hyper_encoder.rs:24-30).
-void or_leaky_relu(float* x, long n) { for (long i = 0; i < n; ++i) if (x[i] < 0.0f) x[i] = x[i] * 0.01f; }
-void or_mul(float* a, const float* b, long n) { for (long i = 0; i < n; ++i) a[i] = a[i] * b[i]; }
+void or_leaky_relu(float* x, long n) {
+#pragma omp parallel for schedule(static)
+    for (long i = 0; i < n; ++i) if (x[i] < 0.0f) x[i] = x[i] * 0.01f;
+}
+void or_mul(float* a, const float* b, long n) {
+#pragma omp parallel for simd schedule(static)
+    for (long i = 0; i < n; ++i) a[i] = a[i] * b[i];
+}
 // `(x * 128 + 127.5).clamp(0, 255)` (synthesis.rs:187-192).
 void or_denormalize(float* x, long n) {
+#pragma omp parallel for schedule(static)
     for (long i = 0; i < n; ++i) {
         float v = x[i] * 128.0f;
         v = v + 127.5f;
@@ -209,13 +227,18 @@ float or_exp(float x) {
     return y * scale;
 }
 
-void or_exp_slice(float* x, long n) { for (long i = 0; i < n; ++i) x[i] = or_exp(x[i]); }
+void or_exp_slice(float* x, long n) {
+#pragma omp parallel for schedule(static)
+    for (long i = 0; i < n; ++i) x[i] = or_exp(x[i]);
+}
 // `1 / (1 + exp(-x))` (math.rs:67-71).
 void or_sigmoid(float* x, long n) {
+#pragma omp parallel for schedule(static)
     for (long i = 0; i < n; ++i) { const float e = or_exp(-x[i]); x[i] = 1.0f / (1.0f + e); }
 }
 // `a = (a > 0 ? a : exp(a) - 1) * b` (math.rs:74-80).
 void or_elu_gate(float* a, const float* b, long n) {
+#pragma omp parallel for schedule(static)
     for (long i = 0; i < n; ++i) {
         const float e = or_exp(a[i]) - 1.0f;
         const float elu = a[i] > 0.0f ? a[i] : e;
@@ -229,28 +252,36 @@ void or_elu_gate(float* a, const float* b, long n) {
 int or_layer_norm_channels(float* x, int c, int h, int w, const float* weight, const float* bias) {
     if (c <= 0) return -1;
     const long n = (long)h * w;
-    std::vector<double> mean(n, 0.0), var(n, 0.0);
-    for (int ch = 0; ch < c; ++ch) {
-        const float* p = x + (size_t)ch * n;
-        for (long i = 0; i < n; ++i) mean[i] += (double)p[i];
-    }
-    for (long i = 0; i < n; ++i) mean[i] /= (double)c;
-    for (int ch = 0; ch < c; ++ch) {
-        const float* p = x + (size_t)ch * n;
-        for (long i = 0; i < n; ++i) { const double d = (double)p[i] - mean[i]; var[i] += d * d; }
-    }
-    std::vector<float> m32(n), den(n);
-    for (long i = 0; i < n; ++i) {
-        m32[i] = (float)mean[i];
-        den[i] = std::sqrt((float)(var[i] / (double)c) + 1e-5f);
-    }
-    for (int ch = 0; ch < c; ++ch) {
-        float* p = x + (size_t)ch * n;
-        for (long i = 0; i < n; ++i) {
-            float v = p[i] - m32[i];
-            v = v / den[i];
-            v = v * weight[ch];
-            p[i] = v + bias[ch];
+    // Positions are independent (each one's channel sums run in channel order): OpenMP splits
+    // the map into blocks of positions.
+    constexpr long B = 256;
+#pragma omp parallel for schedule(static)
+    for (long b0 = 0; b0 < n; b0 += B) {
+        const long nb = std::min(B, n - b0);
+        double mean[B], var[B];
+        float m32[B], den[B];
+        for (long i = 0; i < nb; ++i) mean[i] = var[i] = 0.0;
+        for (int ch = 0; ch < c; ++ch) {
+            const float* p = x + (size_t)ch * n + b0;
+            for (long i = 0; i < nb; ++i) mean[i] += (double)p[i];
+        }
+        for (long i = 0; i < nb; ++i) mean[i] /= (double)c;
+        for (int ch = 0; ch < c; ++ch) {
+            const float* p = x + (size_t)ch * n + b0;
+            for (long i = 0; i < nb; ++i) { const double d = (double)p[i] - mean[i]; var[i] += d * d; }
+        }
+        for (long i = 0; i < nb; ++i) {
+            m32[i] = (float)mean[i];
+            den[i] = std::sqrt((float)(var[i] / (double)c) + 1e-5f);
+        }
+        for (int ch = 0; ch < c; ++ch) {
+            float* p = x + (size_t)ch * n + b0;
+            for (long i = 0; i < nb; ++i) {
+                float v = p[i] - m32[i];
+                v = v / den[i];
+                v = v * weight[ch];
+                p[i] = v + bias[ch];
+            }
         }
     }
     return 0;

@@ -431,6 +431,9 @@ def _bits(a):
     (144, 128, 2, 1, 0, 1, (0, 0, 1, 1), 6, 9),      # SOP upsampler 2x2 with extra pad
     (64, 64, 3, 1, 1, 4, (0, 0, 0, 0), 6, 7),        # 16 per group: the oracle-loop fallback
     (256, 48, 3, 1, 1, 1, (0, 0, 0, 0), 8, 8),       # combine layer
+    (384, 384, 3, 1, 1, 384, (0, 0, 0, 0), 11, 37),  # depthwise (prep_data conv2)
+    (24, 24, 3, 1, 1, 24, (1, 0, 0, 2), 5, 9),       # depthwise with extra pad
+    (16, 16, 2, 1, 0, 16, (0, 0, 1, 1), 4, 3),       # depthwise 2x2
 ])
 def test_fast_conv2d_equals_reference_loops_bit_for_bit(cpu_tier, c, oc, k, stride, pad, groups,
                                                         extra, h, w):
