@@ -577,9 +577,16 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
         ZJAI_HIP(launch_conv_tr_merged(L.dtype, p, ctx.stream));
         return y;
     }
-    if (L.wpk32 && !e.w_batch && !plane && ps == 1 && !e.relu6_in && !(ctx.top().flags & ZJAI_CTX_MFMA16_CONV3X3)) {
+    // conv3x3_m32's 256-position tiles carry twice the work of conv_igemm's 64-channel ones: with
+    // 128 input channels and fewer tiles than CUs the smaller tiles fill the chip better.
+    const int tw32 = conv3x3_m32_width(OH, OW);
+    const long long tiles32 = L.wpk32 ? (long long)((OW + tw32 - 1) / tw32) * ((OH + 256 / tw32 - 1) / (256 / tw32)) *
+                                            N * (L.cout / L.mt32)
+                                      : 0;
+    if (L.wpk32 && (L.cin == 64 || tiles32 >= 256) && !e.w_batch && !plane && ps == 1 && !e.relu6_in &&
+        !(ctx.top().flags & ZJAI_CTX_MFMA16_CONV3X3)) {
         static const char* ty[] = {"float", "_Float16", "__bf16"};
-        const int tw = conv3x3_m32_width(OH, OW);
+        const int tw = tw32;
         p.w = L.wpk32;
         char name[64];
         snprintf(name, sizeof name, "conv3x3_m32<%s, %d, %d>", ty[L.dtype], L.mt32, tw);
