@@ -256,6 +256,21 @@ conv_igemm(const ConvParams p) {
                 for (int i = 0; i < 4; ++i) d[i] = acc[cf][pf][i];
             }
         __syncthreads();
+        if (nb0 * 16 + NB * 16 <= p.cout_g) {
+            // 8 channels per thread and step (all of the tile's channels are real).
+            constexpr int QP8 = NB * 2;
+#pragma unroll 4
+            for (int u = tid; u < TY * 16 * QP8; u += NT) {
+                const int pos = u / QP8, c8 = u - pos * QP8;
+                const int r = pos >> 4, cx = pos & 15;
+                const int oy = TR ? 2 * (oy0 + r) + (phase >> 1) : oy0 + r;
+                const int ox = TR ? 2 * (ox0 + cx) + (phase & 1) : ox0 + cx;
+                const f32x4 v0 = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + c8 * 8);
+                const f32x4 v1 = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + c8 * 8 + 4);
+                if (oy < p.OH && ox < p.OW) epilogue_store8<T>(p, bi, oy, ox, g * p.cout_g + nb0 * 16 + c8 * 8, v0, v1);
+            }
+            return;
+        }
         constexpr int QP = NB * 4;
         for (int u = tid; u < TY * 16 * QP; u += NT) {
             const int pos = u / QP, cq = u - pos * QP;
@@ -478,6 +493,21 @@ conv_dma_f32(const ConvParams p) {
                 for (int i = 0; i < 4; ++i) d[i] = acc[cf][pf][i];
             }
         __syncthreads();
+        if (nb0 * 16 + NB * 16 <= p.cout_g) {
+            // 8 channels per thread and step (all of the tile's channels are real).
+            constexpr int QP8 = NB * 2;
+#pragma unroll 4
+            for (int u = tid; u < TY * 16 * QP8; u += NT) {
+                const int pos = u / QP8, c8 = u - pos * QP8;
+                const int r = pos >> 4, cx = pos & 15;
+                const int oy = TR ? 2 * (oy0 + r) + (phase >> 1) : oy0 + r;
+                const int ox = TR ? 2 * (ox0 + cx) + (phase & 1) : ox0 + cx;
+                const f32x4 v0 = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + c8 * 8);
+                const f32x4 v1 = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + c8 * 8 + 4);
+                if (oy < p.OH && ox < p.OW) epilogue_store8<T>(p, bi, oy, ox, g * p.cout_g + nb0 * 16 + c8 * 8, v0, v1);
+            }
+            return;
+        }
         constexpr int QP = NB * 4;
         for (int u = tid; u < TY * 16 * QP; u += NT) {
             const int pos = u / QP, cq = u - pos * QP;
@@ -693,15 +723,29 @@ conv_tr_merged(const ConvParams p) {
         else put(acc[3]);
         __syncthreads();
         const int py = ph >> 1, px = ph & 1;
-        constexpr int QP = NB * 4;
-        for (int u = tid; u < TY * 16 * QP; u += NT) {
-            const int pos = u / QP, cq = u - pos * QP;
-            const int r = pos >> 4, cx = pos & 15;
-            const int oy = 2 * (oy0 + r) + py, ox = 2 * (ox0 + cx) + px;
-            const int ocl = nb0 * 16 + cq * 4;
-            if (oy >= p.OH || ox >= p.OW || ocl >= p.cout_g) continue;
-            const f32x4 v = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + cq * 4);
-            epilogue_store<T>(p, bi, oy, ox, ocl, min(4, p.cout_g - ocl), v);
+        if (epilogue_simple(p) && nb0 * 16 + NB * 16 <= p.cout_g) {
+            // 8 channels per thread and step (all of the tile's channels are real).
+            constexpr int QP8 = NB * 2;
+#pragma unroll 4
+            for (int u = tid; u < TY * 16 * QP8; u += NT) {
+                const int pos = u / QP8, c8 = u - pos * QP8;
+                const int r = pos >> 4, cx = pos & 15;
+                const int oy = 2 * (oy0 + r) + py, ox = 2 * (ox0 + cx) + px;
+                const f32x4 v0 = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + c8 * 8);
+                const f32x4 v1 = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + c8 * 8 + 4);
+                if (oy < p.OH && ox < p.OW) epilogue_store8<T>(p, bi, oy, ox, nb0 * 16 + c8 * 8, v0, v1);
+            }
+        } else {
+            constexpr int QP = NB * 4;
+            for (int u = tid; u < TY * 16 * QP; u += NT) {
+                const int pos = u / QP, cq = u - pos * QP;
+                const int r = pos >> 4, cx = pos & 15;
+                const int oy = 2 * (oy0 + r) + py, ox = 2 * (ox0 + cx) + px;
+                const int ocl = nb0 * 16 + cq * 4;
+                if (oy >= p.OH || ox >= p.OW || ocl >= p.cout_g) continue;
+                const f32x4 v = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + cq * 4);
+                epilogue_store<T>(p, bi, oy, ox, ocl, min(4, p.cout_g - ocl), v);
+            }
         }
     }
 }

@@ -139,15 +139,15 @@ __device__ __forceinline__ void epilogue_store4(const ConvParams& p, int b, int 
               v);
 }
 
-// True when a launch's epilogue is an NHWC store without pixel shuffle whose activation and
-// residual operation are plain arithmetic (no sigmoid, no CAB gate): epilogue_store8 covers it.
+// True when a launch's epilogue is an NHWC store without pixel shuffle: epilogue_store8 (any
+// activation and residual operation) covers it.
 __device__ __forceinline__ bool epilogue_simple(const ConvParams& p) {
-    return p.out_mode == OUT_NHWC && p.ps == 1 && p.act != ACT_SIGMOID && p.res != RES_CAB;
+    return p.out_mode == OUT_NHWC && p.ps == 1;
 }
 
 // epilogue_store for 8 consecutive channels of one position (all valid) when epilogue_simple
 // holds: the same IEEE operations in the same order, one 16-byte (16-bit types) or two 16-byte
-// (f32) stores.
+// (f32) stores, 8-channel residual loads.
 template <typename T>
 __device__ __forceinline__ void epilogue_store8(const ConvParams& p, int b, int oy, int ox, int oc0, f32x4 v0,
                                                 f32x4 v1) {
@@ -158,6 +158,9 @@ __device__ __forceinline__ void epilogue_store8(const ConvParams& p, int b, int 
     } else if (p.act == ACT_LEAKY) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = v[i] < 0.0f ? v[i] * 0.01f : v[i];
+    } else if (p.act == ACT_SIGMOID) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = sigmoidf_ref(v[i]);
     }
     if (p.res != RES_NONE) {
         const T* r = (const T*)p.r1.p + (long long)b * p.r1.bstride + (long long)oy * p.r1.row +
@@ -170,9 +173,20 @@ __device__ __forceinline__ void epilogue_store8(const ConvParams& p, int b, int 
         } else if (p.res == RES_GATE) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) { const float g = 1.0f + v[i]; v[i] = rv[i] * g; }
-        } else {  // RES_MUL
+        } else if (p.res == RES_MUL) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = rv[i] * v[i];
+        } else {  // RES_CAB: r1 * sigmoid(v) + r2
+            const T* r2 = (const T*)p.r2.p + (long long)b * p.r2.bstride + (long long)oy * p.r2.row +
+                          (long long)ox * p.r2.cs + p.r2.c_off + oc0;
+            const f32x4 sa = load4<T>(r2), sb = load4<T>(r2 + 4);
+            const float sv[8] = {sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float sg = sigmoidf_ref(v[i]);
+                const float t = rv[i] * sg;
+                v[i] = t + sv[i];
+            }
         }
     }
     T* y = (T*)p.y.p + (long long)b * p.y.bstride + (long long)oy * p.y.row + (long long)ox * p.y.cs + p.y.c_off + oc0;
