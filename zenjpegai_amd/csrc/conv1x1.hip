@@ -41,8 +41,9 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
-template <typename T, int WC, int WP, int CF, int PF, int NS>
-__global__ void __launch_bounds__(WC * WP * 64) conv1x1_ring(const ConvParams p) {
+template <typename T, int WC, int WP, int CF, int PF, int NS, int TP, int WPE>
+__global__ void __launch_bounds__(WC * WP * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
+conv1x1_ring(const ConvParams p) {
     constexpr int NT = WC * WP * 64;
     constexpr int NB = WC * CF;
     constexpr int MP = WP * PF * 16;
@@ -51,11 +52,13 @@ __global__ void __launch_bounds__(WC * WP * 64) conv1x1_ring(const ConvParams p)
     constexpr int A_U = NB * 64;  // one chunk of weights: [NB][64 units]
     constexpr int STG_U = B_U + A_U;
     constexpr int OUT_LD = NB * 16 + 4;
-    constexpr int OUT_U = (MP * OUT_LD + 3) / 4;
+    constexpr int PP = MP / TP;  // positions per epilogue pass
+    constexpr int OUT_U = (PP * OUT_LD + 3) / 4;
     constexpr int LDS_U = (NS * STG_U) > OUT_U ? (NS * STG_U) : OUT_U;
     constexpr int BN = B_U / NT, AN = A_U / NT;
     constexpr int L = BN + AN;  // loads per thread and chunk
     static_assert(B_U % NT == 0 && A_U % NT == 0 && NS >= 2 && (NS - 2) * L < 64, "tile");
+    static_assert(PP % 16 == 0 && MP % TP == 0, "epilogue passes cover whole 16-position blocks");
     __shared__ u32x4 s_lds[LDS_U];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -171,43 +174,50 @@ __global__ void __launch_bounds__(WC * WP * 64) conv1x1_ring(const ConvParams p)
     }
 
     // Epilogue: transpose through LDS so that consecutive threads store consecutive channels of
-    // one position.
-    __syncthreads();
+    // one position, TP passes of PP positions (a 16-position fragment lies in one pass).
     float* so = reinterpret_cast<float*>(s_lds);
-#pragma unroll
-    for (int cf = 0; cf < CF; ++cf)
-#pragma unroll
-        for (int pf = 0; pf < PF; ++pf)
-            *reinterpret_cast<f32x4*>(so + bpos[pf] * OUT_LD + (wc * CF + cf) * 16 + grp * 4) = acc[cf][pf];
-    __syncthreads();
     const int oc0 = nb0 * 16;
-    if (epilogue_simple(p)) {
-        constexpr int QP8 = NB * 2;
-#pragma unroll 4
-        for (int u = tid; u < MP * QP8; u += NT) {
-            const int pos = u / QP8, c8 = u - pos * QP8;
-            const int pg = pos0 + pos;
-            const f32x4 v0 = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + c8 * 8);
-            const f32x4 v1 = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + c8 * 8 + 4);
-            if (pg < P) {
-                const int oy = pg / p.OW, ox = pg - oy * p.OW;
-                epilogue_store8<T>(p, bi, oy, ox, oc0 + c8 * 8, v0, v1);
-            }
+    const bool simple = epilogue_simple(p);
+#pragma unroll
+    for (int pass = 0; pass < TP; ++pass) {
+        __syncthreads();
+#pragma unroll
+        for (int pf = 0; pf < PF; ++pf) {
+            if (((wp * PF + pf) * 16) / PP != pass) continue;  // uniform per wave
+#pragma unroll
+            for (int cf = 0; cf < CF; ++cf)
+                *reinterpret_cast<f32x4*>(so + (bpos[pf] - pass * PP) * OUT_LD + (wc * CF + cf) * 16 + grp * 4) =
+                    acc[cf][pf];
         }
-    } else {
-        constexpr int QP = NB * 4;
-        for (int u = tid; u < MP * QP; u += NT) {
-            const int pos = u / QP, cq = u - pos * QP;
-            const int pg = pos0 + pos;
-            if (pg >= P) continue;
-            const int oy = pg / p.OW, ox = pg - oy * p.OW;
-            const f32x4 v = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + cq * 4);
-            epilogue_store<T>(p, bi, oy, ox, oc0 + cq * 4, 4, v);
+        __syncthreads();
+        if (simple) {
+            constexpr int QP8 = NB * 2;
+#pragma unroll 4
+            for (int u = tid; u < PP * QP8; u += NT) {
+                const int pos = u / QP8, c8 = u - pos * QP8;
+                const int pg = pos0 + pass * PP + pos;
+                const f32x4 v0 = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + c8 * 8);
+                const f32x4 v1 = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + c8 * 8 + 4);
+                if (pg < P) {
+                    const int oy = pg / p.OW, ox = pg - oy * p.OW;
+                    epilogue_store8<T>(p, bi, oy, ox, oc0 + c8 * 8, v0, v1);
+                }
+            }
+        } else {
+            constexpr int QP = NB * 4;
+            for (int u = tid; u < PP * QP; u += NT) {
+                const int pos = u / QP, cq = u - pos * QP;
+                const int pg = pos0 + pass * PP + pos;
+                if (pg >= P) continue;
+                const int oy = pg / p.OW, ox = pg - oy * p.OW;
+                const f32x4 v = *reinterpret_cast<const f32x4*>(so + pos * OUT_LD + cq * 4);
+                epilogue_store<T>(p, bi, oy, ox, oc0 + cq * 4, 4, v);
+            }
         }
     }
 }
 
-template <typename T, int WC, int WP, int CF, int PF, int NS>
+template <typename T, int WC, int WP, int CF, int PF, int NS, int TP, int WPE>
 static hipError_t go_1x1(const ConvParams& p0, hipStream_t s) {
     constexpr int NB = WC * CF, MP = WP * PF * 16;
     ConvParams p = p0;
@@ -215,7 +225,8 @@ static hipError_t go_1x1(const ConvParams& p0, hipStream_t s) {
     const long long ptiles = ((long long)p.OH * p.OW + MP - 1) / MP;
     const long long total = ptiles * p.N * p.ntiles;
     if (p.nblk_g % NB || p.cout_g % (NB * 16) || total <= 0 || total > (1ll << 30)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((conv1x1_ring<T, WC, WP, CF, PF, NS>), dim3((unsigned)total), dim3(WC * WP * 64), 0, s, p);
+    hipLaunchKernelGGL((conv1x1_ring<T, WC, WP, CF, PF, NS, TP, WPE>), dim3((unsigned)total), dim3(WC * WP * 64), 0, s,
+                       p);
     return hipGetLastError();
 }
 
@@ -236,8 +247,16 @@ int conv1x1_ring_nb(const ConvParams& p) { return (p.cout_g % 128 == 0 && p.nblk
 
 template <typename T>
 static hipError_t go_1x1_t(const ConvParams& p, hipStream_t s) {
-    if (conv1x1_ring_nb(p) == 8) return go_1x1<T, 2, 2, 4, 4, 4>(p, s);  // 128 channels x 128 positions
-    return go_1x1<T, 1, 4, 4, 2, 4>(p, s);                                 // 64 channels x 128 positions
+    // f32: a ring of 4 chunks, one epilogue pass (2 workgroups per CU). 16-bit (HBM-bound): a ring
+    // of 3 and two epilogue passes, 48 KB of LDS, so 3 workgroups share a CU (bf16 128 -> 1024 on
+    // 202 500 positions 222 -> 186 us, 512 -> 128 87 -> 78 us).
+    if constexpr (sizeof(T) == 4) {
+        if (conv1x1_ring_nb(p) == 8) return go_1x1<T, 2, 2, 4, 4, 4, 1, 1>(p, s);  // 128 ch x 128 positions
+        return go_1x1<T, 1, 4, 4, 2, 4, 1, 1>(p, s);                                 // 64 ch x 128 positions
+    } else {
+        if (conv1x1_ring_nb(p) == 8) return go_1x1<T, 2, 2, 4, 4, 3, 2, 3>(p, s);
+        return go_1x1<T, 1, 4, 4, 2, 3, 2, 3>(p, s);
+    }
 }
 
 hipError_t launch_conv1x1_ring(int dtype, const ConvParams& p, hipStream_t s) {
