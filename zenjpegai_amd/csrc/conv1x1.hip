@@ -247,16 +247,18 @@ int conv1x1_ring_nb(const ConvParams& p) { return (p.cout_g % 128 == 0 && p.nblk
 
 template <typename T>
 static hipError_t go_1x1_t(const ConvParams& p, hipStream_t s) {
-    // A ring of 3 chunks and two epilogue passes: 48 KB of LDS and <= 168 registers, so 3
-    // workgroups share a CU and cover each other's prologue and epilogue (against a ring of 4
-    // and one pass, 2 workgroups per CU, on 202 500 positions: f32 128 -> 1024 664 -> 617 us,
-    // 128 -> 384 268 -> 239 us; bf16 128 -> 1024 223 -> 183 us, 512 -> 128 85 -> 77 us).
+    // Co-resident workgroups cover each other's prologue and epilogue. f32: a ring of 3 chunks and
+    // two epilogue passes (48 KB of LDS, <= 168 registers: 3 workgroups per CU); 16-bit, whose
+    // layers are HBM-bound: a ring of 2 and four passes (32 KB, <= 128 registers: 4 per CU).
+    // Against a ring of 4 and one pass (2 per CU) on 202 500 positions: f32 128 -> 1024 664 ->
+    // 617 us, 128 -> 384 268 -> 239 us; bf16 128 -> 1024 223 -> 172 us, 512 -> 128 85 -> 74 us,
+    // 128 -> 384 76 -> 55 us (4 per CU: f32 no better, bf16 a further 7-10 %).
     if constexpr (sizeof(T) == 4) {
         if (conv1x1_ring_nb(p) == 8) return go_1x1<T, 2, 2, 4, 4, 3, 2, 3>(p, s);  // 128 ch x 128 positions
         return go_1x1<T, 1, 4, 4, 2, 3, 2, 3>(p, s);                                 // 64 ch x 128 positions
     } else {
-        if (conv1x1_ring_nb(p) == 8) return go_1x1<T, 2, 2, 4, 4, 3, 2, 3>(p, s);
-        return go_1x1<T, 1, 4, 4, 2, 3, 2, 3>(p, s);
+        if (conv1x1_ring_nb(p) == 8) return go_1x1<T, 2, 2, 4, 4, 2, 4, 4>(p, s);
+        return go_1x1<T, 1, 4, 4, 2, 2, 4, 4>(p, s);
     }
 }
 
