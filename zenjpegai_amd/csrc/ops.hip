@@ -323,71 +323,122 @@ __global__ void __launch_bounds__(256) k_layer_norm(View src, View dst, int N, i
 
 // ------------------------------------------------------------------------ channel attention
 // Per head h (c = dim / heads channels): S_ij = q_i . k_j, |q_i|^2 and |k_j|^2 summed over the
-// n = h*w positions. One wave per head per chunk of ATT_POS positions runs the sums on f32
-// MFMA (M = q channels, N = k channels, K = 4 positions per instruction); the chunk partials
-// are reduced in f64 by the softmax kernel.
+// n = h*w positions. One wave per head per chunk of ATT_POS positions runs the q . k sums on
+// f32 MFMA (M = q channels, N = k channels, K = 4 positions per instruction) and the squared
+// norms on f32 fma; the chunk partials are reduced in f64 by the softmax kernel.
 constexpr int ATT_POS = 256;
-// Position groups loaded per trip of the Gram loop: 4 for f32 (68 -> 52 us on config 5's TAM
-// maps); the 16-bit loads measured slower batched (58 -> 65 us) and keep one group per trip.
-template <typename T>
-constexpr int att_u() {
-    return sizeof(T) == 4 ? 4 : 1;
-}
-
 int attention_gram_chunks(int h, int w) { return (h * w + ATT_POS - 1) / ATT_POS; }
 
+// The chunk's q and k (the first 2 dim channels of qkv) pass through LDS, 32 KB of positions at
+// a time (GRAM_SUB<T> = 32 f32 or 64 16-bit positions of 2 dim = 256 channels), as stored: every
+// global load is a coalesced 16-byte read of a position's channel run, and the MFMA fragments
+// are read from LDS and widened to f32 there. Wave w takes head h0 + w of each group of four heads
+// (the synthesis nets have four: one group). The q . k sums run on MFMA in groups of 4 positions
+// (a partial last group padded with zeros); |q_i|^2 and |k_j|^2 are f32 fmas in the lane that
+// holds the element (lane l takes positions congruent to l / 16 mod 4), added across the four
+// lane groups at the end. 35 KB of LDS per workgroup: four per CU overlap one another's loads
+// and sums. An LDS row is 2 dim + 16 elements: at dim 128 the four position rows a wave reads
+// fall on disjoint banks.
 template <typename T>
-__global__ void __launch_bounds__(256) k_attention_gram(View qkv, int dim, int heads, int n, int w,
-                                                        float* partial) {
+constexpr int GRAM_SUB = 128 / (int)sizeof(T);
+constexpr int GRAM_PAD = 16;
+
+template <typename T>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+k_attention_gram(View qkv, int dim, int heads, int n, int w, float* partial) {
+    extern __shared__ __align__(16) unsigned char s_raw[];
+    T* s_qk = reinterpret_cast<T*>(s_raw);  // [GRAM_SUB][2 dim + GRAM_PAD]
+    constexpr int VEC = 16 / (int)sizeof(T), SUB = GRAM_SUB<T>;
     const int c = dim / heads, nb = (c + 15) / 16, E = c * c + 2 * c;
+    const int ld = 2 * dim + GRAM_PAD, upp = 2 * dim / VEC;  // LDS row; 16-byte units per position
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m = lane & 15, kq = lane >> 4;
     const int b = blockIdx.y, nchunk = gridDim.x;
     const int p0 = blockIdx.x * ATT_POS;
     const int p1 = min(p0 + ATT_POS, n);
     const T* base = (const T*)qkv.p + (long long)b * qkv.bstride + qkv.c_off;
-    for (int hd = wave; hd < heads; hd += 4) {
-        f32x4 g[2][2], dq[2], dk[2];
-        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Staging: up to UNR 16-byte loads per thread in flight before the first wait. When a
+    // sub-chunk is one round of them (units <= UNR * 256: dim <= 128), positions are dense
+    // (row = w * cs) and upp divides 256, thread t's unit is t % upp of positions t / upp + k * pst
+    // of the sub-chunk, k < UNR (pst = 256 / upp): fixed offsets, computed once.
+    constexpr int UNR = 8;
+    const int units = SUB * upp;
+    const bool fast = units <= UNR * 256 && qkv.row == (long long)w * qkv.cs && 256 % upp == 0;
+    const int pst = fast ? 256 / upp : 0, fpl = fast ? threadIdx.x / upp : 0;
+    const int fq = threadIdx.x - fpl * upp;
+    const int fg = fpl * qkv.cs + fq * VEC, fs = fpl * ld + fq * VEC;
+    for (int h0 = 0; h0 < heads; h0 += 4) {
+        const int hd = h0 + wave;  // a wave past the last head only stages
+        f32x4 g[2][2] = {{z, z}, {z, z}};
+        float sq[2] = {0.0f, 0.0f}, sk[2] = {0.0f, 0.0f};
+        for (int ps = p0; ps < p1; ps += SUB) {
+            const int pe = min(ps + SUB, p1);
+            __syncthreads();  // the previous sub-chunk's reads are done
+            if (fast) {
+                const T* bp = base + (long long)ps * qkv.cs + fg;
+                const int np = pe - ps;
+                u32x4 raw[UNR];
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
-            dq[a] = dk[a] = z;
-            g[a][0] = g[a][1] = z;
-        }
-        // ATT_U groups of 4 positions per trip: all their loads issue before the first MFMA, so
-        // the loads of a trip overlap; the MFMAs then run group by group in position order.
-        constexpr int ATT_U = att_u<T>();
-        for (int p = p0; p < p1; p += 4 * ATT_U) {
-            float aq[ATT_U][2], ak[ATT_U][2];
+                for (int k = 0; k < UNR; ++k) {
+                    raw[k] = u32x4{0u, 0u, 0u, 0u};
+                    if (fpl + k * pst < np) raw[k] = *(const u32x4*)(bp + k * pst * qkv.cs);
+                }
 #pragma unroll
-            for (int u = 0; u < ATT_U; ++u) {
-                aq[u][0] = aq[u][1] = ak[u][0] = ak[u][1] = 0.0f;
-                const int pos = p + 4 * u + kq;
-                if (pos < p1) {
-                    const int y = pos / w, x = pos - y * w;
-                    const T* px = base + (long long)y * qkv.row + (long long)x * qkv.cs + hd * c + m;
+                for (int k = 0; k < UNR; ++k)
+                    if (fpl + k * pst < SUB) *reinterpret_cast<u32x4*>(s_qk + fs + k * pst * ld) = raw[k];
+            } else {
+                for (int u0 = threadIdx.x; u0 < units; u0 += UNR * 256) {
+                    u32x4 raw[UNR];
 #pragma unroll
-                    for (int bb = 0; bb < 2; ++bb)
-                        if (bb * 16 + m < c) {
-                            aq[u][bb] = to_f32(px[bb * 16]);
-                            ak[u][bb] = to_f32(px[dim + bb * 16]);
+                    for (int k = 0; k < UNR; ++k) {
+                        const int u = u0 + k * 256;
+                        const int pl = u / upp, pos = ps + pl;
+                        raw[k] = u32x4{0u, 0u, 0u, 0u};
+                        if (u < units && pos < pe) {
+                            const int y = pos / w, x = pos - y * w, q = u - pl * upp;
+                            raw[k] = *(const u32x4*)(base + (long long)y * qkv.row + (long long)x * qkv.cs + q * VEC);
                         }
+                    }
+#pragma unroll
+                    for (int k = 0; k < UNR; ++k) {
+                        const int u = u0 + k * 256;
+                        if (u >= units) break;
+                        const int pl = u / upp, q = u - pl * upp;
+                        *reinterpret_cast<u32x4*>(s_qk + pl * ld + q * VEC) = raw[k];
+                    }
                 }
             }
+            __syncthreads();
+            if (hd >= heads) continue;  // uniform per wave
+            for (int p = ps; p < pe; p += 4) {
+                float aq[2], ak[2];
+                const T* r = s_qk + (p - ps + kq) * ld + hd * c + m;
+                const bool ok = p + kq < pe;
 #pragma unroll
-            for (int u = 0; u < ATT_U; ++u) {
-                if (p + 4 * u >= p1) break;  // uniform: the groups of the one-position-at-a-time loop
+                for (int bb = 0; bb < 2; ++bb) {
+                    const bool in = ok && bb * 16 + m < c;
+                    aq[bb] = in ? (float)r[bb * 16] : 0.0f;
+                    ak[bb] = in ? (float)r[dim + bb * 16] : 0.0f;
+                    sq[bb] = fmaf(aq[bb], aq[bb], sq[bb]);
+                    sk[bb] = fmaf(ak[bb], ak[bb], sk[bb]);
+                }
 #pragma unroll
                 for (int bi = 0; bi < 2; ++bi) {
                     if (bi >= nb) continue;
 #pragma unroll
                     for (int bj = 0; bj < 2; ++bj)
-                        if (bj < nb)
-                            g[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[u][bi], ak[u][bj], g[bi][bj], 0, 0, 0);
-                    dq[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[u][bi], aq[u][bi], dq[bi], 0, 0, 0);
-                    dk[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(ak[u][bi], ak[u][bi], dk[bi], 0, 0, 0);
+                        if (bj < nb) g[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[bi], ak[bj], g[bi][bj], 0, 0, 0);
                 }
             }
+        }
+        if (hd >= heads) continue;
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+            sq[bb] += __shfl_xor(sq[bb], 16);
+            sq[bb] += __shfl_xor(sq[bb], 32);
+            sk[bb] += __shfl_xor(sk[bb], 16);
+            sk[bb] += __shfl_xor(sk[bb], 32);
         }
         // Lane l holds D[4 * (l / 16) + i][l % 16] of each 16x16 tile.
         float* out = partial + (((long long)b * nchunk + blockIdx.x) * heads + hd) * E;
@@ -401,10 +452,10 @@ __global__ void __launch_bounds__(256) k_attention_gram(View qkv, int dim, int h
 #pragma unroll
                 for (int bj = 0; bj < 2; ++bj)
                     if (bj < nb && bj * 16 + m < c) out[(bi * 16 + r) * c + bj * 16 + m] = g[bi][bj][i];
-                if (r == m) {
-                    out[c * c + bi * 16 + m] = dq[bi][i];
-                    out[c * c + c + bi * 16 + m] = dk[bi][i];
-                }
+            }
+            if (kq == 0 && bi * 16 + m < c) {
+                out[c * c + bi * 16 + m] = sq[bi];
+                out[c * c + c + bi * 16 + m] = sk[bi];
             }
         }
     }
@@ -598,10 +649,15 @@ hipError_t launch_layer_norm(View src, View dst, int dtype, int N, int C, int h,
 hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads, int h, int w,
                                  float* partial, hipStream_t s) {
     const int c = heads > 0 ? dim / heads : 0;
-    if (heads <= 0 || dim % heads || c < 1 || c > 32) return hipErrorInvalidValue;
+    const int vec = dtype == DT_F32 ? 4 : 8;
+    if (heads <= 0 || dim % heads || c < 1 || c > 32 || (2 * dim) % vec || qkv.cs % vec ||
+        qkv.c_off % vec || qkv.row % vec || qkv.bstride % vec || (uintptr_t)qkv.p % 16)
+        return hipErrorInvalidValue;
     const int nchunk = attention_gram_chunks(h, w);
     if (nchunk == 0 || N == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_attention_gram, <<<dim3(nchunk, N), 256, 0, s>>>(qkv, dim, heads, h * w, w, partial))
+    const size_t lds = (size_t)(dtype == DT_F32 ? 4 * GRAM_SUB<float> : 2 * GRAM_SUB<__bf16>) * (2 * dim + GRAM_PAD);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    ZJAI_DISPATCH(dtype, k_attention_gram, <<<dim3(nchunk, N), 256, lds, s>>>(qkv, dim, heads, h * w, w, partial))
     return hipGetLastError();
 }
 
