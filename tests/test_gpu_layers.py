@@ -238,6 +238,100 @@ def test_conv1x1_kernels_are_bit_identical(engines, prec, cin, cout, h, w, op, c
     np.testing.assert_array_equal(got[0], got[1])
 
 
+# Launch-time tile choice: (kind, cin, cout, small input h x w, large input side, expected
+# kernel family on the small map). The small maps' grids are below the workgroup thresholds (narrow
+# 32- / 16-channel tiles, phase-split transposed conv); the large map is the same input embedded
+# top-left in zeros, whose grid takes the layer's own tile or the merged transposed kernel.
+SMALL_GRID_CASES = [
+    ("3x3", 192, 192, 24, 40, 256, "conv_igemm"),
+    ("3x3", 192, 192, 80, 96, 256, "conv_igemm"),
+    ("s2", 192, 192, 48, 80, 256, "conv_igemm"),
+    ("convT", 192, 192, 20, 24, 160, "conv_igemm"),
+    ("convT", 192, 192, 80, 80, 160, "conv_igemm"),
+]
+
+
+@pytest.mark.parametrize("prec", ["f32", "bf16"])
+@pytest.mark.parametrize("kind,cin,cout,h,w,big,small_kernel", SMALL_GRID_CASES)
+def test_small_grid_tiles_are_bit_identical(engines, prec, kind, cin, cout, h, w, big, small_kernel):
+    """A layer whose tile grid is small takes narrower tiles (or the phase-split transposed
+    kernel) at launch; every tile shape sums each output in the same order, so the small map's
+    output equals, bit for bit, the matching region of the same map embedded top-left in a large
+    zero map (whose padding is the same zeros), which runs on the layer's default kernel."""
+    eng = engines[prec]
+    x = synth.uniform(11, f"sg/x{kind}{h}", (cin, h, w), -1, 1)
+    xb = np.zeros((cin, big, big), np.float32)
+    xb[:, :h, :w] = x
+    if kind == "convT":
+        wt = _he(f"sg/w{kind}", (cin, cout, 3, 3), 9 * cin)
+        layer = nn.ConvTransposeLayer(nn.ConvTranspose2d(cin, cout, 3, 2, 1, 1, wt, synth.normal(11, "sg/bt", (cout,), 0.05)), eng)
+        oh, ow = 2 * h, 2 * w
+    else:
+        stride = 2 if kind == "s2" else 1
+        wt = _he(f"sg/w{kind}", (cout, cin, 3, 3), 9 * cin)
+        layer = nn.ConvLayer(nn.Conv2d(cin, cout, (3, 3), stride, (1, 1), 1, wt, synth.normal(11, "sg/b", (cout,), 0.05)), eng)
+        oh, ow = (h - 1) // stride + 1, (w - 1) // stride + 1
+    outs, kernels = [], []
+    for xin in (x, xb):
+        xt = nn.BTensor.from_planar(eng, xin)
+        eng.sync()
+        eng.profile_begin()
+        y = layer.forward(eng, xt)
+        kernels.append([r[0] for r in eng.profile_end()][-1])
+        outs.append(y.to_planar())
+    print(f"{prec} {kind} {cin}->{cout} {h}x{w}: {kernels}")
+    assert kernels[0].startswith(small_kernel) and kernels[0] != kernels[1], kernels
+    assert outs[0].shape == (cout, oh, ow)
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1][:, :oh, :ow].view(np.uint32))
+
+
+# (cin, cout, input side, epilogue): maps whose merged grid has >= 256 workgroups, with the
+# epilogues the synthesis nets put on 3x3 transposed convs (CAB upscale: RES_CAB, r1 * sigmoid(v) + r2).
+CONVT_MERGED_CASES = [(160, 128, 192, "none"), (128, 128, 200, "cab"), (128, 64, 256, "add"),
+                      (128, 128, 192, "leaky")]
+
+
+@pytest.mark.parametrize("prec", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("cin,cout,side,epi", CONVT_MERGED_CASES)
+def test_merged_transposed_conv_is_bit_identical_to_phase_split(engines, prec, cin, cout, side, epi):
+    """conv_tr_merged (all four output phases per workgroup) against the phase-split kernel
+    (ZJAI_CTX_PHASE_SPLIT_CONVT) on maps large enough for the merged kernel to be chosen: the same
+    bits for every epilogue, and the merged output meets the oracle at the layer tolerance on the
+    region a 17 x 17 input window determines."""
+    x = synth.uniform(12, f"tm/x{cin}{side}", (cin, side, side - 8), -1, 1)
+    wt = _he(f"tm/w{cin}{cout}", (cin, cout, 3, 3), 9 * cin)
+    b = synth.normal(12, f"tm/b{cout}", (cout,), 0.05)
+    oh, ow = 2 * side, 2 * (side - 8)
+    r1 = synth.uniform(13, f"tm/r1{cout}{side}", (cout, oh, ow), -1, 1)
+    r2 = synth.uniform(14, f"tm/r2{cout}{side}", (cout, oh, ow), -1, 1)
+    split = nn.Engine(0, prec, flags=_lib.CTX_PHASE_SPLIT_CONVT)
+    outs = []
+    for eng, merged in ((engines[prec], True), (split, False)):
+        layer = nn.ConvTransposeLayer(nn.ConvTranspose2d(cin, cout, 3, 2, 1, 1, wt, b), eng)
+        kw = {"none": {}, "leaky": dict(act=_lib.ACT_LEAKY_RELU),
+              "add": dict(res=_lib.RES_ADD, r1=nn.BTensor.from_planar(eng, r1)),
+              "cab": dict(res=_lib.RES_CAB, r1=nn.BTensor.from_planar(eng, r1), r2=nn.BTensor.from_planar(eng, r2))}[epi]
+        xt = nn.BTensor.from_planar(eng, x)
+        eng.sync()
+        eng.profile_begin()
+        y = layer.forward_fused(eng, xt, **kw)
+        names = [r[0] for r in eng.profile_end()]
+        is_merged = names[-1].startswith("conv_tr_merged<")
+        assert is_merged == merged and (merged or "3, 3, 1, true," in names[-1]), names
+        outs.append(y.to_planar())
+    split.close()
+    # Oracle on the top-left 17 x 17 inputs: output rows / cols < 32 depend on no other input.
+    base = oracle.conv_transpose2d(np.ascontiguousarray(x[:, :17, :17]), wt, b, 2, 1, 1)[:, :32, :32]
+    q1, q2 = r1[:, :32, :32], r2[:, :32, :32]
+    want = {"none": base, "leaky": oracle.leaky_relu(base),
+            "add": oracle.add(base, np.ascontiguousarray(q1)),
+            "cab": oracle.add(oracle.mul(np.ascontiguousarray(q1), oracle.sigmoid(base)), np.ascontiguousarray(q2))}[epi]
+    err = rel_err(outs[0][:, :32, :32], want)
+    print(f"{prec} convT {cin}->{cout} {side} {epi}: {err:.2e}")
+    assert err <= TOL[prec]
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("prec", ["f32", "bf16"])
 def test_config2_convt4_leaky(engines, prec):
     """BASELINE config 2 at full size: ConvT k4 s2 p1 192->128, 64^2 -> 128^2, then

@@ -437,6 +437,45 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
 
 // ------------------------------------------------------------------------------ conv launch
 // The kernel's name as profilers print it: conv_igemm<T, KH, KW, S, TR, WC, WP, CF, PF>.
+// Launch-time tile shape of a dense layer. The layer's own shape (64 channels x 16 or 8 rows)
+// suits large maps; on small ones its grid leaves most of the 256 CUs idle while each workgroup
+// walks the whole K loop, so narrower tiles (32 or 16 channels x 8 rows; the weights are packed
+// per 16-channel block, so any of them reads the same packing) take over below a workgroup
+// count. Every shape sums each output in the same order (bias, then K chunk by chunk, tap by
+// tap), so the choice never changes a result. Thresholds from the per-layer sweep (fp32 /
+// 16-bit): 3x3 192 -> 192 at 40 x 80 runs 112 -> 44 us / 25 -> 17 us; at 256^2 and 128 channels
+// (512 tiles) the 16-row tile stays fastest.
+static TileCfg launch_tile_cfg(const Layer& L, int N, int OH, int OW) {
+    const TileCfg c = L.cfg;
+    if (L.groups != 1) return c;
+    const long long nt4 = L.nblk_g / 4;
+    if (L.kind == CK_3x3 && c.wc == 2 && c.wp == 4 && c.cf == 2 && c.pf == 4) {
+        const long long w0 = (long long)((OW + 15) / 16) * ((OH + 15) / 16) * N * nt4;
+        if (L.dtype == DT_F32) return w0 < 256 ? TileCfg{1, 4, 1, 2} : c;
+        return w0 < 64 ? TileCfg{1, 4, 1, 2} : w0 < 256 ? TileCfg{1, 4, 2, 2} : c;
+    }
+    if (L.kind == CK_3x3_S2 && c.wc == 2 && c.wp == 2 && c.cf == 2 && c.pf == 4) {
+        const long long w0 = (long long)((OW + 15) / 16) * ((OH + 7) / 8) * N * nt4;
+        return w0 < 128 ? TileCfg{1, 4, 1, 2} : c;
+    }
+    if (L.kind == CK_T3 && L.wpk_m && c.wc == 2 && c.wp == 2 && c.cf == 2 && c.pf == 4) {
+        // 3x3 transposed layers whose merged grid is small (see convT_merged_fills).
+        const long long wm = (long long)(((OW + 1) / 2 + 15) / 16) * (((OH + 1) / 2 + 15) / 16) * N * nt4;
+        return wm < 64 ? TileCfg{1, 4, 1, 2} : wm < 256 ? TileCfg{1, 4, 2, 2} : c;
+    }
+    return c;
+}
+
+// Transposed 3x3 layers take the merged four-phase kernel when its grid (16 x 16 phase positions
+// x 64 channels per workgroup) has at least 256 workgroups, else the phase-split kernel on a
+// narrow tile: 192 -> 192 from 40^2 runs 119 -> 38 us (fp32), from 80^2 125 -> 88 us; from 160^2
+// the merged kernel is faster (257 vs 304 us).
+static bool convT_merged_fills(const Layer& L, int N, int OH, int OW) {
+    const long long wm = (long long)(((OW + 1) / 2 + 15) / 16) * (((OH + 1) / 2 + 15) / 16) * N *
+                         (L.nblk_g / TR_MERGED_NB);
+    return wm >= 256;
+}
+
 std::string conv_kernel_name(int kind, int dtype, TileCfg c) {
     static const char* geo[] = {"1, 1, 1, false", "2, 2, 1, false", "3, 3, 1, false", "3, 3, 2, false",
                                 "3, 3, 1, true"};
@@ -567,7 +606,7 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
         ZJAI_HIP(launch_convT_narrow(L.dtype, L.coutp, p, L.wn, L.cin, ctx.stream));
         return y;
     }
-    if (L.wpk_m && !e.w_batch && !plane && ps == 1 && !e.relu6_in &&
+    if (L.wpk_m && !e.w_batch && !plane && ps == 1 && !e.relu6_in && convT_merged_fills(L, N, OH, OW) &&
         !(ctx.top().flags & ZJAI_CTX_PHASE_SPLIT_CONVT)) {
         static const char* ty[] = {"float", "_Float16", "__bf16"};
         p.w = L.wpk_m;
@@ -602,8 +641,10 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
         ZJAI_HIP(launch_conv1x1_ring(L.dtype, p, ctx.stream));
         return y;
     }
-    LaunchScope sc(ctx, conv_kernel_name(L.kind, L.dtype, L.cfg), 2.0 * macs, bytes);
-    ZJAI_HIP(launch_conv(L.kind, L.dtype, L.cfg, p, ctx.stream));
+    const TileCfg cfg = launch_tile_cfg(L, N, OH, OW);
+    p.ntiles = L.groups * L.nblk_g / (cfg.wc * cfg.cf);
+    LaunchScope sc(ctx, conv_kernel_name(L.kind, L.dtype, cfg), 2.0 * macs, bytes);
+    ZJAI_HIP(launch_conv(L.kind, L.dtype, cfg, p, ctx.stream));
     return y;
 }
 
