@@ -561,6 +561,20 @@ def test_attention_one_position_kat(engines):
     assert got[0:2, 0, 0].tolist() == [15.0, 15.0]
 
 
+@pytest.mark.parametrize("prec", ["f32", "bf16"])
+def test_new_tensors_are_zero_at_any_byte_size(engines, prec):
+    """zjai_tensor_create clears its buffer with the zero-fill kernel (no hipMemsetAsync, so a
+    capturing caller may create tensors), on odd map sizes too. The first tensor's nonzero buffer
+    goes back to the pool and is handed out again to the second."""
+    eng = engines[prec]
+    for c, h, w in ((4, 5, 7), (8, 3, 3), (4, 1, 1)):
+        t = nn.BTensor.from_planar(eng, np.full((c, h, w), 3.0, np.float32))
+        del t
+        eng.sync()
+        z = nn.BTensor.zeros(eng, c, h, w)
+        assert not np.any(z.to_planar()), (c, h, w)
+
+
 def test_tensors_and_layers_may_outlive_their_context():
     """Destroying the context first is allowed: tensors return their blocks to the pool they
     share with it (which lives until the last of them), layers free their own weights."""

@@ -233,7 +233,7 @@ extern "C" int32_t zjai_tensor_create(zjai_ctx* ctx, int32_t c, int32_t h, int32
         need(precision >= DT_F32 && precision <= DT_BF16, "precision");
         need(c > 0 && h > 0 && w > 0, "bad shape");
         TensorP t = ctx->c.alloc(1, c, h, w, precision);
-        ZJAI_HIP(hipMemsetAsync(t->v.p, 0, (size_t)t->v.bstride * dtype_size(precision), ctx->c.stream));
+        ZJAI_HIP(launch_zero(t->v.p, (size_t)t->v.bstride * dtype_size(precision), ctx->c.stream));
         *out = new zjai_tensor{t};
     });
 }

@@ -549,20 +549,26 @@ __global__ void k_attention_fold(const float* proj, const float* attn, int dim, 
 }
 
 // Zero fill with vector stores (instead of hipMemsetAsync, which callers capturing the stream
-// into a HIP graph cannot rely on).
-__global__ void k_zero_u32(uint32_t* p, long long n) {
+// into a HIP graph cannot rely on): n 4-byte words, then `tail` (< 4) bytes after them.
+__global__ void k_zero_u32(uint32_t* p, long long n, int tail) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0u;
+    if (i < n) {
+        p[i] = 0u;
+    } else if (i == n) {
+        unsigned char* t = reinterpret_cast<unsigned char*>(p + n);
+        for (int k = 0; k < tail; ++k) t[k] = 0;
+    }
 }
 
 // ------------------------------------------------------------------------------- launchers
 static inline dim3 grid_for(long long n) { return dim3((unsigned)((n + 255) / 256)); }
 
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s) {
-    if (bytes % 4 || ((uintptr_t)p & 3)) return hipErrorInvalidValue;
+    if ((uintptr_t)p & 3) return hipErrorInvalidValue;
     const long long n = (long long)(bytes / 4);
-    if (n == 0) return hipSuccess;
-    k_zero_u32<<<grid_for(n), 256, 0, s>>>((uint32_t*)p, n);
+    const int tail = (int)(bytes % 4);
+    if (bytes == 0) return hipSuccess;
+    k_zero_u32<<<grid_for(n + (tail ? 1 : 0)), 256, 0, s>>>((uint32_t*)p, n, tail);
     return hipGetLastError();
 }
 

@@ -119,8 +119,8 @@ void reconstruct_latent(Context& ctx, const Net& net, int height, int width, con
     DevBuf zdev(ctx, zn), rdev(ctx, rn * 4), psi(ctx, pn * 4), yhat(ctx, rn * 4);
     ZJAI_HIP(hipMemcpyAsync(zdev.p, z_hat, zn, hipMemcpyHostToDevice, ctx.stream));
     ZJAI_HIP(hipMemcpyAsync(rdev.p, residual, rn * 4, hipMemcpyHostToDevice, ctx.stream));
-    ZJAI_HIP(hipMemsetAsync(psi.p, 0, pn * 4, ctx.stream));
-    ZJAI_HIP(hipMemsetAsync(yhat.p, 0, rn * 4, ctx.stream));
+    ZJAI_HIP(launch_zero(psi.p, pn * 4, ctx.stream));
+    ZJAI_HIP(launch_zero(yhat.p, rn * 4, ctx.stream));
 
     // Regions of one shape run as one batch (up to MAXB) through each network; the results are
     // merged region by region in raster order afterwards, so where extended regions overlap the

@@ -666,7 +666,7 @@ std::shared_ptr<void> attention_fold(Context& ctx, const TensorP& qkv, int heads
     *w_bstride = (long long)(proj.wpk_bytes / dtype_size(proj.dtype));
     const int CK = 64 / dtype_size(proj.dtype);
     if (proj.nblk_g * 16 != dim || proj.nchunks * CK != dim)  // padded rows / columns stay zero
-        ZJAI_HIP(hipMemsetAsync(wfold, 0, proj.wpk_bytes * N, ctx.stream));
+        ZJAI_HIP(launch_zero(wfold, proj.wpk_bytes * N, ctx.stream));
     {
         LaunchScope sc(ctx, kname("k_attention_gram", qkv->dtype), 2.0 * N * total * n, es * N * 2 * dim * n + 4.0 * N * nchunk * total);
         ZJAI_HIP(launch_attention_gram(qkv->v, qkv->dtype, N, dim, heads, qkv->h, qkv->w, partial, ctx.stream));
