@@ -33,6 +33,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <memory>
 #include <vector>
 
 extern "C" int or_conv2d(const float* x, int c, int h, int w, const float* weight, const float* bias,
@@ -138,25 +139,57 @@ void dispatch(int V, const Row& r) {
     else run_row8(r);
 }
 
-// planar [c][h][w] -> NCHWc [ceil(c/V)][h][w][V] with left/top/right/bottom zero borders.
-std::vector<float> to_blocked(const float* x, int c, int h, int w, int V, int pt, int pl, int pb, int pr) {
+// An uninitialised float buffer (every element is written before it is read).
+struct FBuf {
+    std::unique_ptr<float[]> p;
+    explicit FBuf(size_t n) : p(new float[n]) {}
+    float* data() { return p.get(); }
+    const float* data() const { return p.get(); }
+};
+
+// planar [c][h][w] -> NCHWc [ceil(c/V)][h][w][V] with left/top/right/bottom zero borders. One
+// (block, padded row) per iteration: V contiguous source rows into one contiguous destination
+// row, so no cache line is fetched more than once.
+FBuf to_blocked(const float* x, int c, int h, int w, int V, int pt, int pl, int pb, int pr) {
     const int nb = (c + V - 1) / V, ph = h + pt + pb, pw = w + pl + pr;
-    std::vector<float> o((size_t)nb * ph * pw * V, 0.0f);
-#pragma omp parallel for
-    for (int ch = 0; ch < c; ++ch) {
-        float* d = o.data() + (size_t)(ch / V) * ph * pw * V + ch % V;
-        for (int yy = 0; yy < h; ++yy)
-            for (int xx = 0; xx < w; ++xx) d[((size_t)(yy + pt) * pw + xx + pl) * V] = x[((size_t)ch * h + yy) * w + xx];
-    }
+    FBuf o((size_t)nb * ph * pw * V);
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < nb; ++b)
+        for (int r = 0; r < ph; ++r) {
+            float* d = o.data() + ((size_t)b * ph + r) * pw * V;
+            const int yy = r - pt;
+            if (yy < 0 || yy >= h) {
+                std::memset(d, 0, sizeof(float) * pw * V);
+                continue;
+            }
+            std::memset(d, 0, sizeof(float) * pl * V);
+            std::memset(d + (size_t)(pl + w) * V, 0, sizeof(float) * pr * V);
+            for (int v = 0; v < V; ++v) {
+                const int ch = b * V + v;
+                float* dv = d + (size_t)pl * V + v;
+                if (ch >= c) {
+                    for (int xx = 0; xx < w; ++xx) dv[(size_t)xx * V] = 0.0f;
+                    continue;
+                }
+                const float* s = x + ((size_t)ch * h + yy) * w;
+                for (int xx = 0; xx < w; ++xx) dv[(size_t)xx * V] = s[xx];
+            }
+        }
     return o;
 }
 
+// NCHWc -> planar, one (block, row) per iteration as in to_blocked.
 void from_blocked(const float* o, int c, int h, int w, int V, float* y) {
-#pragma omp parallel for
-    for (int ch = 0; ch < c; ++ch) {
-        const float* s = o + (size_t)(ch / V) * h * w * V + ch % V;
-        for (size_t i = 0; i < (size_t)h * w; ++i) y[(size_t)ch * h * w + i] = s[i * V];
-    }
+    const int nb = (c + V - 1) / V;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < nb; ++b)
+        for (int yy = 0; yy < h; ++yy) {
+            const float* s = o + ((size_t)b * h + yy) * w * V;
+            for (int v = 0; v < V && b * V + v < c; ++v) {
+                float* d = y + ((size_t)(b * V + v) * h + yy) * w;
+                for (int xx = 0; xx < w; ++xx) d[xx] = s[(size_t)xx * V + v];
+            }
+        }
 }
 
 // [oc][ic][t] accessor -> [ocb][icb][V in][t][V out].
@@ -164,6 +197,7 @@ template <typename F>
 std::vector<float> pack(int V, int out_ch, int in_ch, int nt, F get) {
     const int ocb = (out_ch + V - 1) / V, icb = (in_ch + V - 1) / V;
     std::vector<float> w((size_t)ocb * icb * V * nt * V, 0.0f);
+#pragma omp parallel for schedule(static)
     for (int oc = 0; oc < out_ch; ++oc)
         for (int ic = 0; ic < in_ch; ++ic)
             for (int t = 0; t < nt; ++t)
@@ -252,7 +286,7 @@ int fc_conv2d(const float* x, int c, int h, int w, const float* weight, const fl
     const int ph = h + pt + pb, pw = w + pl + pr;
     if (ph < kh || pw < kw) return -1;
     const int oh = (ph - kh) / stride + 1, ow = (pw - kw) / stride + 1;
-    const std::vector<float> xb = to_blocked(x, c, h, w, V, pt, pl, pb, pr);
+    const FBuf xb = to_blocked(x, c, h, w, V, pt, pl, pb, pr);
     // Per group, packed weights [ocb][icb][V][nt][V] and bias.
     std::vector<std::vector<float>> wp(groups);
     for (int g = 0; g < groups; ++g)
@@ -261,7 +295,7 @@ int fc_conv2d(const float* x, int c, int h, int w, const float* weight, const fl
         });
     const std::vector<float> bp = pack_bias(V, out_ch, bias);
     const int icbg = (icg + V - 1) / V, ocbg = (ocg + V - 1) / V, ocb = (out_ch + V - 1) / V;
-    std::vector<float> yb((size_t)ocb * oh * ow * V);
+    FBuf yb((size_t)ocb * oh * ow * V);
     const long wlen = (long)icbg * V * nt * V;
 #pragma omp parallel
     {
@@ -300,7 +334,7 @@ int fc_conv_transpose2d(const float* x, int c, int h, int w, const float* weight
     const int EXT = 2;
     const int oh = (h - 1) * 2 + k + out_pad - 2 * pad, ow = (w - 1) * 2 + k + out_pad - 2 * pad;
     const int ph = h + 2 * EXT, pw = w + 2 * EXT;
-    const std::vector<float> xb = to_blocked(x, c, h, w, V, EXT, EXT, EXT, EXT);
+    const FBuf xb = to_blocked(x, c, h, w, V, EXT, EXT, EXT, EXT);
     // Phase (row parity a, column parity b) of ky / kx: the taps with ky % 2 == a, kx % 2 == b,
     // ascending, (ky, kx) order; weights [in][out][k][k].
     std::vector<int> kys[2], kxs[2];
@@ -319,7 +353,7 @@ int fc_conv_transpose2d(const float* x, int c, int h, int w, const float* weight
         }
     const std::vector<float> bp = pack_bias(V, out_ch, bias);
     const int icb = (c + V - 1) / V, ocb = (out_ch + V - 1) / V;
-    std::vector<float> yb((size_t)ocb * oh * ow * V);
+    FBuf yb((size_t)ocb * oh * ow * V);
 #pragma omp parallel
     {
         // Per tap, the input row read by this output row, gathered as a strip [icb][tap][n][V].
