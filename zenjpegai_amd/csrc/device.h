@@ -95,8 +95,10 @@ __device__ __forceinline__ float cephes_exp(float x) {
     float y = p * (r * r);
     y = y + r;
     y = y + 1.0f;
-    const int ni = (n != n) ? 0 : (int)n;
-    return y * __int_as_float((ni + 127) << 23);
+    // y * 2^n. After the clamps n is an integer in [-125, 127], so 2^n is a normal float and
+    // the product is exact scaling with one rounding: v_ldexp_f32 gives the same bits as
+    // multiplying by the constructed power of two (and a NaN x still gives a NaN, y being NaN).
+    return ldexpf(y, (int)n);
 }
 
 __device__ __forceinline__ float sigmoidf_ref(float x) {
