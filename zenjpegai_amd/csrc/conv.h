@@ -67,7 +67,6 @@ struct TileCfg {
 enum ConvKind : int { CK_1x1 = 0, CK_2x2 = 1, CK_3x3 = 2, CK_3x3_S2 = 3, CK_T3 = 4 };
 
 hipError_t launch_conv(int kind, int dtype, TileCfg cfg, const ConvParams& p, hipStream_t s);
-bool conv_cfg_supported(int kind, int dtype, TileCfg cfg);
 
 // Stride-2 transposed conv with 3x3 kernels (9 taps over the four output phases), all four
 // phases of a tile in one workgroup: p.w is the phase-merged packing [chunk][nblk][9][16][CK]

@@ -1149,15 +1149,6 @@ static hipError_t go_kind(int kind, const ConvParams& p, hipStream_t s) {
 //   {1,4,1,2}: 16 channels x 8 rows  (16-channel groups / narrow outputs)
 #define ZJAI_CFGS(X) X(2, 2, 2, 4) X(1, 4, 2, 2) X(1, 4, 1, 2)
 
-bool conv_cfg_supported(int kind, int dtype, TileCfg c) {
-    if (c.wc == 2 && c.wp == 4 && c.cf == 2 && c.pf == 4) return kind == CK_3x3;
-    if (c.wc == 4 && c.wp == 2 && c.cf == 2 && c.pf == 4) return kind == CK_1x1 && dtype == DT_F32;
-#define ZJAI_CHECK(a, b, cc, d) if (c.wc == a && c.wp == b && c.cf == cc && c.pf == d) return true;
-    ZJAI_CFGS(ZJAI_CHECK)
-#undef ZJAI_CHECK
-    return false;
-}
-
 template <typename T>
 static hipError_t go_cfg(int kind, TileCfg c, const ConvParams& p, hipStream_t s) {
     if (c.wc == 2 && c.wp == 4 && c.cf == 2 && c.pf == 4)

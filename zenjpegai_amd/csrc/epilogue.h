@@ -109,36 +109,6 @@ __device__ __forceinline__ void epilogue_store(const ConvParams& p, int b, int o
     }
 }
 
-// epilogue_store for 4 channels of one position (all valid) when epilogue_simple holds: the
-// same IEEE operations in the same order, kept small for kernels that store straight from their
-// accumulators.
-template <typename T>
-__device__ __forceinline__ void epilogue_store4(const ConvParams& p, int b, int oy, int ox, int oc0, f32x4 v) {
-    if (p.act == ACT_RELU) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], 0.0f);
-    } else if (p.act == ACT_LEAKY) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = v[i] < 0.0f ? v[i] * 0.01f : v[i];
-    }
-    if (p.res != RES_NONE) {
-        const f32x4 r = load4<T>((const T*)p.r1.p + (long long)b * p.r1.bstride + (long long)oy * p.r1.row +
-                                 (long long)ox * p.r1.cs + p.r1.c_off + oc0);
-        if (p.res == RES_ADD) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = v[i] + r[i];
-        } else if (p.res == RES_GATE) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { const float g = 1.0f + v[i]; v[i] = r[i] * g; }
-        } else {  // RES_MUL
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = r[i] * v[i];
-        }
-    }
-    store4<T>((T*)p.y.p + (long long)b * p.y.bstride + (long long)oy * p.y.row + (long long)ox * p.y.cs + p.y.c_off + oc0,
-              v);
-}
-
 // True when a launch's epilogue is an NHWC store without pixel shuffle: epilogue_store8 (any
 // activation and residual operation) covers it.
 __device__ __forceinline__ bool epilogue_simple(const ConvParams& p) {
