@@ -539,13 +539,35 @@ def test_depthwise_and_layer_norm_are_bit_exact(engines):
     assert np.array_equal(got.view(np.uint32), oracle.layer_norm_channels(xl, lw, lb).view(np.uint32))
 
 
-@pytest.mark.parametrize("dim,h,w", [(128, 24, 40), (64, 33, 17)])
-def test_channel_attention(engines, dim, h, w):
-    eng = engines["f32"]
-    qkv = synth.normal(10, f"at/{dim}", (3 * dim, h, w), 1.0)
-    temp = np.array([0.7, 1.0, 1.3, 2.0], np.float32)
-    got = nn.channel_attention(eng, nn.BTensor.from_planar(eng, qkv), 4, temp).to_planar()
-    assert rel_err(got, oracle.channel_attention(qkv, 4, temp)) <= 1e-5
+# (dim, heads, h, w, cropped view). Besides the synthesis nets' shapes (4 heads, dim 128 / 64)
+# these reach the Gram kernel's other paths: more than four heads (two head groups), a sub-chunk
+# needing more than one round of loads (dim 256), 12 channels per head (one 16-channel block),
+# and a cropped view (rows wider than the map: per-unit addresses).
+ATTENTION_CASES = [(128, 4, 24, 40, False), (64, 4, 33, 17, False), (128, 8, 21, 30, False),
+                   (256, 8, 20, 26, False), (48, 4, 19, 23, False), (128, 4, 24, 40, True)]
+
+
+@pytest.mark.parametrize("prec", ["f32", "bf16"])
+@pytest.mark.parametrize("dim,heads,h,w,crop", ATTENTION_CASES)
+def test_channel_attention(engines, prec, dim, heads, h, w, crop):
+    """Channel attention through the C-ABI against the oracle: 1e-5 of the largest output in
+    f32 (the reference normalises q and k before its dot, the kernels divide the raw dot by the
+    norms after); in bf16 against the oracle on the rounded input, 1e-2 (the output's own
+    rounding is 2^-9)."""
+    eng = engines[prec]
+    hh, ww = (h + 3, w + 5) if crop else (h, w)
+    qkv = synth.normal(10, f"at/{dim}/{heads}", (3 * dim, hh, ww), 1.0)
+    temp = np.linspace(0.7, 2.0, heads).astype(np.float32)
+    t = nn.BTensor.from_planar(eng, qkv)
+    if crop:
+        t = t.crop(h, w)
+    got = nn.channel_attention(eng, t, heads, temp).to_planar()
+    q = np.ascontiguousarray(qkv[:, :h, :w])
+    if prec != "f32":
+        q = _round_storage(q, prec)
+    err = rel_err(got, oracle.channel_attention(q, heads, temp))
+    print(f"{prec} dim {dim} heads {heads} {h}x{w} crop {crop}: {err:.2e}")
+    assert err <= (1e-5 if prec == "f32" else 1e-2)
 
 
 def test_attention_one_position_kat(engines):
