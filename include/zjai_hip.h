@@ -83,8 +83,9 @@ typedef struct zjai_picture zjai_picture;
  * (the two give bit-identical results). */
 #define ZJAI_CTX_UNFUSED_BLOCKS 0x1u
 /* Run every 3x3 stride-2 transposed convolution (`conv3x3_t`, src/model/attention.rs:78-91) one
- * output phase per workgroup instead of all four phases per workgroup (same results bit for bit;
- * for A/B runs and the parity test that proves it). */
+ * output phase per workgroup. By default a layer whose four-phase grid fills the chip (>= 256
+ * workgroups) runs all four phases per workgroup and a smaller one runs phase-split on a narrow
+ * tile (same results bit for bit; the flag is for A/B runs and the parity test that proves it). */
 #define ZJAI_CTX_PHASE_SPLIT_CONVT 0x2u
 /* Run the dense stride-1 3x3 convolutions of the 16-bit precisions on the 16x16x32 MFMA kernel
  * instead of the 32x32x16 one (for A/B runs and the test that compares the two). */
