@@ -98,7 +98,7 @@ def test_fast_paths_psnr(engines, prec, floor, op):
     assert np.isfinite(got).all() and v >= floor
 
 
-@pytest.mark.parametrize("prec", ["bf16", "f16"])
+@pytest.mark.parametrize("prec", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("comp", ["y", "uv"])
 def test_fused_transformer_blocks_are_bit_identical_to_unfused(prec, comp):
     """The fused prep_data (LN + 1x1 + depthwise) and feed-forward kernels (HOP luma TAM: dim

@@ -1,4 +1,5 @@
-// The feed-forward half of a transformer block as one kernel (16-bit storage types):
+// The feed-forward half of a transformer block as one kernel (16-bit storage types here; the f32
+// form, k_ffn_f32, follows the same plan with the LayerNorm output in registers):
 //   u = LayerNorm(x); p = project_in(u) (1x1, dim -> 2 * hid); d = depthwise3x3(p);
 //   g = elu(d[:hid]) * d[hid:]; y = x + project_out(g) (1x1, hid -> dim)
 // (TransformerBlock::forward, src/model/attention.rs:346-369; LayerNorm :267-279).
@@ -579,11 +580,473 @@ __global__ void __launch_bounds__(FTHREADS) k_qkv(const QkvArgs p) {
     }
 }
 
-bool qkv_fused_supported(int dtype, int dim) { return (dtype == DT_F16 || dtype == DT_BF16) && (dim == 64 || dim == 128); }
+// ------------------------------------------------------------------------- f32 storage
+// The same two kernels for f32 nets. A 16 x 16 halo of f32 LayerNorm output (128 KB at dim 128)
+// does not fit LDS beside the slice buffers, so each wave keeps the LayerNorm output of its own
+// two 16-position halo blocks in registers, already in the MFMA B-fragment layout of the 1x1's
+// f32 instruction sequence (lane group g holds channels 16 c + 4 g .. 16 c + 4 g + 3 of K chunk
+// c), and every wave computes all channels of a slice for its 32 positions. The weights of each
+// slice arrive by direct global -> LDS loads issued one phase ahead. The arithmetic is the f32
+// unfused kernels' instruction for instruction: LayerNorm as k_layer_norm (f64 sums in channel
+// order per position), the 1x1 convs as conv1x1_ring (bias, then v_mfma_f32_16x16x4_f32 over K
+// chunks of 16 channels in ascending order), the depthwise 3x3 and gate as k_depthwise3x3, so the
+// fused and unfused f32 paths agree bit for bit.
+
+namespace {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ u32x4 g_zero_ffn32[8];  // 128 zero bytes: the source of absent biases
+
+typedef __attribute__((address_space(3))) void* lds_addr_ffn_t;
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited for); gfx9 splits vmcnt over [3:0] and [15:14].
+template <int N>
+__device__ __forceinline__ void ffn_wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// 16 bytes per lane from global memory to LDS (lane i lands at dst + 16 i; dst wave-uniform).
+__device__ __forceinline__ void ffn_dma(const void* src, u32x4* dst) {
+    __builtin_amdgcn_global_load_lds(src, (lds_addr_ffn_t)dst, 16, 0, 0);
+}
+
+// LayerNorm of this wave's halo positions into B fragments: u[i][c] holds channels
+// 16 c + 4 grp .. + 3 of halo position (2 wave + i) * 16 + col. Statistics as k_layer_norm: one
+// thread per halo position sums its channels in order in f64 (positions outside the picture
+// read zeros; their values are never used, the 1x1's output is zeroed there). Ends after the
+// statistics barrier; the caller's direct loads issued before it are waited for by the loads here.
+template <int DIM>
+__device__ __forceinline__ void ln_frags_f32(const float* xb, const View& xv, int y0, int x0, int h, int w,
+                                             const float* ln_w, const float* ln_b, float* s_stat, int tid,
+                                             int wave, int col, int grp, f32x4 (&u)[2][DIM / 16]) {
+    constexpr int NCH = DIM / 16;
+    if (tid < FNP) {
+        const int iy = y0 - 1 + tid / FH, ix = x0 - 1 + tid % FH;
+        double mean = 0.0, var = 0.0;
+        if (iy >= 0 && iy < h && ix >= 0 && ix < w) {
+            const float* r = xb + (long long)iy * xv.row + (long long)ix * xv.cs;
+#pragma unroll 8
+            for (int q = 0; q < DIM / 4; ++q) {
+                const f32x4 v = *(const f32x4*)(r + 4 * q);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) mean += (double)v[k];
+            }
+            mean /= (double)DIM;
+#pragma unroll 8
+            for (int q = 0; q < DIM / 4; ++q) {
+                const f32x4 v = *(const f32x4*)(r + 4 * q);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const double e = (double)v[k] - mean;
+                    var = var + e * e;
+                }
+            }
+        } else {
+            mean /= (double)DIM;
+            var = 0.0;
+        }
+        s_stat[tid] = (float)mean;
+        s_stat[FNP + tid] = sqrtf((float)(var / (double)DIM) + 1e-5f);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int pos = (2 * wave + i) * 16 + col;
+        const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
+        const bool inside = iy >= 0 && iy < h && ix >= 0 && ix < w;
+        const float* r = xb + (long long)iy * xv.row + (long long)ix * xv.cs + 4 * grp;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) u[i][c] = inside ? *(const f32x4*)(r + 16 * c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int pos = (2 * wave + i) * 16 + col;
+        const float m = s_stat[pos], d = s_stat[FNP + pos];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const f32x4 lw = *(const f32x4*)(ln_w + 16 * c + 4 * grp);
+            const f32x4 lb = *(const f32x4*)(ln_b + 16 * c + 4 * grp);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float e = u[i][c][k] - m;
+                e = e / d;
+                e = e * lw[k];
+                u[i][c][k] = e + lb[k];
+            }
+        }
+    }
+}
+
+// acc[cb][i] = bias + W (64 rows: four 16-row blocks in LDS as [chunk][block][16][4 units]) x u
+// for this wave's two position blocks, the 1x1's f32 instruction sequence.
+template <int NCH>
+__device__ __forceinline__ void slice_gemm_f32(const u32x4* s_w, const float* bias64, const f32x4 (&u)[2][NCH],
+                                               int col, int grp, f32x4 (&acc)[4][2]) {
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+        const f32x4 bi = *(const f32x4*)(bias64 + cb * 16 + 4 * grp);
+        acc[cb][0] = bi;
+        acc[cb][1] = bi;
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        // One chunk's 16 weight registers at a time (32 MFMAs cover the LDS latency); without the
+        // fence the compiler hoists every chunk's reads and spills.
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 a[4];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) a[cb] = __builtin_bit_cast(f32x4, s_w[(c * 4 + cb) * 64 + col * 4 + grp]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    acc[cb][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[cb][k], u[i][c][k], acc[cb][i], 0, 0, 0);
+    }
+}
+
+}  // namespace
+
+// Feed-forward, f32: as k_ffn, slices of 32 gate pairs (64 p channels). LDS: W_in slice
+// [chunk][4 blocks][16][4] (32 KB at dim 128), p [256 positions][64] (a and b halves swapped on
+// odd positions), g [208 positions][32] (16-byte units XOR-swizzled by position pair), W_out
+// slice [2 chunks][dim / 16 blocks][16][4], and per slice b_in, the depthwise taps and biases.
+template <int DIM>
+__global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
+    constexpr int HID = 4 * DIM, C2 = 2 * HID, NS = HID / 32, NCH = DIM / 16;
+    constexpr int CB2 = DIM / 16, WPC = 8 / CB2, NPB = (FPB + WPC - 1) / WPC;
+    constexpr int WIN_U = NCH * 4 * 64, P_U = FNP * 16, G_U = FPB * 16 * 8, WO_U = 2 * CB2 * 64;
+    constexpr int X_U = 11 * 16;  // b_in [64], depthwise taps [9][64], depthwise bias [64] (f32)
+    constexpr int WIN_W = NCH * 4 / 8, WO_W = 2 * CB2 / 8;  // direct loads per wave and slice
+    static_assert(WIN_W * 8 == NCH * 4 && WO_W * 8 == 2 * CB2, "load shapes");
+    static_assert(FOP <= FPB * 16 && 2 * 8 * 16 == FNP, "tile shapes");
+    // One LDS object per buffer: the compiler then sees that the direct loads into one buffer
+    // cannot alias the reads of another and waits for them only where this code does.
+    __shared__ u32x4 s_win[WIN_U];
+    __shared__ float s_p[P_U * 4];
+    __shared__ float s_g[G_U * 4];
+    __shared__ u32x4 s_wo[WO_U];
+    __shared__ u32x4 s_x[2 * X_U];
+    __shared__ float s_stat[2 * FNP];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int bid = (int)blockIdx.x;
+    const int tx = bid % p.gx, ty = (bid / p.gx) % p.gy, b = bid / (p.gx * p.gy);
+    const int y0 = ty * FT, x0 = tx * FT;
+    const float* xb = (const float*)p.x.p + (long long)b * p.x.bstride + p.x.c_off;
+    const u32x4* w_in = (const u32x4*)p.w_in;
+    const u32x4* w_out = (const u32x4*)p.w_out;
+
+    // Slice s weights. W_in block (c, cb): 16 rows of p channels 32 s + 16 cb (cb < 2) or
+    // hid + 32 s + 16 (cb - 2), K chunk c: one contiguous KB of the packed weight.
+    auto issue_win = [&](int s) {
+#pragma unroll
+        for (int j = 0; j < WIN_W; ++j) {
+            const int blk = wave + 8 * j, c = blk >> 2, cb = blk & 3;
+            const int gb = cb < 2 ? 2 * s + cb : HID / 16 + 2 * s + (cb - 2);
+            ffn_dma(w_in + ((long long)c * p.nblk_in + gb) * 64 + lane, s_win + blk * 64);
+        }
+    };
+    auto issue_wout = [&](int s) {  // K chunks 2 s, 2 s + 1: 2 CB2 contiguous KB
+#pragma unroll
+        for (int j = 0; j < WO_W; ++j) {
+            const int blk = wave + 8 * j;
+            ffn_dma(w_out + ((long long)2 * s * p.nblk_out + blk) * 64 + lane, s_wo + blk * 64);
+        }
+    };
+    // Unit u of X (176): run u / 8 of 32 floats; runs 0-1 b_in, 2-19 tap (run - 2) / 2, 20-21 the
+    // depthwise bias; even runs the first-half channels 32 s .., odd runs hid + 32 s ...
+    auto issue_x = [&](int s, int buf) {
+        if (wave < 3) {
+            const int u = wave * 64 + lane;
+            if (u < X_U) {
+                const int run = u >> 3, half = run & 1, q = u & 7;
+                const int ch = (half ? HID : 0) + 32 * s + 4 * q;
+                const void* src;
+                if (run < 2) src = p.b_in ? (const void*)(p.b_in + ch) : (const void*)(g_zero_ffn32 + q);
+                else if (run < 20) src = p.dw_w + ((run - 2) >> 1) * C2 + ch;
+                else src = p.dw_b ? (const void*)(p.dw_b + ch) : (const void*)(g_zero_ffn32 + q);
+                ffn_dma(src, s_x + buf * X_U + wave * 64);
+            }
+        }
+    };
+
+    issue_win(0);
+    issue_x(0, 0);
+    f32x4 u[2][NCH];
+    ln_frags_f32<DIM>(xb, p.x, y0, x0, p.h, p.w, p.ln_w, p.ln_b, s_stat, tid, wave, col, grp, u);
+
+    const int cb2 = wave % CB2, pw2 = wave / CB2;
+    f32x4 acc2[NPB];
+    {
+        f32x4 bo = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (p.b_out) bo = *(const f32x4*)(p.b_out + cb2 * 16 + 4 * grp);
+#pragma unroll
+        for (int i = 0; i < NPB; ++i) acc2[i] = bo;
+    }
+    // Depthwise role (tid < 448, waves 0-6): gate pair pg of the slice, column dc, all rows.
+    const int pg = tid & 31, dc = (tid >> 5) % FT;
+    const bool dw_thread = tid < 32 * FT;
+
+    for (int s = 0; s < NS; ++s) {
+        ffn_wait_vmcnt<0>();
+        __syncthreads();  // W_in(s), X(s) landed; p, g and the W_out buffer free
+        issue_wout(s);
+        if (s + 1 < NS) issue_x(s + 1, (s + 1) & 1);
+        const float* sx = reinterpret_cast<const float*>(s_x + (s & 1) * X_U);
+
+        // a. p slice = b_in + W_in x u for this wave's positions; zero outside the picture.
+        {
+            f32x4 acc1[4][2];
+            slice_gemm_f32<NCH>(s_win, sx, u, col, grp, acc1);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int pos = (2 * wave + i) * 16 + col;
+                const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
+                const bool inside = iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) {
+                    const int half = (cb >> 1) ^ (col & 1);  // pos & 1 == col & 1
+                    const f32x4 v = inside ? acc1[cb][i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    *(f32x4*)(s_p + pos * 64 + half * 32 + (cb & 1) * 16 + 4 * grp) = v;
+                }
+            }
+        }
+        __syncthreads();  // p ready; W_in(s) consumed
+
+        // b. depthwise 3x3 + ELU gate (k_depthwise3x3's order: bias, then taps (ky, kx) ascending).
+        if (dw_thread) {
+            const float* dww = sx + 64;
+            float wa[9], wb[9];
+            const float ba = dww[576 + pg], bb = dww[576 + 32 + pg];
+#pragma unroll
+            for (int tp = 0; tp < 9; ++tp) {
+                wa[tp] = dww[tp * 64 + pg];
+                wb[tp] = dww[tp * 64 + 32 + pg];
+            }
+            auto ld = [&](int hr, int kx, float& oa, float& ob) {
+                const int pos = hr * FH + dc + kx, odd = pos & 1;
+                oa = s_p[pos * 64 + odd * 32 + pg];
+                ob = s_p[pos * 64 + (odd ^ 1) * 32 + pg];
+            };
+            float xa[3][3], xq[3][3];
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                ld(0, kx, xa[0][kx], xq[0][kx]);
+                ld(1, kx, xa[1][kx], xq[1][kx]);
+            }
+#pragma unroll 2
+            for (int oy = 0; oy < FT; ++oy) {
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx) ld(oy + 2, kx, xa[2][kx], xq[2][kx]);
+                float a = ba, bq = bb;
+#pragma unroll
+                for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+                    for (int kx = 0; kx < 3; ++kx) {
+                        a = fmaf(wa[ky * 3 + kx], xa[ky][kx], a);
+                        bq = fmaf(wb[ky * 3 + kx], xq[ky][kx], bq);
+                    }
+                const float e = cephes_exp(a) - 1.0f;
+                const float elu = a > 0.0f ? a : e;
+                const int o = oy * FT + dc;
+                s_g[o * 32 + (((pg >> 2) ^ (((o >> 1) & 1) << 2)) << 2) + (pg & 3)] = elu * bq;
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx) {
+                    xa[0][kx] = xa[1][kx];
+                    xa[1][kx] = xa[2][kx];
+                    xq[0][kx] = xq[1][kx];
+                    xq[1][kx] = xq[2][kx];
+                }
+            }
+        }
+        // W_in(s + 1) flies during phase c. W_out(s), issued before it, has landed once at most
+        // WIN_W loads are pending.
+        if (s + 1 < NS) issue_win(s + 1);
+        if (s + 1 < NS) ffn_wait_vmcnt<WIN_W>();
+        else ffn_wait_vmcnt<0>();
+        __syncthreads();  // g ready; W_out(s) landed
+
+        // c. y += W_out(s) x g: K chunks 2 s, 2 s + 1 (channel 16 cc + 4 grp + k of the slice).
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const f32x4 a = __builtin_bit_cast(f32x4, s_wo[(cc * CB2 + cb2) * 64 + col * 4 + grp]);
+            // The g swizzle depends on bit 1 of the position, i.e. of col: one base address.
+            const float* gq = s_g + (pw2 * 16 + col) * 32 + (((cc * 4 + grp) ^ (((col >> 1) & 1) << 2)) << 2);
+            // Position blocks in groups of GB (fewer live fragment registers).
+            constexpr int GB = 7;
+#pragma unroll
+            for (int i0 = 0; i0 < NPB; i0 += GB) {
+                __builtin_amdgcn_sched_barrier(0);
+                f32x4 bv[GB];
+#pragma unroll
+                for (int j = 0; j < GB; ++j)
+                    if (i0 + j < NPB && pw2 + WPC * (i0 + j) < FPB) bv[j] = *(const f32x4*)(gq + WPC * (i0 + j) * 512);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+#pragma unroll
+                    for (int j = 0; j < GB; ++j)
+                        if (i0 + j < NPB && pw2 + WPC * (i0 + j) < FPB)
+                            acc2[i0 + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[k], bv[j][k], acc2[i0 + j], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- 3. y = acc + x, stored from the fragments (16 bytes per lane, 64-byte channel runs).
+    float* yb = (float*)p.y.p + (long long)b * p.y.bstride + p.y.c_off;
+#pragma unroll
+    for (int i = 0; i < NPB; ++i) {
+        const int pb = pw2 + WPC * i, pos = pb * 16 + col;
+        if (pb >= FPB || pos >= FOP) continue;
+        const int oy = y0 + pos / FT, ox = x0 + pos % FT;
+        if (oy >= p.h || ox >= p.w) continue;
+        const int ch = cb2 * 16 + 4 * grp;
+        const f32x4 r = *(const f32x4*)(xb + (long long)oy * p.x.row + (long long)ox * p.x.cs + ch);
+        f32x4 v = acc2[i];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = v[k] + r[k];
+        *(f32x4*)(yb + (long long)oy * p.y.row + (long long)ox * p.y.cs + ch) = v;
+    }
+}
+
+// prep_data, f32: as k_qkv, slices of 64 of the 3 dim conv1 channels; the 1x1 as in k_ffn_f32,
+// p [256 positions][64] in LDS, the depthwise stored straight to qkv. The biases and depthwise
+// taps of every slice (17 KB at dim 128) are loaded once, with the first slice's weights.
+template <int DIM>
+__global__ void __launch_bounds__(FTHREADS) k_qkv_f32(const QkvArgs p) {
+    constexpr int C3 = 3 * DIM, NS = C3 / 64, NCH = DIM / 16;
+    constexpr int W1_U = NCH * 4 * 64, P_U = FNP * 16, X_U = 11 * 16;
+    constexpr int W1_W = NCH * 4 / 8;
+    static_assert(W1_W * 8 == NCH * 4 && C3 % 64 == 0, "load shapes");
+    __shared__ u32x4 s_w1[W1_U];
+    __shared__ float s_p[P_U * 4];
+    __shared__ u32x4 s_x[NS * X_U];
+    __shared__ float s_stat[2 * FNP];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int bid = (int)blockIdx.x;
+    const int tx = bid % p.gx, ty = (bid / p.gx) % p.gy, b = bid / (p.gx * p.gy);
+    const int y0 = ty * FT, x0 = tx * FT;
+    const float* xb = (const float*)p.x.p + (long long)b * p.x.bstride + p.x.c_off;
+    const u32x4* w1 = (const u32x4*)p.w1;
+
+    // Slice s: conv1 output channels 64 s .. 64 s + 63 (blocks 4 s .. 4 s + 3).
+    auto issue_w1 = [&](int s) {
+#pragma unroll
+        for (int j = 0; j < W1_W; ++j) {
+            const int blk = wave + 8 * j, c = blk >> 2, cb = blk & 3;
+            ffn_dma(w1 + ((long long)c * p.nblk1 + 4 * s + cb) * 64 + lane, s_w1 + blk * 64);
+        }
+    };
+    // Unit u of slice s's X (176): run u / 16 of 64 floats; run 0 b1, 1-9 tap run - 1, 10 the
+    // depthwise bias. Wave w loads 64-unit pieces w, w + 8, ... of all NS * 176 units.
+    for (int j = wave; j * 64 < NS * X_U; j += 8) {
+        const int v = j * 64 + lane;
+        if (v < NS * X_U) {
+            const int s = v / X_U, u = v - s * X_U;
+            const int run = u >> 4, q = u & 15;
+            const int ch = 64 * s + 4 * q;
+            const void* src;
+            if (run == 0) src = p.b1 ? (const void*)(p.b1 + ch) : (const void*)(g_zero_ffn32 + (q & 7));
+            else if (run < 10) src = p.dw_w + (run - 1) * C3 + ch;
+            else src = p.dw_b ? (const void*)(p.dw_b + ch) : (const void*)(g_zero_ffn32 + (q & 7));
+            ffn_dma(src, s_x + j * 64);
+        }
+    }
+    issue_w1(0);
+    f32x4 u[2][NCH];
+    ln_frags_f32<DIM>(xb, p.x, y0, x0, p.h, p.w, p.ln_w, p.ln_b, s_stat, tid, wave, col, grp, u);
+
+    // Depthwise role (tid < 448, waves 0-6): channel pair pg of the slice, column dc, all rows.
+    const int pg = tid & 31, dc = (tid >> 5) % FT;
+    const bool dw_thread = tid < 32 * FT;
+    float* yb = (float*)p.y.p + (long long)b * p.y.bstride + p.y.c_off;
+
+    for (int s = 0; s < NS; ++s) {
+        ffn_wait_vmcnt<0>();
+        __syncthreads();  // W1(s) landed; p free
+        const float* sx = reinterpret_cast<const float*>(s_x + s * X_U);
+        {
+            f32x4 acc1[4][2];
+            slice_gemm_f32<NCH>(s_w1, sx, u, col, grp, acc1);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int pos = (2 * wave + i) * 16 + col;
+                const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
+                const bool inside = iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb)
+                    *(f32x4*)(s_p + pos * 64 + cb * 16 + 4 * grp) =
+                        inside ? acc1[cb][i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+        __syncthreads();  // p ready; W1(s) consumed
+        if (s + 1 < NS) issue_w1(s + 1);
+        if (dw_thread) {
+            const float* dww = sx + 64;
+            float wv[9][2], bv[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                bv[k] = dww[576 + 2 * pg + k];
+#pragma unroll
+                for (int tp = 0; tp < 9; ++tp) wv[tp][k] = dww[tp * 64 + 2 * pg + k];
+            }
+            const float* sp = s_p + dc * 64 + 2 * pg;
+            float xw[3][3][2];
+            auto ld = [&](int hr, int kx, float (&o)[2]) {
+                const f32x2 v = *(const f32x2*)(sp + (hr * FH + kx) * 64);
+                o[0] = v[0];
+                o[1] = v[1];
+            };
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                ld(0, kx, xw[0][kx]);
+                ld(1, kx, xw[1][kx]);
+            }
+            const int ox = x0 + dc;
+#pragma unroll
+            for (int r = 0; r < FT; ++r) {
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx) ld(r + 2, kx, xw[2][kx]);
+                float o[2];
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    float a = bv[k];
+#pragma unroll
+                    for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+                        for (int kx = 0; kx < 3; ++kx) a = fmaf(wv[ky * 3 + kx][k], xw[ky][kx][k], a);
+                    o[k] = a;
+                }
+                const int oy = y0 + r;
+                if (oy < p.h && ox < p.w)
+                    *(f32x2*)(yb + (long long)oy * p.y.row + (long long)ox * p.y.cs + 64 * s + 2 * pg) = f32x2{o[0], o[1]};
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx)
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        xw[0][kx][k] = xw[1][kx][k];
+                        xw[1][kx][k] = xw[2][kx][k];
+                    }
+            }
+        }
+    }
+}
+
+bool qkv_fused_supported(int dtype, int dim) {
+    return (dtype == DT_F32 || dtype == DT_F16 || dtype == DT_BF16) && (dim == 64 || dim == 128);
+}
 
 hipError_t launch_qkv_fused(const QkvArgs& a, int dtype, int dim, hipStream_t s) {
     if (!qkv_fused_supported(dtype, dim)) return hipErrorInvalidValue;
-    if (a.x.cs % 8 || a.x.c_off % 8 || a.x.row % 8 || a.x.bstride % 8 || a.y.cs % 2 || a.y.c_off % 2 ||
+    // 16-byte loads of x (4 f32 or 8 16-bit channels), 2-channel stores of y.
+    const int xv = dtype == DT_F32 ? 4 : 8;
+    if (a.x.cs % xv || a.x.c_off % xv || a.x.row % xv || a.x.bstride % xv || a.y.cs % 2 || a.y.c_off % 2 ||
         a.y.row % 2 || a.y.bstride % 2)
         return hipErrorInvalidValue;
     if (a.N <= 0 || a.h <= 0 || a.w <= 0) return hipSuccess;
@@ -593,7 +1056,10 @@ hipError_t launch_qkv_fused(const QkvArgs& a, int dtype, int dim, hipStream_t s)
     const long long blocks = (long long)p.gx * p.gy * a.N;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
     const dim3 grid((unsigned)blocks), block(FTHREADS);
-    if (dtype == DT_BF16) {
+    if (dtype == DT_F32) {
+        if (dim == 128) k_qkv_f32<128><<<grid, block, 0, s>>>(p);
+        else k_qkv_f32<64><<<grid, block, 0, s>>>(p);
+    } else if (dtype == DT_BF16) {
         if (dim == 128) k_qkv<__bf16, 128><<<grid, block, 0, s>>>(p);
         else k_qkv<__bf16, 64><<<grid, block, 0, s>>>(p);
     } else {
@@ -604,14 +1070,15 @@ hipError_t launch_qkv_fused(const QkvArgs& a, int dtype, int dim, hipStream_t s)
 }
 
 bool ffn_fused_supported(int dtype, int dim) {
-    return (dtype == DT_F16 || dtype == DT_BF16) && (dim == 64 || dim == 128);
+    return (dtype == DT_F32 || dtype == DT_F16 || dtype == DT_BF16) && (dim == 64 || dim == 128);
 }
 
 hipError_t launch_ffn_fused(const FfnArgs& a, int dtype, int dim, hipStream_t s) {
     if (!ffn_fused_supported(dtype, dim)) return hipErrorInvalidValue;
-    // 16-byte vector accesses of x and y.
-    if (a.x.cs % 8 || a.x.c_off % 8 || a.x.row % 8 || a.x.bstride % 8 || a.y.cs % 8 || a.y.c_off % 8 ||
-        a.y.row % 8 || a.y.bstride % 8)
+    // 16-byte vector accesses of x and y (4 f32 or 8 16-bit channels).
+    const int v = dtype == DT_F32 ? 4 : 8;
+    if (a.x.cs % v || a.x.c_off % v || a.x.row % v || a.x.bstride % v || a.y.cs % v || a.y.c_off % v ||
+        a.y.row % v || a.y.bstride % v)
         return hipErrorInvalidValue;
     if (a.N <= 0 || a.h <= 0 || a.w <= 0) return hipSuccess;
     FfnArgs p = a;
@@ -620,7 +1087,10 @@ hipError_t launch_ffn_fused(const FfnArgs& a, int dtype, int dim, hipStream_t s)
     const long long blocks = (long long)p.gx * p.gy * a.N;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
     const dim3 grid((unsigned)blocks), block(FTHREADS);
-    if (dtype == DT_BF16) {
+    if (dtype == DT_F32) {
+        if (dim == 128) k_ffn_f32<128><<<grid, block, 0, s>>>(p);
+        else k_ffn_f32<64><<<grid, block, 0, s>>>(p);
+    } else if (dtype == DT_BF16) {
         if (dim == 128) k_ffn<__bf16, 128><<<grid, block, 0, s>>>(p);
         else k_ffn<__bf16, 64><<<grid, block, 0, s>>>(p);
     } else {

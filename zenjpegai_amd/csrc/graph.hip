@@ -358,9 +358,9 @@ struct Fwd {
                                    net.vec.at(pfx + ".bias"), ctx.stream));
         return y;
     }
-    // The fused feed-forward kernel applies to 16-bit nets with dim 64 / 128 whose 1x1 weights
-    // are packed unpadded (K chunks of 32 channels, 16-row blocks) and whose input is a whole
-    // 16-byte-aligned NHWC tensor.
+    // The fused feed-forward kernel applies to nets with dim 64 / 128 whose 1x1 weights are
+    // packed unpadded (K chunks of 64 bytes of channels, 16-row blocks) and whose input is a
+    // whole 16-byte-aligned NHWC tensor.
     bool ffn_fusable(const std::string& p, const TensorP& x) {
         if (ctx.top().flags & ZJAI_CTX_UNFUSED_BLOCKS) return false;
         const int dim = x->c, hidden = 4 * dim;

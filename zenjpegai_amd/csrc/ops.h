@@ -47,9 +47,9 @@ hipError_t launch_depthwise3x3(View src, View dst, int dtype, int N, int C, int 
 // Layer norm over channels per position (f64 sums), src -> dst.
 hipError_t launch_layer_norm(View src, View dst, int dtype, int N, int C, int h, int w,
                              const float* weight, const float* bias, hipStream_t s);
-// The feed-forward half of a transformer block in one kernel (16-bit storage types, dim 64 or
+// The feed-forward half of a transformer block in one kernel (every storage type, dim 64 or
 // 128): y = x + project_out(elu(dw(project_in(LN(x)))[:hid]) * dw(...)[hid:]), hid = 4 * dim.
-// Weights: the packed 1x1 layers ([chunk][nblk][16][32], storage type) and the depthwise
+// Weights: the packed 1x1 layers ([chunk][nblk][16][64 bytes], storage type) and the depthwise
 // [9][2 * hid] f32. y must not alias x (neighbouring tiles read x over their halos).
 struct FfnArgs {
     View x, y;
@@ -68,7 +68,7 @@ struct FfnArgs {
 };
 bool ffn_fused_supported(int dtype, int dim);
 // The attention branch's qkv = depthwise3x3(conv1x1(LN(x))) (dim -> 3 dim) in one kernel
-// (16-bit storage types, dim 64 or 128); weights as FfnArgs. y must not alias x.
+// (every storage type, dim 64 or 128); weights as FfnArgs. y must not alias x.
 struct QkvArgs {
     View x, y;
     int N, h, w;
