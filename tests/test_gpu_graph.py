@@ -122,9 +122,10 @@ def test_fused_transformer_blocks_are_bit_identical_to_unfused(prec, comp):
         names.append([r[0] for r in eng.profile_end()])
         outs.append(out)
     dim = 128 if comp == "y" else 64
-    for k in ("k_ffn<", "k_qkv<"):
-        assert sum(n.startswith(k) and n.endswith(f", {dim}>") for n in names[0]) == 2, k
-        assert not any(n.startswith(k) for n in names[1]), k
+    for k in ("k_ffn", "k_qkv"):
+        want = f"{k}_f32<{dim}>" if prec == "f32" else f"{k}<{'__bf16' if prec == 'bf16' else '_Float16'}, {dim}>"
+        assert sum(n == want for n in names[0]) == 2, (want, names[0])
+        assert not any(n.startswith(k + "<") or n.startswith(k + "_f32<") for n in names[1]), k
     assert np.isfinite(outs[0]).all()
     np.testing.assert_array_equal(outs[0], outs[1])
     fused.close()

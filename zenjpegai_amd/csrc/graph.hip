@@ -358,6 +358,13 @@ struct Fwd {
                                    net.vec.at(pfx + ".bias"), ctx.stream));
         return y;
     }
+    // Profile name of a fused block kernel, as the kernel symbol reads: k_ffn<__bf16, 128>,
+    // k_ffn_f32<128>.
+    static std::string fused_name(const char* base, int dtype, int dim) {
+        if (dtype == DT_F32) return std::string(base) + "_f32<" + std::to_string(dim) + ">";
+        const std::string kn = kname(base, dtype);
+        return kn.substr(0, kn.size() - 1) + ", " + std::to_string(dim) + ">";
+    }
     // The fused feed-forward kernel applies to nets with dim 64 / 128 whose 1x1 weights are
     // packed unpadded (K chunks of 64 bytes of channels, 16-row blocks) and whose input is a
     // whole 16-byte-aligned NHWC tensor.
@@ -417,8 +424,7 @@ struct Fwd {
             a.dw_w = c2.dw_w;
             a.dw_b = c2.bias;
             const double npos = (double)x->n * x->h * x->w;
-            const std::string kn = kname("k_qkv", x->dtype);
-            LaunchScope sc(ctx, kn.substr(0, kn.size() - 1) + ", " + std::to_string(dim) + ">",
+            LaunchScope sc(ctx, fused_name("k_qkv", x->dtype, dim),
                            2.0 * npos * (3.0 * dim * dim + 9.0 * 3 * dim),
                            (double)dtype_size(x->dtype) * npos * 4 * dim);
             ZJAI_HIP(launch_qkv_fused(a, x->dtype, dim, ctx.stream));
@@ -460,8 +466,7 @@ struct Fwd {
             a.nblk_out = pout.nblk_g;
             a.b_out = pout.bias;
             const double npos = (double)x->n * x->h * x->w;
-            const std::string kn = kname("k_ffn", x->dtype);
-            LaunchScope sc(ctx, kn.substr(0, kn.size() - 1) + ", " + std::to_string(dim) + ">",
+            LaunchScope sc(ctx, fused_name("k_ffn", x->dtype, dim),
                            2.0 * npos * (2.0 * hidden * dim + 9.0 * 2 * hidden + (double)hidden * dim),
                            2.0 * dtype_size(x->dtype) * npos * dim);
             ZJAI_HIP(launch_ffn_fused(a, x->dtype, dim, ctx.stream));
