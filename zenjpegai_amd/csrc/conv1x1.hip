@@ -177,7 +177,7 @@ conv1x1_ring(const ConvParams p) {
     // one position, TP passes of PP positions (a 16-position fragment lies in one pass).
     float* so = reinterpret_cast<float*>(s_lds);
     const int oc0 = nb0 * 16;
-    const bool simple = epilogue_simple(p);
+    const bool simple = epilogue_simple(p), ps2 = epilogue_ps2(p);
 #pragma unroll
     for (int pass = 0; pass < TP; ++pass) {
         __syncthreads();
@@ -202,6 +202,18 @@ conv1x1_ring(const ConvParams p) {
                     const int oy = pg / p.OW, ox = pg - oy * p.OW;
                     epilogue_store8<T>(p, bi, oy, ox, oc0 + c8 * 8, v0, v1);
                 }
+            }
+        } else if (ps2) {
+            // Unit u: position, sub-position s, output-channel quad cq (conv channels
+            // 16 cq + 4 j + s, j = 0..3, of this tile).
+#pragma unroll 2
+            for (int u = tid; u < PP * 4 * NB; u += NT) {
+                const int pos = u / (4 * NB), r = u - pos * (4 * NB), s = r / NB, cq = r - s * NB;
+                const int pg = pos0 + pass * PP + pos;
+                if (pg >= P) continue;
+                const int oy = pg / p.OW, ox = pg - oy * p.OW;
+                const float* sv = so + pos * OUT_LD + 16 * cq + s;
+                epilogue_store_ps2<T>(p, bi, oy, ox, s, oc0 / 4 + 4 * cq, f32x4{sv[0], sv[4], sv[8], sv[12]});
             }
         } else {
             constexpr int QP = NB * 4;

@@ -115,6 +115,25 @@ __device__ __forceinline__ bool epilogue_simple(const ConvParams& p) {
     return p.out_mode == OUT_NHWC && p.ps == 1;
 }
 
+// NHWC output with a pixel shuffle by 2 and no residual operation: epilogue_store_ps2 applies.
+__device__ __forceinline__ bool epilogue_ps2(const ConvParams& p) {
+    return p.out_mode == OUT_NHWC && p.ps == 2 && p.res == RES_NONE;
+}
+
+// epilogue_store for the pixel shuffle by 2 when epilogue_ps2 holds, four output channels at a
+// time: output channels c .. c + 3 at sub-position s of position (oy, ox) take conv channels
+// 4 c + s, 4 (c + 1) + s, .. (v in that order); the activation per element, then one vector
+// store of the four (epilogue_store writes the same values one channel at a time).
+template <typename T>
+__device__ __forceinline__ void epilogue_store_ps2(const ConvParams& p, int b, int oy, int ox, int s, int c,
+                                                   f32x4 v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = apply_act(p.act, v[i]);
+    T* y = (T*)p.y.p + (long long)b * p.y.bstride;
+    const int Y = 2 * oy + (s >> 1), X = 2 * ox + (s & 1);
+    store4<T>(y + (long long)Y * p.y.row + (long long)X * p.y.cs + p.y.c_off + c, v);
+}
+
 // epilogue_store for 8 consecutive channels of one position (all valid) when epilogue_simple
 // holds: the same IEEE operations in the same order, one 16-byte (16-bit types) or two 16-byte
 // (f32) stores, 8-channel residual loads.
