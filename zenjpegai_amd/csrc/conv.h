@@ -73,6 +73,8 @@ hipError_t launch_conv(int kind, int dtype, TileCfg cfg, const ConvParams& p, hi
 // (taps phase by phase, each phase's taps in its table order), p.ntiles = nblk_g / 4; NHWC
 // output without pixel shuffle, no relu6 on load.
 hipError_t launch_conv_tr_merged(int dtype, const ConvParams& p, hipStream_t s);
+// The per-phase tap counts conv_tr_merged is instantiated for (3x3 kernels, stride 2).
+bool conv_tr_merged_taps_supported(const int (&ntaps)[4]);
 constexpr int TR_MERGED_TAPS = 9;
 constexpr int TR_MERGED_NB = 4;
 

@@ -546,9 +546,11 @@ conv_dma_f32(const ConvParams p) {
 // CF x PF tile for all four phases (acc[4][CF][PF]); the stage pipeline is conv_dma_f32's
 // (direct global -> LDS loads, double-buffered, one barrier per stage), for every storage type.
 // Per output the products are summed exactly as in the phase-per-workgroup kernel: bias, then
-// per K chunk the phase's taps in table order, k ascending within a tap.
+// per K chunk the phase's taps in table order, k ascending within a tap. The phases' tap counts
+// are template parameters (1, 2, 2, 4 for padding 1; 4, 2, 2, 1 for padding 0 or 2), so the tap
+// loops unroll and each tap's fragment reads overlap the previous tap's MFMAs.
 // ---------------------------------------------------------------------------------------------
-template <typename T>
+template <typename T, int N0, int N1, int N2, int N3>
 __global__ void __launch_bounds__(512)
 conv_tr_merged(const ConvParams p) {
     constexpr int WC = 2, WP = 4, CF = 2, PF = 4;
@@ -618,18 +620,17 @@ conv_tr_merged(const ConvParams p) {
 
     // Tap tables in registers (compile-time indices below), so that the kernel argument block
     // is never indexed at run time.
-    int ntp[4], base[4], tdy[4][4], tdx[4][4];
-    base[0] = 0;
+    static_assert(N0 + N1 + N2 + N3 == NTALL, "tap counts");
+    constexpr int NTP[4] = {N0, N1, N2, N3};
+    constexpr int BASE[4] = {0, N0, N0 + N1, N0 + N1 + N2};
+    int tdy[4][4], tdx[4][4];
 #pragma unroll
-    for (int ph = 0; ph < 4; ++ph) {
-        ntp[ph] = p.ntaps[ph];
-        if (ph < 3) base[ph + 1] = base[ph] + ntp[ph];
+    for (int ph = 0; ph < 4; ++ph)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            tdy[ph][t] = p.tap_dy[ph][t];
-            tdx[ph][t] = p.tap_dx[ph][t];
+            tdy[ph][t] = t < NTP[ph] ? p.tap_dy[ph][t] : 0;
+            tdx[ph][t] = t < NTP[ph] ? p.tap_dx[ph][t] : 0;
         }
-    }
     const int nchunks = p.nchunks, cin_g = p.cin_g;
 
     auto issue = [&](int chunk, int buf) __attribute__((always_inline)) {
@@ -667,9 +668,8 @@ conv_tr_merged(const ConvParams p) {
         auto phase_taps = [&](auto phc) __attribute__((always_inline)) {
             constexpr int ph = decltype(phc)::value;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                if (t >= ntp[ph]) break;
-                const int e = base[ph] + t;
+            for (int t = 0; t < NTP[ph]; ++t) {
+                const int e = BASE[ph] + t;
                 const int dy = tdy[ph][t], dx = tdx[ph][t];
                 u32x4 a[CF], b[PF];
 #pragma unroll
@@ -764,13 +764,28 @@ hipError_t launch_conv_tr_merged(int dtype, const ConvParams& p0, hipStream_t s)
     p.gy = ((p.OH + 1) / 2 + 15) / 16;
     const long long total = (long long)p.gx * p.gy * p.N * p.ntiles;
     if (total <= 0 || total > (1ll << 30)) return hipErrorInvalidValue;
+    const bool pad1 = p.ntaps[0] == 1 && p.ntaps[1] == 2 && p.ntaps[2] == 2 && p.ntaps[3] == 4;
+    const bool pad02 = p.ntaps[0] == 4 && p.ntaps[1] == 2 && p.ntaps[2] == 2 && p.ntaps[3] == 1;
+    if (!pad1 && !pad02) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)total), block(512);
+#define ZJAI_TRM(TY)                                                                                 \
+    do {                                                                                             \
+        if (pad1) hipLaunchKernelGGL((conv_tr_merged<TY, 1, 2, 2, 4>), grid, block, 0, s, p);       \
+        else hipLaunchKernelGGL((conv_tr_merged<TY, 4, 2, 2, 1>), grid, block, 0, s, p);            \
+    } while (0)
     switch (dtype) {
-        case DT_F32: hipLaunchKernelGGL(conv_tr_merged<float>, dim3((unsigned)total), dim3(512), 0, s, p); break;
-        case DT_F16: hipLaunchKernelGGL(conv_tr_merged<_Float16>, dim3((unsigned)total), dim3(512), 0, s, p); break;
-        case DT_BF16: hipLaunchKernelGGL(conv_tr_merged<__bf16>, dim3((unsigned)total), dim3(512), 0, s, p); break;
+        case DT_F32: ZJAI_TRM(float); break;
+        case DT_F16: ZJAI_TRM(_Float16); break;
+        case DT_BF16: ZJAI_TRM(__bf16); break;
         default: return hipErrorInvalidValue;
     }
+#undef ZJAI_TRM
     return hipGetLastError();
+}
+
+bool conv_tr_merged_taps_supported(const int (&ntaps)[4]) {
+    return (ntaps[0] == 1 && ntaps[1] == 2 && ntaps[2] == 2 && ntaps[3] == 4) ||
+           (ntaps[0] == 4 && ntaps[1] == 2 && ntaps[2] == 2 && ntaps[3] == 1);
 }
 
 // ---------------------------------------------------------------------------------------------

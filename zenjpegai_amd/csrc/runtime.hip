@@ -395,8 +395,7 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
     }
     L->wpk = upload_as(ctx, pk, dtype, &L->wpk_bytes);
     if (bias) L->bias = upload_f32(bias, cout);
-    if (k == 3 && cout > 8 && L->ntaps[0] + L->ntaps[1] + L->ntaps[2] + L->ntaps[3] == TR_MERGED_TAPS &&
-        L->nblk_g % TR_MERGED_NB == 0) {
+    if (k == 3 && cout > 8 && conv_tr_merged_taps_supported(L->ntaps) && L->nblk_g % TR_MERGED_NB == 0) {
         // All four phases per workgroup (launch_conv_tr_merged): the nine taps side by side per
         // K chunk and block, phase by phase, each phase's taps in its table order.
         std::vector<float> pm((size_t)L->nchunks * L->nblk_g * TR_MERGED_TAPS * 16 * CK, 0.0f);
@@ -611,7 +610,11 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
         static const char* ty[] = {"float", "_Float16", "__bf16"};
         p.w = L.wpk_m;
         p.ntiles = L.nblk_g / TR_MERGED_NB;
-        LaunchScope sc(ctx, std::string("conv_tr_merged<") + ty[L.dtype] + ">", 2.0 * macs,
+        LaunchScope sc(ctx,
+                       std::string("conv_tr_merged<") + ty[L.dtype] + ", " + std::to_string(L.ntaps[0]) + ", " +
+                           std::to_string(L.ntaps[1]) + ", " + std::to_string(L.ntaps[2]) + ", " +
+                           std::to_string(L.ntaps[3]) + ">",
+                       2.0 * macs,
                        bytes - (double)L.wpk_bytes + (double)L.wpk_m_bytes);
         ZJAI_HIP(launch_conv_tr_merged(L.dtype, p, ctx.stream));
         return y;
