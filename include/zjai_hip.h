@@ -282,6 +282,16 @@ ZJAI_API int32_t zjai_picture_set_lanes(zjai_ctx* ctx, zjai_picture* pic, int32_
 /* Copies the planes out (synchronises): Y out_h*out_w, U/V ceil(out_h/sv)*ceil(out_w/sh)
  * samples each, as float (bit_depth 0) or uint16. u/v may be NULL without net_uv. */
 ZJAI_API int32_t zjai_picture_download(zjai_ctx* ctx, zjai_picture* pic, void* y, void* u, void* v);
+/* Page-locked host memory (hipHostMalloc) of `bytes` bytes, 16-byte aligned, for the host
+ * buffers of zjai_picture_upload / zjai_picture_download and the other copies: the device reads
+ * and writes it directly at the link's DMA rate, where pageable memory goes through the
+ * runtime's staging copies (config 5 fp32 from latents on the host to planes on the host: 36.6
+ * -> 34.8 ms). No counterpart in the reference, whose host buffers are plain `Vec`s
+ * (src/nn/fast/tensor.rs); for callers that keep transfer buffers across pictures. Release with
+ * zjai_host_free (ctx may be NULL there: the memory outlives the context); bytes == 0 is an
+ * error. */
+ZJAI_API int32_t zjai_host_alloc(zjai_ctx* ctx, size_t bytes, void** out);
+ZJAI_API int32_t zjai_host_free(zjai_ctx* ctx, void* p);
 
 /* ------------------------------------------------------------------------ output stage */
 

@@ -228,6 +228,43 @@ def test_picture_lanes_are_bit_identical(engines, prec):
                 assert np.array_equal(g, r), lanes
 
 
+def test_picture_with_page_locked_host_buffers(engines):
+    """Latents uploaded from and planes downloaded into page-locked host memory
+    (zjai_host_alloc) give the pageable path's planes, bit for bit, picture after picture; a
+    wrongly shaped output array is rejected; the buffers outlive their engine."""
+    eng = nn.Engine(0, "f32")
+    h, w, op = 192, 256, "hop"
+    lh, lw = h // 16, w // 16
+    py = synth.random_params(op, "y", seed=43, gain=0.5)
+    puv = synth.random_params(op, "uv", seed=43, gain=0.5)
+    y = synth.latent(43, "pin/y", 160, lh, lw)
+    uv = synth.latent(43, "pin/uv", 96, lh, lw)
+    tiles = model.synthesis_tiles(h, w, lh, lw, (128, 64), (1, 1))
+    pic = model.Picture(eng, model.SynthesisPrimary.load(py, op, eng),
+                        model.SynthesisSecondary.load(puv, op, eng), lh, lw, h, w, tiles, 2, 2, bit_depth=10)
+    pic.upload(y, uv)
+    pic.run()
+    ref = pic.download()
+    yp, uvp = eng.host_array(y.shape), eng.host_array(uv.shape)
+    assert not yp.any()
+    yp[...], uvp[...] = y, uv
+    out = (eng.host_array((h, w), np.uint16), eng.host_array((h // 2, w // 2), np.uint16),
+           eng.host_array((h // 2, w // 2), np.uint16))
+    for _ in range(2):
+        pic.upload(yp, uvp)
+        pic.run()
+        got = pic.download(out)
+        assert all(g is o for g, o in zip(got, out))
+        for g, r in zip(got, ref):
+            assert np.array_equal(g, r)
+    with pytest.raises(nn.HipError):
+        pic.download((out[0], out[1][:, :-1], out[2]))
+    del pic
+    eng.close()
+    assert np.array_equal(out[0], ref[0])  # still readable after the engine is gone
+    del out, yp, uvp
+
+
 def test_picture_10bit_and_float(engines):
     eng = engines["f32"]
     got, want = _picture(eng, "sop", 128, 192, (96, 32), None, 2, 2, 10, seed=33)

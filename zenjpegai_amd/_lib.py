@@ -126,6 +126,8 @@ PROTOTYPES = {
     "zjai_picture_run": [_vp, _vp],
     "zjai_picture_set_lanes": [_vp, _vp, _i32],
     "zjai_picture_download": [_vp, _vp, _vp, _vp, _vp],
+    "zjai_host_alloc": [_vp, _sz, _pp],
+    "zjai_host_free": [_vp, _vp],
     "zjai_resize": [_vp, _i32, _f32p, _i32, _i32, _i32, _i32, _i32, _f32p],
     "zjai_picture_download_rgb": [_vp, _vp, _i32, _vp, _f32p],
     "zjai_region_grid": [_i32, _i32, _i32, ctypes.POINTER(ZjaiRegions), _i32,

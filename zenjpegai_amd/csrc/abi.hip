@@ -936,6 +936,21 @@ extern "C" int32_t zjai_picture_download(zjai_ctx* ctx, zjai_picture* pic, void*
     });
 }
 
+extern "C" int32_t zjai_host_alloc(zjai_ctx* ctx, size_t bytes, void** out) {
+    if (!ctx || !out || bytes == 0) return ZJAI_E_INVALID_ARGUMENT;
+    *out = nullptr;
+    return guard(ctx, [&] {
+        void* p = nullptr;
+        ZJAI_HIP(hipHostMalloc(&p, bytes, hipHostMallocDefault));
+        *out = p;
+    });
+}
+
+extern "C" int32_t zjai_host_free(zjai_ctx* ctx, void* p) {
+    if (!p) return ZJAI_OK;
+    return guard(ctx, [&] { ZJAI_HIP(hipHostFree(p)); });
+}
+
 // ------------------------------------------------------------------------- output stage
 extern "C" int32_t zjai_resize(zjai_ctx* ctx, int32_t mode, const float* src, int32_t c, int32_t h,
                                int32_t w, int32_t out_h, int32_t out_w, float* dst) {

@@ -184,12 +184,23 @@ class Picture:
     def run(self):
         check(lib().zjai_picture_run(self.eng.handle, self._h), self.eng.handle)
 
-    def download(self):
+    def download(self, out=None):
+        """The Y, U, V planes (U, V None without a chroma net); ``out``: preallocated (y, u, v)
+        arrays of the right shapes and dtype to fill instead, e.g. from ``Engine.host_array``."""
         dt = np.uint16 if self.bit_depth else np.float32
-        y = np.empty((self.out_h, self.out_w), dt)
         ch, cw = -(-self.out_h // self.sv), -(-self.out_w // self.sh)
-        u = np.empty((ch, cw), dt) if self.secondary else None
-        v = np.empty((ch, cw), dt) if self.secondary else None
+        if out is not None:
+            y, u, v = out
+            want = [(y, (self.out_h, self.out_w))] + ([(u, (ch, cw)), (v, (ch, cw))] if self.secondary else [])
+            for a, shape in want:
+                if a is None or a.shape != shape or a.dtype != dt or not a.flags.c_contiguous:
+                    raise HipError(_lib.E_INVALID_ARGUMENT, "download: output arrays of the wrong shape or dtype")
+            if not self.secondary:
+                u = v = None
+        else:
+            y = np.empty((self.out_h, self.out_w), dt)
+            u = np.empty((ch, cw), dt) if self.secondary else None
+            v = np.empty((ch, cw), dt) if self.secondary else None
         check(lib().zjai_picture_download(
             self.eng.handle, self._h, y.ctypes.data_as(ctypes.c_void_p),
             u.ctypes.data_as(ctypes.c_void_p) if u is not None else None,

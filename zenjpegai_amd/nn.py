@@ -8,6 +8,7 @@ operations. Every call goes through the C-ABI of ``libzjai_hip.so``.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -85,8 +86,8 @@ class Engine:
     (device + stream) and the precision layers are packed for ("f32", "f16" or "bf16")."""
 
     def __init__(self, device: int = 0, precision: str = "f32", flags: int = 0):
-        """``flags``: 0 or ``_lib.CTX_UNFUSED_BLOCKS`` (the transformer blocks as separate
-        kernels instead of the fused ones the 16-bit precisions use)."""
+        """``flags``: 0 or an OR of ``_lib.CTX_*`` (``CTX_UNFUSED_BLOCKS``: the transformer
+        blocks as separate kernels instead of the fused ones every precision uses)."""
         self.precision = precision
         self.dtype = _lib.PRECISIONS[precision]
         self._h = ctypes.c_void_p()
@@ -98,6 +99,20 @@ class Engine:
 
     def sync(self):
         check(lib().zjai_sync(self._h), self._h)
+
+    def host_array(self, shape, dtype=np.float32) -> np.ndarray:
+        """A zeroed numpy array in page-locked host memory (``zjai_host_alloc``), for transfer
+        buffers reused across pictures; freed with the array (``zjai_host_free``, which needs no
+        context, so the array may outlive the engine)."""
+        dt = np.dtype(dtype)
+        n = int(np.prod(shape)) * dt.itemsize
+        p = ctypes.c_void_p()
+        check(lib().zjai_host_alloc(self._h, max(n, 1), ctypes.byref(p)), self._h)
+        buf = (ctypes.c_byte * max(n, 1)).from_address(p.value)
+        arr = np.frombuffer(buf, dtype=np.uint8, count=n).view(dt).reshape(shape)
+        arr[...] = 0
+        weakref.finalize(buf, lib().zjai_host_free, None, p)
+        return arr
 
     def set_stop(self, stop: bool):
         check(lib().zjai_set_stop(self._h, 1 if stop else 0), self._h)
