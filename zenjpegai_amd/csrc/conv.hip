@@ -338,7 +338,11 @@ conv_dma_f32(const ConvParams p) {
     constexpr int STG_U = SG * CH_U;
     constexpr int OUT_LD = NB * 16 + 4;
     constexpr int OUT_U = (TY * 16 * OUT_LD + 3) / 4;
-    constexpr int LDS_U = (2 * STG_U) > OUT_U ? (2 * STG_U) : OUT_U;
+    // Stride-2 stages (a 17 x 33 halo and 4 x 9 weight blocks, 73 KB) are single-buffered: two
+    // workgroups per CU then overlap each other's loads, where one double-buffered workgroup left
+    // one wave per SIMD.
+    constexpr int NBUF = S == 2 ? 1 : 2;
+    constexpr int LDS_U = (NBUF * STG_U) > OUT_U ? (NBUF * STG_U) : OUT_U;
     constexpr int HN = (HALO_U + NT - 1) / NT, WN = (W_U + NT - 1) / NT;
     __shared__ u32x4 s_lds[LDS_U];
 
@@ -446,8 +450,8 @@ conv_dma_f32(const ConvParams p) {
     for (int st = 0; st < nst; ++st) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of stage st are in LDS
         __syncthreads();                     // ... and every other wave's
-        if (st + 1 < nst) issue(st + 1, (st + 1) & 1);
-        const u32x4* sb = s_lds + (st & 1) * STG_U;
+        if (NBUF == 2 && st + 1 < nst) issue(st + 1, (st + 1) & 1);
+        const u32x4* sb = s_lds + (NBUF == 2 ? (st & 1) : 0) * STG_U;
         auto stage = [&](auto relu6) {
 #pragma unroll
             for (int s = 0; s < SG; ++s) {
@@ -479,6 +483,10 @@ conv_dma_f32(const ConvParams p) {
         };
         if (p.relu6_in) stage(std::true_type{});
         else stage(std::false_type{});
+        if (NBUF == 1 && st + 1 < nst) {
+            __syncthreads();  // every wave is done with the buffer
+            issue(st + 1, 0);
+        }
     }
 
     if (p.out_mode == OUT_NHWC && p.ps == 1) {
