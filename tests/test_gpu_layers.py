@@ -246,6 +246,7 @@ SMALL_GRID_CASES = [
     ("3x3", 192, 192, 24, 40, 256, "conv_igemm"),
     ("3x3", 192, 192, 80, 96, 256, "conv_igemm"),
     ("s2", 192, 192, 48, 80, 256, "conv_igemm"),
+    ("s2", 128, 128, 48, 80, 384, "conv_igemm"),  # 16-bit large map: 128-channel tiles
     ("convT", 192, 192, 20, 24, 160, "conv_igemm"),
     ("convT", 192, 192, 80, 80, 160, "conv_igemm"),
 ]

@@ -1178,7 +1178,7 @@ static hipError_t go_cfg(int kind, TileCfg c, const ConvParams& p, hipStream_t s
         return kind == CK_3x3 ? go<T, 3, 3, 1, false, 2, 4, 2, 4>(p, s) : hipErrorInvalidValue;
     if (c.wc == 4 && c.wp == 2 && c.cf == 2 && c.pf == 4) {
         if constexpr (sizeof(T) == 4) return kind == CK_1x1 ? go<T, 1, 1, 1, false, 4, 2, 2, 4>(p, s) : hipErrorInvalidValue;
-        return hipErrorInvalidValue;
+        return kind == CK_3x3_S2 ? go<T, 3, 3, 2, false, 4, 2, 2, 4>(p, s) : hipErrorInvalidValue;
     }
 #define ZJAI_GO(a, b, cc, d) \
     if (c.wc == a && c.wp == b && c.cf == cc && c.pf == d) return go_kind<T, a, b, cc, d>(kind, p, s);

@@ -455,7 +455,10 @@ static TileCfg launch_tile_cfg(const Layer& L, int N, int OH, int OW) {
     }
     if (L.kind == CK_3x3_S2 && c.wc == 2 && c.wp == 2 && c.cf == 2 && c.pf == 4) {
         const long long w0 = (long long)((OW + 15) / 16) * ((OH + 7) / 8) * N * nt4;
-        return w0 < 128 ? TileCfg{1, 4, 1, 2} : c;
+        if (w0 < 128) return TileCfg{1, 4, 1, 2};
+        // 16-bit: 128-channel tiles (8 waves) share each staged halo between twice the outputs.
+        if (L.dtype != DT_F32 && L.nblk_g % 8 == 0 && w0 >= 512) return TileCfg{4, 2, 2, 4};
+        return c;
     }
     if (L.kind == CK_T3 && L.wpk_m && c.wc == 2 && c.wp == 2 && c.cf == 2 && c.pf == 4) {
         // 3x3 transposed layers whose merged grid is small (see convT_merged_fills).
