@@ -117,3 +117,33 @@ def test_config5_16bit_psnr(he05, prec):
               f"max step {mx}, {n / size:.2%} of samples differ")
         assert np.isfinite(g).all() and psnr >= (35.0 if prec == "f16" else 28.0)
     eng.close()
+
+
+def test_config5_f32_output_does_not_depend_on_the_batching():
+    """Every f32 kernel choice sums each output in the same order, so a tile's planes must not
+    change with the batch it runs in: the 24-tile picture (four batches of 6) against two
+    12-tile pictures of 3 tiles per shape (batches of 3, so other launch grids and tile shapes),
+    compared bit for bit on each tile's core (float planes)."""
+    py, puv, y, uv = _workload(5, 0.5)
+    eng = nn.Engine(0, "f32")
+    tiles = model.synthesis_tiles(H, W, LH, LW, (640, 128), (2, 3))
+    prim = model.SynthesisPrimary.load(py, "hop", eng)
+    sec = model.SynthesisSecondary.load(puv, "hop", eng)
+    full = model.synthesize(eng, prim, sec, y, uv, H, W, tiles, 2, 2, bit_depth=0, lanes=4)
+    by_shape = {}
+    for t in tiles:
+        by_shape.setdefault((t.image.height, t.image.width), []).append(t)
+    assert sorted(len(v) for v in by_shape.values()) == [6, 6, 6, 6]
+    for half in (0, 1):
+        sub = [t for v in by_shape.values() for t in v[half::2]]
+        got = model.synthesize(eng, prim, sec, y, uv, H, W, sub, 2, 2, bit_depth=0, lanes=4)
+        for t in sub:
+            c = t.core
+            assert c.x % 2 == 0 and c.y % 2 == 0 and c.width % 2 == 0 and c.height % 2 == 0
+            rects = [(full[0], got[0], c.y, c.x, c.height, c.width)]
+            rects += [(f, g, c.y // 2, c.x // 2, c.height // 2, c.width // 2) for f, g in zip(full[1:], got[1:])]
+            for f, g, r0, c0, h, w in rects:
+                a = f[r0:r0 + h, c0:c0 + w]
+                b = g[r0:r0 + h, c0:c0 + w]
+                assert a.size > 0 and np.array_equal(a.view(np.uint32), b.view(np.uint32)), (half, c)
+    eng.close()
