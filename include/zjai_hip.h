@@ -75,8 +75,8 @@ typedef struct zjai_picture zjai_picture;
 
 /* Replaces `Engine` construction (src/nn/fast/mod.rs:128-172) for the HIP backend: binds a
  * device and creates its stream. flags: 0 or an OR of ZJAI_CTX_UNFUSED_BLOCKS,
- * ZJAI_CTX_PHASE_SPLIT_CONVT, ZJAI_CTX_MFMA16_CONV3X3 and ZJAI_CTX_IGEMM_CONV1X1 (other bits are
- * rejected). */
+ * ZJAI_CTX_PHASE_SPLIT_CONVT, ZJAI_CTX_MFMA16_CONV3X3, ZJAI_CTX_IGEMM_CONV1X1 and
+ * ZJAI_CTX_COUNT_F16_RANGE (other bits are rejected). */
 /* Run the transformer blocks (src/model/attention.rs:328-372) as the reference's separate ops --
  * layer norm, 1x1, depthwise (+ ELU gate), 1x1 -- instead of the fused kernels every precision
  * uses by default for `prep_data` (LN + 1x1 + depthwise) and for the feed-forward half (the two
@@ -93,6 +93,13 @@ typedef struct zjai_picture zjai_picture;
 /* Run the 1x1 convolutions on the implicit-GEMM conv kernel instead of the dedicated 1x1 GEMM
  * kernel (same results bit for bit; for A/B runs and the test that proves it). */
 #define ZJAI_CTX_IGEMM_CONV1X1 0x8u
+/* Count the f16 activations the context's kernels store as non-finite: an IEEE overflow (a
+ * value whose rounding exceeds 65504 is stored as +-inf) or a NaN. After every launch that writes
+ * an f16 tensor a scan adds the tensor's non-finite samples to a device counter, read by
+ * zjai_get_stats (`f16_nonfinite`). No counterpart in the reference (its f16 study rounds
+ * weights only, src/weights/f16.rs:70-72, with f32 activations); it tells whether a 16-bit run of
+ * a net stayed inside f16's range. Off by default: one extra pass over every f16 tensor. */
+#define ZJAI_CTX_COUNT_F16_RANGE 0x10u
 ZJAI_API int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out);
 ZJAI_API int32_t zjai_ctx_destroy(zjai_ctx* ctx);
 /* Copies the last failure message (NUL-terminated, truncated to len). Works with ctx == NULL
@@ -111,9 +118,23 @@ typedef struct zjai_stats {
     uint64_t pool_in_use;     /* device bytes held by live tensors */
     uint64_t pool_peak;       /* high-water mark of pool_in_use */
     uint64_t pool_cached;     /* device bytes held by the pool in total */
+    uint64_t f16_nonfinite;   /* ZJAI_CTX_COUNT_F16_RANGE: non-finite f16 samples stored so far */
 } zjai_stats;
-/* Replaces the reference's `DecodeStats` probe (src/decoder/stats.rs:301) for device work. */
+/* Replaces the reference's `DecodeStats` probe (src/decoder/stats.rs:301) for device work. With
+ * ZJAI_CTX_COUNT_F16_RANGE it synchronises the context's streams to read the counter. */
 ZJAI_API int32_t zjai_get_stats(zjai_ctx* ctx, zjai_stats* out);
+/* Host-side failure injection for tests of the error paths. After `after` more successful
+ * events of kind `what` the next one fails, once: ZJAI_FAIL_ALLOC counts device pool
+ * allocations (cached or not) and fails one as an out-of-memory hipMalloc does
+ * (ZJAI_E_LIMIT); ZJAI_FAIL_LAUNCH counts kernel launches and fails one as a failed launch does
+ * (ZJAI_E_DEVICE). The failure is raised on the host before the allocation or launch, so nothing
+ * faulty reaches the device, and the context stays usable. ZJAI_FAIL_NONE disarms. It exercises
+ * the reference GPU backend's rule that such failures mean "fall back to the CPU engine"
+ * (gpu/src/error.rs:6-25). */
+#define ZJAI_FAIL_NONE 0
+#define ZJAI_FAIL_ALLOC 1
+#define ZJAI_FAIL_LAUNCH 2
+ZJAI_API int32_t zjai_inject_failure(zjai_ctx* ctx, int32_t what, int64_t after);
 /* Per-launch profile, the device-side counterpart of the reference's GPU `Timing` / per-dispatch
  * profile (gpu/src/synthesis.rs:758): between begin and end every kernel launch of the context
  * is bracketed by HIP events on its stream. zjai_profile_end synchronises and writes up to `cap`

@@ -119,13 +119,15 @@ def test_config5_16bit_psnr(he05, prec):
     eng.close()
 
 
-def test_config5_f32_output_does_not_depend_on_the_batching():
-    """Every f32 kernel choice sums each output in the same order, so a tile's planes must not
-    change with the batch it runs in: the 24-tile picture (four batches of 6) against two
-    12-tile pictures of 3 tiles per shape (batches of 3, so other launch grids and tile shapes),
-    compared bit for bit on each tile's core (float planes)."""
+@pytest.mark.parametrize("prec", ["f32", "bf16"])
+def test_config5_output_does_not_depend_on_the_batching(prec):
+    """Every kernel choice is either made from one batch item's geometry or sums each output in
+    the same order as its alternatives, so a tile's planes must not change with the batch it runs
+    in: the 24-tile picture (four batches of 6) against two 12-tile pictures of 3 tiles per shape
+    (batches of 3, so other launch grids and tile shapes), compared bit for bit on each tile's
+    core (float planes), in f32 and in bf16."""
     py, puv, y, uv = _workload(5, 0.5)
-    eng = nn.Engine(0, "f32")
+    eng = nn.Engine(0, prec)
     tiles = model.synthesis_tiles(H, W, LH, LW, (640, 128), (2, 3))
     prim = model.SynthesisPrimary.load(py, "hop", eng)
     sec = model.SynthesisSecondary.load(puv, "hop", eng)

@@ -109,7 +109,8 @@ def test_noalloc_attention_equals_the_allocating_entry_point(prec, dim, heads):
 
 def test_noalloc_attention_rejects_a_map_beyond_the_scratch():
     """Checked on the host before any launch: 1024 x 1024 positions at dim 128 need ~71 MB of
-    Gram partials, more than the 16 MiB scratch. The buffers are never touched."""
+    Gram partials, more than the 16 MiB scratch; dim 640 exceeds the Gram kernel's LDS stage.
+    The buffers are never touched."""
     eng = nn.Engine(0, "f32")
     hip = _hip()
     d = DevBuf(hip, 4096)
@@ -120,6 +121,11 @@ def test_noalloc_attention_rejects_a_map_beyond_the_scratch():
         rc = _lib.lib().zjai_channel_attention_noalloc(eng.handle, d.p, 384, 16, 16, 5, d.p,
                                                        _lib.F32, d.p)
         assert rc == _lib.E_INVALID_ARGUMENT
+        # dim 640 (20 heads of 32): the Gram kernel's LDS stage would exceed 160 KB; refused as
+        # Unsupported before the padding fill or any other launch.
+        rc = _lib.lib().zjai_channel_attention_noalloc(eng.handle, d.p, 1920, 4, 4, 20, d.p,
+                                                       _lib.F32, d.p)
+        assert rc == _lib.E_UNSUPPORTED
     finally:
         d.free()
     eng.close()

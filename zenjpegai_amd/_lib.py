@@ -37,6 +37,8 @@ CTX_UNFUSED_BLOCKS = 0x1  # zjai_ctx_create flags
 CTX_PHASE_SPLIT_CONVT = 0x2
 CTX_MFMA16_CONV3X3 = 0x4
 CTX_IGEMM_CONV1X1 = 0x8
+CTX_COUNT_F16_RANGE = 0x10
+FAIL_NONE, FAIL_ALLOC, FAIL_LAUNCH = 0, 1, 2  # zjai_inject_failure kinds
 RESIZE_BICUBIC, RESIZE_BILINEAR = 0, 1
 PLANE_LATENT, PLANE_PSI, PLANE_HYPER_LATENT, PLANE_IMAGE = 0, 1, 2, 3
 
@@ -59,7 +61,7 @@ class ZjaiArea(ctypes.Structure):
 class ZjaiStats(ctypes.Structure):
     _fields_ = [("last_run_ms", ctypes.c_float), ("kernel_launches", ctypes.c_int64),
                 ("pool_in_use", ctypes.c_uint64), ("pool_peak", ctypes.c_uint64),
-                ("pool_cached", ctypes.c_uint64)]
+                ("pool_cached", ctypes.c_uint64), ("f16_nonfinite", ctypes.c_uint64)]
 
 
 class ZjaiProfRecord(ctypes.Structure):
@@ -83,6 +85,7 @@ PROTOTYPES = {
     "zjai_set_stop": [_vp, _i32],
     "zjai_get_stats": [_vp, ctypes.POINTER(ZjaiStats)],
     "zjai_release_buffers": [_vp],
+    "zjai_inject_failure": [_vp, _i32, ctypes.c_int64],
     "zjai_profile_begin": [_vp],
     "zjai_profile_end": [_vp, ctypes.POINTER(ZjaiProfRecord), _i32, _i32p],
     "zjai_tensor_create": [_vp, _i32, _i32, _i32, _i32, _pp],

@@ -112,7 +112,7 @@ extern "C" int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** ou
     if (!out) return ZJAI_E_INVALID_ARGUMENT;
     *out = nullptr;
     if (flags & ~(ZJAI_CTX_UNFUSED_BLOCKS | ZJAI_CTX_PHASE_SPLIT_CONVT | ZJAI_CTX_MFMA16_CONV3X3 |
-                  ZJAI_CTX_IGEMM_CONV1X1))
+                  ZJAI_CTX_IGEMM_CONV1X1 | ZJAI_CTX_COUNT_F16_RANGE))
         return guard(nullptr, [] { throw Error(ZJAI_E_INVALID_ARGUMENT, "zjai_ctx_create: unknown flags"); });
     zjai_ctx* ctx = new (std::nothrow) zjai_ctx();
     if (!ctx) return ZJAI_E_LIMIT;
@@ -184,7 +184,19 @@ extern "C" int32_t zjai_get_stats(zjai_ctx* ctx, zjai_stats* out) {
     out->pool_in_use = ctx->c.pool.in_use();
     out->pool_peak = ctx->c.pool.peak();
     out->pool_cached = ctx->c.pool.cached();
-    return ZJAI_OK;
+    out->f16_nonfinite = 0;
+    if (!(ctx->c.flags & ZJAI_CTX_COUNT_F16_RANGE)) return ZJAI_OK;
+    return guard(ctx, [&] { out->f16_nonfinite = f16_range_total(ctx->c); });
+}
+
+extern "C" int32_t zjai_inject_failure(zjai_ctx* ctx, int32_t what, int64_t after) {
+    if (!ctx) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        need(what == ZJAI_FAIL_NONE || what == ZJAI_FAIL_ALLOC || what == ZJAI_FAIL_LAUNCH, "inject: unknown kind");
+        need(after >= 0, "inject: negative count");
+        ctx->c.faults->what = what == ZJAI_FAIL_ALLOC ? FAULT_ALLOC : what == ZJAI_FAIL_LAUNCH ? FAULT_LAUNCH : FAULT_NONE;
+        ctx->c.faults->left = after;
+    });
 }
 
 extern "C" int32_t zjai_profile_begin(zjai_ctx* ctx) {
@@ -428,6 +440,7 @@ extern "C" int32_t zjai_channel_attention(zjai_ctx* ctx, const zjai_tensor* qkv,
         const int dim = a.c / 3, c = dim / heads;
         need(dim % 8 == 0, "attention: dim must be a multiple of 8");
         need(c >= 1 && c <= 32, "attention: at most 32 channels per head");
+        if (!attention_gram_fits(a.dtype, dim)) throw Error(ZJAI_E_UNSUPPORTED, "attention: dim too large for the Gram kernel's LDS stage");
         // attn . v as a 1x1 conv over v with the block-diagonal attention matrix as its weight
         // (identity projection folded in).
         std::vector<float> eye((size_t)dim * dim, 0.0f);
@@ -457,6 +470,7 @@ extern "C" int32_t zjai_channel_attention_noalloc(zjai_ctx* ctx, const void* qkv
         const int dim = channels / 3, c = dim / heads;
         need(dim % 8 == 0, "attention: dim must be a multiple of 8");
         need(c >= 1 && c <= 32, "attention: at most 32 channels per head");
+        if (!attention_gram_fits(precision, dim)) throw Error(ZJAI_E_UNSUPPORTED, "attention: dim too large for the Gram kernel's LDS stage");
         need((((uintptr_t)qkv | (uintptr_t)out) & 15) == 0 && ((uintptr_t)temperature & 3) == 0,
              "attention: buffers not aligned (16 bytes; temperature 4)");
         // The dim x dim 1x1 projection (the identity) the attention is folded into, in the
@@ -855,6 +869,19 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
         if (nl > 1) {
             for (int i = 0; i < nl; ++i) ZJAI_HIP(hipStreamWaitEvent(root.lane(i).stream, root.ev0, 0));
         }
+        // A failure or cancellation part way through leaves the other lanes' batches queued:
+        // drain every stream before reporting it, so the picture and the context are idle and
+        // reusable when the call returns.
+        struct Drain {
+            Context& root;
+            int nl;
+            bool armed = true;
+            ~Drain() {
+                if (!armed) return;
+                for (int i = 0; i < nl && nl > 1; ++i) (void)hipStreamSynchronize(root.lane(i).stream);
+                (void)hipStreamSynchronize(root.stream);
+            }
+        } drain{root, nl};
         for (size_t bidx = 0; bidx < pic->batches.size(); ++bidx) {
             const std::vector<int>& group = pic->batches[bidx];
             Context& c = nl > 1 ? root.lane((int)bidx % nl) : root;
@@ -909,6 +936,7 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
                 ZJAI_HIP(hipStreamWaitEvent(root.stream, pic->lane_ev[i], 0));
             }
         }
+        drain.armed = false;
         ZJAI_HIP(hipEventRecord(root.ev1, root.stream));
         ZJAI_HIP(hipEventSynchronize(root.ev1));
         ZJAI_HIP(hipEventElapsedTime(&root.last_ms, root.ev0, root.ev1));

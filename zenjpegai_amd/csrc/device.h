@@ -95,10 +95,13 @@ __device__ __forceinline__ float cephes_exp(float x) {
     float y = p * (r * r);
     y = y + r;
     y = y + 1.0f;
-    // y * 2^n. After the clamps n is an integer in [-125, 127], so 2^n is a normal float and
-    // the product is exact scaling with one rounding: v_ldexp_f32 gives the same bits as
-    // multiplying by the constructed power of two (and a NaN x still gives a NaN, y being NaN).
-    return ldexpf(y, (int)n);
+    // y * 2^n. After the clamps n is an integer in [-126, 127] (x = -87 gives n = -126), so 2^n
+    // is a normal float and the product is exact scaling with one rounding: v_ldexp_f32 gives the
+    // same bits as multiplying by the constructed power of two. The clamps are comparisons, so a
+    // NaN x reaches here with n NaN; converting NaN to int is undefined, so it takes 0 instead
+    // (y is NaN then, and so is the result).
+    const int ni = (n != n) ? 0 : (int)n;
+    return ldexpf(y, ni);
 }
 
 __device__ __forceinline__ float sigmoidf_ref(float x) {

@@ -353,9 +353,12 @@ struct Fwd {
     }
     TensorP layer_norm(const std::string& pfx, const TensorP& x) {
         TensorP y = ctx.alloc(x->n, x->c, x->h, x->w, x->dtype);
-        LaunchScope sc(ctx, kname("k_layer_norm", x->dtype), 0.0, 2.0 * dtype_size(x->dtype) * x->n * x->c * x->h * x->w);
-        ZJAI_HIP(launch_layer_norm(x->v, y->v, x->dtype, x->n, x->c, x->h, x->w, net.vec.at(pfx + ".weight"),
-                                   net.vec.at(pfx + ".bias"), ctx.stream));
+        {
+            LaunchScope sc(ctx, kname("k_layer_norm", x->dtype), 0.0, 2.0 * dtype_size(x->dtype) * x->n * x->c * x->h * x->w);
+            ZJAI_HIP(launch_layer_norm(x->v, y->v, x->dtype, x->n, x->c, x->h, x->w, net.vec.at(pfx + ".weight"),
+                                       net.vec.at(pfx + ".bias"), ctx.stream));
+        }
+        count_f16_range(ctx, *y);
         return y;
     }
     // Profile name of a fused block kernel, as the kernel symbol reads: k_ffn<__bf16, 128>,
@@ -424,10 +427,13 @@ struct Fwd {
             a.dw_w = c2.dw_w;
             a.dw_b = c2.bias;
             const double npos = (double)x->n * x->h * x->w;
-            LaunchScope sc(ctx, fused_name("k_qkv", x->dtype, dim),
-                           2.0 * npos * (3.0 * dim * dim + 9.0 * 3 * dim),
-                           (double)dtype_size(x->dtype) * npos * 4 * dim);
-            ZJAI_HIP(launch_qkv_fused(a, x->dtype, dim, ctx.stream));
+            {
+                LaunchScope sc(ctx, fused_name("k_qkv", x->dtype, dim),
+                               2.0 * npos * (3.0 * dim * dim + 9.0 * 3 * dim),
+                               (double)dtype_size(x->dtype) * npos * 4 * dim);
+                ZJAI_HIP(launch_qkv_fused(a, x->dtype, dim, ctx.stream));
+            }
+            count_f16_range(ctx, *t);
         } else {
             t = layer_norm(p + ".prep_data.norm1", x);
             t = conv(p + ".prep_data.conv1", t);
@@ -466,10 +472,13 @@ struct Fwd {
             a.nblk_out = pout.nblk_g;
             a.b_out = pout.bias;
             const double npos = (double)x->n * x->h * x->w;
-            LaunchScope sc(ctx, fused_name("k_ffn", x->dtype, dim),
-                           2.0 * npos * (2.0 * hidden * dim + 9.0 * 2 * hidden + (double)hidden * dim),
-                           2.0 * dtype_size(x->dtype) * npos * dim);
-            ZJAI_HIP(launch_ffn_fused(a, x->dtype, dim, ctx.stream));
+            {
+                LaunchScope sc(ctx, fused_name("k_ffn", x->dtype, dim),
+                               2.0 * npos * (2.0 * hidden * dim + 9.0 * 2 * hidden + (double)hidden * dim),
+                               2.0 * dtype_size(x->dtype) * npos * dim);
+                ZJAI_HIP(launch_ffn_fused(a, x->dtype, dim, ctx.stream));
+            }
+            count_f16_range(ctx, *y);
             return y;
         }
         TensorP u = layer_norm(p + ".ffn.norm1", x);
@@ -482,6 +491,7 @@ struct Fwd {
             ZJAI_HIP(launch_depthwise3x3(u->v, f->v, u->dtype, u->n, 2 * hidden, u->h, u->w, dw.dw_w, dw.bias,
                                          hidden, ctx.stream));
         }
+        count_f16_range(ctx, *f);
         u.reset();
         Epilogue ef;
         ef.res = RES_ADD;

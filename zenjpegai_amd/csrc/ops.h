@@ -98,6 +98,9 @@ hipError_t launch_ffn_fused(const FfnArgs& a, int dtype, int dim, hipStream_t s)
 // 3. fold with the output projection proj [dim][dim] into a packed 1x1 conv weight per item
 //    (wpk + b * w_bstride).
 int attention_gram_chunks(int h, int w);
+// Whether the Gram kernel's LDS stage (64 16-bit or 32 f32 positions of 2 dim channels) fits the
+// 160 KB of a CU for this dim: callers check it before their first launch.
+bool attention_gram_fits(int dtype, int dim);
 hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads, int h, int w,
                                  float* partial, hipStream_t s);
 hipError_t launch_attention_softmax(const float* partial, int N, int nchunk, int dim, int heads,
@@ -107,6 +110,10 @@ hipError_t launch_attention_fold(const float* proj, const float* attn, int N, in
                                  hipStream_t s);
 // Zero `bytes` (a multiple of 4, 4-byte aligned) at p with a kernel.
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
+// Adds the non-finite f16 samples of an N x [h][w][C] view to slots[0 .. nslots) (nslots
+// workgroups, each adding to its own slot).
+hipError_t launch_count_f16_nonfinite(View v, int N, int C, int h, int w, unsigned long long* slots,
+                                      int nslots, hipStream_t s);
 
 // Latent reconstruction (src/decoder/reconstruct.rs:81-234), N regions of one shape per launch:
 // int8 planar z_hat windows (per item origin) -> NHWC view of the storage type;

@@ -560,8 +560,44 @@ __global__ void k_zero_u32(uint32_t* p, long long n, int tail) {
     }
 }
 
+// Non-finite f16 samples (exponent field all ones: +-inf from an overflow past 65504, or NaN) of
+// an N x [h][w][C] view, added to slots[blockIdx.x]. A fixed grid of `nslots` workgroups walks
+// the view; each workgroup sums its count in LDS and one thread adds it to its own slot, so no
+// two workgroups write one slot and successive launches on one stream accumulate in order.
+__global__ void __launch_bounds__(256) k_count_f16_nonfinite(View v, int N, int C, int h, int w,
+                                                             unsigned long long* slots) {
+    __shared__ unsigned int s_cnt[256];
+    const long long total = (long long)N * h * w * C;
+    const uint16_t* base = reinterpret_cast<const uint16_t*>(v.p);
+    unsigned int cnt = 0;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long long)gridDim.x * 256) {
+        const int c = (int)(i % C);
+        long long r = i / C;
+        const int x = (int)(r % w);
+        r /= w;
+        const int y = (int)(r % h);
+        const int b = (int)(r / h);
+        const uint16_t bits = base[(long long)b * v.bstride + (long long)y * v.row + (long long)x * v.cs + v.c_off + c];
+        cnt += (bits & 0x7c00u) == 0x7c00u ? 1u : 0u;
+    }
+    s_cnt[threadIdx.x] = cnt;
+    __syncthreads();
+    for (int k = 128; k > 0; k >>= 1) {
+        if ((int)threadIdx.x < k) s_cnt[threadIdx.x] += s_cnt[threadIdx.x + k];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0 && s_cnt[0]) slots[blockIdx.x] += s_cnt[0];
+}
+
 // ------------------------------------------------------------------------------- launchers
 static inline dim3 grid_for(long long n) { return dim3((unsigned)((n + 255) / 256)); }
+
+hipError_t launch_count_f16_nonfinite(View v, int N, int C, int h, int w, unsigned long long* slots,
+                                      int nslots, hipStream_t s) {
+    if (N <= 0 || C <= 0 || h <= 0 || w <= 0 || nslots <= 0) return hipSuccess;
+    k_count_f16_nonfinite<<<dim3((unsigned)nslots), 256, 0, s>>>(v, N, C, h, w, slots);
+    return hipGetLastError();
+}
 
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s) {
     if ((uintptr_t)p & 3) return hipErrorInvalidValue;
@@ -652,6 +688,12 @@ hipError_t launch_layer_norm(View src, View dst, int dtype, int N, int C, int h,
     return hipGetLastError();
 }
 
+bool attention_gram_fits(int dtype, int dim) {
+    if (dim <= 0) return false;
+    const size_t lds = (size_t)(dtype == DT_F32 ? 4 * GRAM_SUB<float> : 2 * GRAM_SUB<__bf16>) * (2 * dim + GRAM_PAD);
+    return lds <= 160 * 1024;
+}
+
 hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads, int h, int w,
                                  float* partial, hipStream_t s) {
     const int c = heads > 0 ? dim / heads : 0;
@@ -661,8 +703,8 @@ hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads,
         return hipErrorInvalidValue;
     const int nchunk = attention_gram_chunks(h, w);
     if (nchunk == 0 || N == 0) return hipSuccess;
+    if (!attention_gram_fits(dtype, dim)) return hipErrorInvalidValue;
     const size_t lds = (size_t)(dtype == DT_F32 ? 4 * GRAM_SUB<float> : 2 * GRAM_SUB<__bf16>) * (2 * dim + GRAM_PAD);
-    if (lds > 160 * 1024) return hipErrorInvalidValue;
     ZJAI_DISPATCH(dtype, k_attention_gram, <<<dim3(nchunk, N), 256, lds, s>>>(qkv, dim, heads, h * w, w, partial))
     return hipGetLastError();
 }

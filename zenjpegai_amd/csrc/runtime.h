@@ -30,6 +30,26 @@ inline int dtype_size(int dt) { return dt == DT_F32 ? 4 : 2; }
 inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// Host-side failure injection (zjai_inject_failure): after `left` more events of the armed kind
+// (FAULT_ALLOC: a pool allocation, cached or not; FAULT_LAUNCH: a kernel launch) the next one
+// throws, once, the error a failed hipMalloc (LimitExceeded) or a failed launch (device) throws.
+// Nothing reaches the device: the throw happens before the allocation or the launch.
+enum FaultKind : int { FAULT_NONE = 0, FAULT_ALLOC = 1, FAULT_LAUNCH = 2 };
+struct FaultPlan {
+    int what = FAULT_NONE;
+    long long left = 0;
+    // Called once per event of `kind`: true when this event is the one to fail (then disarms).
+    bool take(int kind) {
+        if (what != kind) return false;
+        if (left > 0) {
+            --left;
+            return false;
+        }
+        what = FAULT_NONE;
+        return true;
+    }
+};
+
 // Caching device allocator: freed blocks go back to a per-size free list and are reused, so a
 // steady-state decode allocates nothing (the reference's buffer pool, src/nn/fast/tensor.rs:21-119,
 // keeps its host buffers the same way).
@@ -41,6 +61,7 @@ public:
     size_t in_use() const { return in_use_; }
     size_t peak() const { return peak_; }
     size_t cached() const { return cached_; }
+    std::shared_ptr<FaultPlan> faults;  // the root context's plan (shared with its lanes)
     ~Pool();
 
 private:
@@ -79,6 +100,10 @@ struct Context {
     // context (a caller destroying the context first) still returns its block to a live pool.
     std::shared_ptr<Pool> pool_owner = std::make_shared<Pool>();
     Pool& pool = *pool_owner;
+    std::shared_ptr<FaultPlan> faults = std::make_shared<FaultPlan>();
+    // ZJAI_CTX_COUNT_F16_RANGE: per-workgroup counts of non-finite f16 samples written, one
+    // array per lane (each lane's scans run in its own stream order), summed by zjai_get_stats.
+    unsigned long long* range_slots = nullptr;
     std::string last_error;
     volatile int stop = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -100,6 +125,7 @@ struct Context {
     Context& lane(int i);
     Context& top() { return root ? *root : *this; }
 
+    Context() { pool.faults = faults; }
     TensorP alloc(int n, int c, int h, int w, int dtype);
     void check_stop();
     hipEvent_t take_event();
@@ -118,6 +144,13 @@ private:
     Context& c_;
     long idx_ = -1;
 };
+
+// ZJAI_CTX_COUNT_F16_RANGE: adds the non-finite samples of an f16 tensor just written on ctx's
+// stream to ctx's counters (no-op for other precisions or without the flag).
+void count_f16_range(Context& ctx, const Tensor& t);
+constexpr int RANGE_SLOTS = 256;
+// Sum of every lane's counters (synchronises the context's streams).
+unsigned long long f16_range_total(Context& root);
 
 // View of the top-left h x w corner (`BTensor::crop_par`, src/nn/fast/tensor.rs:349-367).
 TensorP crop_view(const TensorP& t, int h, int w);

@@ -17,6 +17,7 @@ size_t Pool::bucket(size_t bytes) {
 }
 
 void* Pool::alloc(size_t bytes) {
+    if (faults && faults->take(FAULT_ALLOC)) throw Error(ZJAI_E_LIMIT, "hipMalloc: injected allocation failure");
     const size_t b = bucket(bytes ? bytes : 256);
     auto it = free_.lower_bound(b);
     void* p = nullptr;
@@ -99,6 +100,8 @@ Context& Context::lane(int i) {
         auto l = std::make_unique<Context>();
         l->root = this;
         l->device = device;
+        l->faults = faults;
+        l->pool.faults = faults;
         ZJAI_HIP(hipSetDevice(device));
         ZJAI_HIP(hipStreamCreateWithFlags(&l->stream, hipStreamNonBlocking));
         l->owns_stream = true;
@@ -124,10 +127,36 @@ Context::~Context() {
         (void)hipStreamDestroy(stream);
     }
     for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
+    if (range_slots) (void)hipFree(range_slots);
+}
+
+void count_f16_range(Context& ctx, const Tensor& t) {
+    if (t.dtype != DT_F16 || !(ctx.top().flags & ZJAI_CTX_COUNT_F16_RANGE)) return;
+    if (!ctx.range_slots) {
+        ZJAI_HIP(hipMalloc(&ctx.range_slots, sizeof(unsigned long long) * RANGE_SLOTS));
+        ZJAI_HIP(launch_zero(ctx.range_slots, sizeof(unsigned long long) * RANGE_SLOTS, ctx.stream));
+    }
+    LaunchScope sc(ctx, "k_count_f16_nonfinite", 0.0, 2.0 * t.n * t.c * t.h * t.w);
+    ZJAI_HIP(launch_count_f16_nonfinite(t.v, t.n, t.c, t.h, t.w, ctx.range_slots, RANGE_SLOTS, ctx.stream));
+}
+
+unsigned long long f16_range_total(Context& root) {
+    unsigned long long total = 0;
+    std::vector<unsigned long long> h(RANGE_SLOTS);
+    auto add = [&](Context& c) {
+        if (!c.range_slots) return;
+        ZJAI_HIP(hipStreamSynchronize(c.stream));
+        ZJAI_HIP(hipMemcpy(h.data(), c.range_slots, sizeof(unsigned long long) * RANGE_SLOTS, hipMemcpyDeviceToHost));
+        for (unsigned long long v : h) total += v;
+    };
+    add(root);
+    for (auto& l : root.lanes) add(*l);
+    return total;
 }
 
 LaunchScope::LaunchScope(Context& c, const std::string& name, double flops, double bytes) : c_(c) {
     Context& t = c_.top();
+    if (t.faults->take(FAULT_LAUNCH)) throw Error(ZJAI_E_DEVICE, name + ": injected launch failure");
     ++t.launches;
     if (!t.profiling) return;
     ProfRec r;
@@ -493,8 +522,8 @@ std::string conv_kernel_name(int kind, int dtype, TileCfg c) {
 }
 static View view_of(const Tensor* t) { return t ? t->v : View{nullptr, 0, 0, 0, 0}; }
 
-TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilogue& e,
-                     const TensorP& dst, const PlaneOut* plane) {
+static TensorP conv_forward_impl(Context& ctx, const Layer& L, const TensorP& x, const Epilogue& e,
+                                 const TensorP& dst, const PlaneOut* plane) {
     if (x->c != L.cin) throw Error(ZJAI_E_INVALID_ARGUMENT, "conv: input channel count mismatch");
     if (x->dtype != L.dtype) throw Error(ZJAI_E_INVALID_ARGUMENT, "conv: input precision mismatch");
     const int N = x->n;
@@ -623,12 +652,16 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
         return y;
     }
     // conv3x3_m32's 256-position tiles carry twice the work of conv_igemm's 64-channel ones: with
-    // 128 input channels and fewer tiles than CUs the smaller tiles fill the chip better.
+    // 128 input channels and few tiles the smaller tiles fill the chip better. The two kernels
+    // sum each output in different orders (16 channels per MFMA against 32), so the choice is
+    // made from one batch item's tile count, never the batch's: a tile's 16-bit result does not
+    // depend on how many tiles of its shape share its launch. 43 tiles per item is 256 workgroups
+    // for the 6-tile batches of a 4K picture.
     const int tw32 = conv3x3_m32_width(OH, OW);
-    const long long tiles32 = L.wpk32 ? (long long)((OW + tw32 - 1) / tw32) * ((OH + 256 / tw32 - 1) / (256 / tw32)) *
-                                            N * (L.cout / L.mt32)
-                                      : 0;
-    if (L.wpk32 && (L.cin == 64 || tiles32 >= 256) && !e.w_batch && !plane && ps == 1 && !e.relu6_in &&
+    const long long item_tiles32 = L.wpk32 ? (long long)((OW + tw32 - 1) / tw32) *
+                                                 ((OH + 256 / tw32 - 1) / (256 / tw32)) * (L.cout / L.mt32)
+                                           : 0;
+    if (L.wpk32 && (L.cin == 64 || item_tiles32 >= 43) && !e.w_batch && !plane && ps == 1 && !e.relu6_in &&
         !(ctx.top().flags & ZJAI_CTX_MFMA16_CONV3X3)) {
         static const char* ty[] = {"float", "_Float16", "__bf16"};
         const int tw = tw32;
@@ -654,6 +687,13 @@ TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilo
     return y;
 }
 
+TensorP conv_forward(Context& ctx, const Layer& L, const TensorP& x, const Epilogue& e,
+                     const TensorP& dst, const PlaneOut* plane) {
+    TensorP y = conv_forward_impl(ctx, L, x, e, dst, plane);
+    if (y) count_f16_range(ctx, *y);
+    return y;
+}
+
 // -------------------------------------------------------------------- attention + projection
 std::shared_ptr<void> attention_fold(Context& ctx, const TensorP& qkv, int heads, const float* temperature,
                                      const Layer& proj, long long* w_bstride) {
@@ -661,6 +701,8 @@ std::shared_ptr<void> attention_fold(Context& ctx, const TensorP& qkv, int heads
     if (proj.kind != CK_1x1 || proj.groups != 1 || proj.depthwise || proj.transposed || !proj.w_f32 ||
         proj.cin != dim || proj.cout != dim || proj.dtype != qkv->dtype)
         throw Error(ZJAI_E_INVALID_ARGUMENT, "attention: projection is not a dense dim x dim 1x1 layer");
+    if (!attention_gram_fits(qkv->dtype, dim))
+        throw Error(ZJAI_E_UNSUPPORTED, "attention: dim too large for the Gram kernel's LDS stage");
     const int n = qkv->h * qkv->w, nchunk = std::max(attention_gram_chunks(qkv->h, qkv->w), 1);
     const int total = heads * (c * c + 2 * c);
     const double es = dtype_size(qkv->dtype);

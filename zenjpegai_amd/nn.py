@@ -136,6 +136,11 @@ class Engine:
     def release_buffers(self):
         check(lib().zjai_release_buffers(self._h), self._h)
 
+    def inject_failure(self, what: int, after: int = 0):
+        """Fail the next allocation (``_lib.FAIL_ALLOC``) or launch (``_lib.FAIL_LAUNCH``)
+        after ``after`` successful ones, from the host (``zjai_inject_failure``)."""
+        check(lib().zjai_inject_failure(self._h, what, after), self._h)
+
     def close(self):
         if self._h:
             lib().zjai_ctx_destroy(self._h)

@@ -225,6 +225,14 @@ def random_params(op: str, component: str, seed: int = 1, gain: float = 1.0,
     return params
 
 
+def f16_weights(params: dict) -> dict:
+    """The reference's f16-weight semantics (src/weights/f16.rs:70-72 ``round_trip``, as a
+    ``ZJB2`` bundle stores a synthesis net): every float tensor rounded to IEEE half (round to
+    nearest even, subnormals kept, overflow to infinity) and widened back, for nets that still
+    compute in f32."""
+    return {k: np.asarray(v, np.float32).astype(np.float16).astype(np.float32) for k, v in params.items()}
+
+
 # ---------------------------------------------------------------------------------------------
 # Latent reconstruction networks (hyper-decoder + multi-stage context model) of one component.
 # ---------------------------------------------------------------------------------------------
