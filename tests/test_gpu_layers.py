@@ -249,6 +249,8 @@ SMALL_GRID_CASES = [
     ("s2", 128, 128, 48, 80, 384, "conv_igemm"),  # 16-bit large map: 128-channel tiles
     ("convT", 192, 192, 20, 24, 160, "conv_igemm"),
     ("convT", 192, 192, 80, 80, 160, "conv_igemm"),
+    ("2x2", 160, 256, 64, 64, 160, "conv_igemm"),  # SOP up1 (extra pad right / bottom)
+    ("2x2", 64, 128, 128, 128, 256, "conv_igemm"),  # SOP up2
 ]
 
 
@@ -267,6 +269,10 @@ def test_small_grid_tiles_are_bit_identical(engines, prec, kind, cin, cout, h, w
         wt = _he(f"sg/w{kind}", (cin, cout, 3, 3), 9 * cin)
         layer = nn.ConvTransposeLayer(nn.ConvTranspose2d(cin, cout, 3, 2, 1, 1, wt, synth.normal(11, "sg/bt", (cout,), 0.05)), eng)
         oh, ow = 2 * h, 2 * w
+    elif kind == "2x2":
+        wt = _he(f"sg/w{kind}", (cout, cin, 2, 2), 4 * cin)
+        layer = nn.ConvLayer(nn.Conv2d(cin, cout, (2, 2), 1, (0, 0), 1, wt), eng, extra_pad=(0, 0, 1, 1))
+        oh, ow = h, w
     else:
         stride = 2 if kind == "s2" else 1
         wt = _he(f"sg/w{kind}", (cout, cin, 3, 3), 9 * cin)

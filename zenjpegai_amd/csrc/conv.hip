@@ -67,6 +67,8 @@ template <> __device__ __forceinline__ u32x4 relu6_vec<__bf16>(u32x4 v) {
 // SG: input-channel chunks staged per barrier. 1x1 layers do little matrix work per chunk, so
 // they stage several (SG = 4: the whole K of a 128-channel f16 layer) with every global load of
 // the stage issued before its LDS stores -- more bytes in flight per workgroup, fewer barriers.
+__device__ u32x4 g_zero_igemm[1];  // 16 zero bytes: the source of padding units
+
 template <typename T, int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF, int SG>
 __global__ void __launch_bounds__(WC * WP * 64)
 conv_igemm(const ConvParams p) {
@@ -164,78 +166,75 @@ conv_igemm(const ConvParams p) {
         }
     };
 
+    // Halo element offsets of this thread's units (u = tid + i * NT), -1 in the padding; the
+    // same for every K chunk.
+    long long hoff[HN];
+#pragma unroll
+    for (int i = 0; i < HN; ++i) {
+        const int u = tid + i * NT, pix = u >> 2, q = u & 3;
+        const int hy = pix / HX, hx = pix - hy * HX;
+        const int iy = iy0 + hy, ix = ix0 + hx;
+        hoff[i] = (u < HALO_U && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W)
+                      ? (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + q * VEC
+                      : -1;
+    }
+    // One K chunk's halo and weight units into registers. Every load is unconditional, from the
+    // unit's address or from a zeroed buffer (padding, channels past cin_g, units past the
+    // stage), so all of them are in flight together: a load inside a branch would be waited for
+    // before the next one issues.
+    auto load_chunk = [&](int chunk, u32x4 (&rh)[HN], u32x4 (&rw)[WN]) __attribute__((always_inline)) {
+        const int cl0 = chunk * CK;
+#pragma unroll
+        for (int i = 0; i < HN; ++i) {
+            const int q = (tid + i * NT) & 3;
+            const bool ok = hoff[i] >= 0 && cl0 + q * VEC < p.cin_g;
+            rh[i] = *(ok ? (const u32x4*)(xg + hoff[i] + cl0) : g_zero_igemm);
+        }
+        const u32x4* wsrc = (const u32x4*)(wg + ((long long)(g * p.nchunks + chunk) * p.nblk_g + nb0) *
+                                                     (long long)(NTAP * 16 * CK));
+#pragma unroll
+        for (int i = 0; i < WN; ++i) {
+            const int u = tid + i * NT;
+            rw[i] = *(u < W_U ? wsrc + u : g_zero_igemm);
+        }
+    };
+    auto store_chunk = [&](u32x4* dst, const u32x4 (&rh)[HN], const u32x4 (&rw)[WN]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < HN; ++i) {
+            const int u = tid + i * NT;
+            u32x4 v = rh[i];
+            if (p.relu6_in) v = relu6_vec<T>(v);
+            if (u < HALO_U) dst[u] = v;
+        }
+#pragma unroll
+        for (int i = 0; i < WN; ++i) {
+            const int u = tid + i * NT;
+            if (u < W_U) dst[HALO_U + u] = rw[i];
+        }
+    };
+
     if constexpr (SG == 1) {
+        // The next chunk's loads fly during this chunk's MFMAs.
+        u32x4 rh[HN], rw[WN];
+        load_chunk(0, rh, rw);
         for (int chunk = 0; chunk < p.nchunks; ++chunk) {
             __syncthreads();
-            const int cl0 = chunk * CK;
-            for (int u = tid; u < HALO_U; u += NT) {
-                const int pix = u >> 2, q = u & 3;
-                const int hy = pix / HX, hx = pix - hy * HX;
-                const int iy = iy0 + hy, ix = ix0 + hx, cl = cl0 + q * VEC;
-                u32x4 v = {0u, 0u, 0u, 0u};
-                if (iy >= 0 && iy < p.H && ix >= 0 && ix < p.W && cl < p.cin_g) {
-                    v = *(const u32x4*)(xg + (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + cl);
-                    if (p.relu6_in) v = relu6_vec<T>(v);
-                }
-                s_lds[u] = v;
-            }
-            const u32x4* wsrc = (const u32x4*)(wg + ((long long)(g * p.nchunks + chunk) * p.nblk_g + nb0) *
-                                                         (long long)(NTAP * 16 * CK));
-            for (int u = tid; u < W_U; u += NT) s_lds[HALO_U + u] = wsrc[u];
+            store_chunk(s_lds, rh, rw);
             __syncthreads();
+            if (chunk + 1 < p.nchunks) load_chunk(chunk + 1, rh, rw);
             compute(s_lds, s_lds + HALO_U);
         }
     } else {
-        // Halo element offsets of this thread's units (u = tid + i * NT), -1 in the padding.
-        long long hoff[HN];
-#pragma unroll
-        for (int i = 0; i < HN; ++i) {
-            const int u = tid + i * NT, pix = u >> 2, q = u & 3;
-            const int hy = pix / HX, hx = pix - hy * HX;
-            const int iy = iy0 + hy, ix = ix0 + hx;
-            hoff[i] = (u < HALO_U && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W)
-                          ? (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + q * VEC
-                          : -1;
-        }
         for (int c0 = 0; c0 < p.nchunks; c0 += SG) {
             const int ns = min(SG, p.nchunks - c0);
             u32x4 rh[SG][HN], rw[SG][WN];
 #pragma unroll
-            for (int s = 0; s < SG; ++s) {
-                if (s >= ns) break;
-                const int cl0 = (c0 + s) * CK;
-#pragma unroll
-                for (int i = 0; i < HN; ++i) {
-                    const int q = (tid + i * NT) & 3;
-                    u32x4 v = {0u, 0u, 0u, 0u};
-                    if (hoff[i] >= 0 && cl0 + q * VEC < p.cin_g) v = *(const u32x4*)(xg + hoff[i] + cl0);
-                    rh[s][i] = v;
-                }
-                const u32x4* wsrc = (const u32x4*)(wg + ((long long)(g * p.nchunks + c0 + s) * p.nblk_g + nb0) *
-                                                             (long long)(NTAP * 16 * CK));
-#pragma unroll
-                for (int i = 0; i < WN; ++i) {
-                    const int u = tid + i * NT;
-                    rw[s][i] = u < W_U ? wsrc[u] : u32x4{0u, 0u, 0u, 0u};
-                }
-            }
+            for (int s = 0; s < SG; ++s)
+                if (s < ns) load_chunk(c0 + s, rh[s], rw[s]);
             __syncthreads();
 #pragma unroll
-            for (int s = 0; s < SG; ++s) {
-                if (s >= ns) break;
-#pragma unroll
-                for (int i = 0; i < HN; ++i) {
-                    const int u = tid + i * NT;
-                    u32x4 v = rh[s][i];
-                    if (p.relu6_in) v = relu6_vec<T>(v);
-                    if (u < HALO_U) s_lds[s * STG_U + u] = v;
-                }
-#pragma unroll
-                for (int i = 0; i < WN; ++i) {
-                    const int u = tid + i * NT;
-                    if (u < W_U) s_lds[s * STG_U + HALO_U + u] = rw[s][i];
-                }
-            }
+            for (int s = 0; s < SG; ++s)
+                if (s < ns) store_chunk(s_lds + s * STG_U, rh[s], rw[s]);
             __syncthreads();
             for (int s = 0; s < ns; ++s) compute(s_lds + s * STG_U, s_lds + s * STG_U + HALO_U);
         }

@@ -104,6 +104,16 @@ __device__ __forceinline__ float cephes_exp(float x) {
     return ldexpf(y, ni);
 }
 
+// ELU(a) = a > 0 ? a : exp(a) - 1 for the 16-bit storage paths' transformer gate, with exp from
+// the hardware's 2^x (v_exp_f32 on a * log2 e; for a <= 0 the error of exp(a) - 1 stays within
+// ~1e-7 absolute, far below the f16 / bf16 rounding of the gate's result) instead of the Cephes
+// polynomial the f32 path keeps for parity with the reference (src/nn/fast/math.rs:74-80). One transcendental and a multiply against ~25 vector
+// instructions: the feed-forward's gate phase is bound by its vector ALUs.
+__device__ __forceinline__ float elu_fast16(float a) {
+    const float e = __builtin_amdgcn_exp2f(a * 1.44269504088896340736f) - 1.0f;
+    return a > 0.0f ? a : e;
+}
+
 __device__ __forceinline__ float sigmoidf_ref(float x) {
     const float e = cephes_exp(-x);
     return 1.0f / (1.0f + e);

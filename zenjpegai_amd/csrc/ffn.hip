@@ -31,6 +31,8 @@ namespace zjai {
 
 namespace {
 
+__device__ u32x4 g_zero16[1];  // 16 zero bytes: the source of absent biases
+
 constexpr int FT = 14;          // output tile side
 constexpr int FH = FT + 2;      // halo side
 constexpr int FNP = FH * FH;    // halo positions (256: sixteen 16-position MFMA blocks)
@@ -82,14 +84,23 @@ __device__ __forceinline__ void ln_halo(const T* xb, const View& xv, int y0, int
                                         float* s_stat, int tid) {
     constexpr int UPR = DIM / 8, LN_PT = FNP * UPR / FTHREADS;
     static_assert((FNP * UPR) % FTHREADS == 0, "halo shape");
+    // Every load is issued before the first is used: each reads the clamped (in-picture) pixel
+    // and positions outside the picture take zeros afterwards, so no load sits in a branch that
+    // would wait for it before the next one issues.
+    u32x4 xv8[LN_PT];
+    bool in8[LN_PT];
 #pragma unroll
     for (int i = 0; i < LN_PT; ++i) {
         const int u = tid + i * FTHREADS, pos = u / UPR, q = u % UPR;
         const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (iy >= 0 && iy < h && ix >= 0 && ix < w)
-            v = *(const u32x4*)(xb + (long long)iy * xv.row + (long long)ix * xv.cs + q * 8);
-        s_u[pos * UPR + (q ^ ukey<DIM>(pos))] = v;
+        in8[i] = iy >= 0 && iy < h && ix >= 0 && ix < w;
+        const int cy = min(max(iy, 0), h - 1), cx = min(max(ix, 0), w - 1);
+        xv8[i] = *(const u32x4*)(xb + (long long)cy * xv.row + (long long)cx * xv.cs + q * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < LN_PT; ++i) {
+        const int u = tid + i * FTHREADS, pos = u / UPR, q = u % UPR;
+        s_u[pos * UPR + (q ^ ukey<DIM>(pos))] = in8[i] ? xv8[i] : u32x4{0u, 0u, 0u, 0u};
     }
     __syncthreads();
     if (tid < FNP) {
@@ -195,19 +206,19 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
             rwo = *(const u32x4*)(w_out + off);
         }
         // Thread u < 16: b_in of local channels 4u..4u+3; 16 <= u < 160: depthwise tap
-        // (u - 16) / 16 of local channels 4 (u % 16)..; 160 <= u < 176: depthwise bias.
-        if (tid < X_U) {
-            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (tid < BIN_U) {
-                if (p.b_in) v = *(const f32x4*)(p.b_in + gch(s, 4 * tid));
-            } else if (tid < BIN_U + 144) {
-                const int u = tid - BIN_U;
-                v = *(const f32x4*)(p.dw_w + (u >> 4) * C2 + gch(s, 4 * (u & 15)));
-            } else if (p.dw_b) {
-                v = *(const f32x4*)(p.dw_b + gch(s, 4 * (tid - BIN_U - 144)));
-            }
-            rx = __builtin_bit_cast(u32x4, v);
+        // (u - 16) / 16 of local channels 4 (u % 16)..; 160 <= u < 176: depthwise bias; absent
+        // biases and threads >= 176 read zeros. One load per thread at a selected address, so
+        // nothing waits for it before its use in put_w.
+        const float* src = reinterpret_cast<const float*>(g_zero16);
+        if (tid < BIN_U) {
+            if (p.b_in) src = p.b_in + gch(s, 4 * tid);
+        } else if (tid < BIN_U + 144) {
+            const int u = tid - BIN_U;
+            src = p.dw_w + (u >> 4) * C2 + gch(s, 4 * (u & 15));
+        } else if (tid < X_U && p.dw_b) {
+            src = p.dw_b + gch(s, 4 * (tid - BIN_U - 144));
         }
+        rx = *(const u32x4*)src;
     };
     auto put_w = [&](int s) {
 #pragma unroll
@@ -346,9 +357,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
                             a = fmaf(wa[ky * 3 + kx][k], xa[ky][kx][k], a);
                             bq = fmaf(wb[ky * 3 + kx][k], xb[ky][kx][k], bq);
                         }
-                    const float e = cephes_exp(a) - 1.0f;
-                    const float elu = a > 0.0f ? a : e;
-                    g[k] = elu * bq;
+                    g[k] = elu_fast16(a) * bq;
                 }
                 typedef T t2 __attribute__((ext_vector_type(2)));
                 *reinterpret_cast<t2*>((T*)s_g + (oy * FT + dc) * 32 + 2 * pg) = t2{(T)g[0], (T)g[1]};
@@ -388,17 +397,33 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
         }
     }
     __syncthreads();
+    // 16-byte units (8 channels) of the 196 output positions: every thread issues all of its
+    // residual loads before the first add, so their latencies overlap instead of adding up.
     T* yb = (T*)p.y.p + (long long)b * p.y.bstride + p.y.c_off;
-    for (int u = tid; u < FOP * (DIM / 4); u += FTHREADS) {
-        const int pos = u / (DIM / 4), q = u % (DIM / 4);
-        const int oy = y0 + pos / FT, ox = x0 + pos % FT;
-        if (oy >= p.h || ox >= p.w) continue;
-        const float* sv = so + pos * OLD + q * 4;
-        f32x4 v = {sv[0], sv[1], sv[2], sv[3]};
-        const f32x4 r = load4<T>(xb + (long long)oy * p.x.row + (long long)ox * p.x.cs + q * 4);
+    constexpr int U8 = DIM / 8, NU = FOP * U8, EIT = (NU + FTHREADS - 1) / FTHREADS, EG = 4;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) v[k] = v[k] + r[k];
-        store4<T>(yb + (long long)oy * p.y.row + (long long)ox * p.y.cs + q * 4, v);
+    for (int i0 = 0; i0 < EIT; i0 += EG) {
+        u32x4 rres[EG];
+#pragma unroll
+        for (int j = 0; j < EG; ++j) {
+            const int u = tid + (i0 + j) * FTHREADS, pos = u / U8, q = u % U8;
+            const int oy = min(y0 + pos / FT, p.h - 1), ox = min(x0 + pos % FT, p.w - 1);
+            rres[j] = u32x4{0u, 0u, 0u, 0u};
+            if (i0 + j < EIT && u < NU)  // (clamped pixel: loads issue back to back; unused beyond the picture)
+                rres[j] = *(const u32x4*)(xb + (long long)oy * p.x.row + (long long)ox * p.x.cs + q * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < EG; ++j) {
+            const int u = tid + (i0 + j) * FTHREADS, pos = u / U8, q = u % U8;
+            const int oy = y0 + pos / FT, ox = x0 + pos % FT;
+            if (i0 + j >= EIT || u >= NU || oy >= p.h || ox >= p.w) continue;
+            const float* sv = so + pos * OLD + q * 8;
+            float r[8], v[8];
+            unpack8<T>(rres[j], r);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = sv[k] + r[k];
+            *(u32x4*)(yb + (long long)oy * p.y.row + (long long)ox * p.y.cs + q * 8) = pack8<T>(v);
+        }
     }
 }
 
@@ -443,18 +468,18 @@ __global__ void __launch_bounds__(FTHREADS) k_qkv(const QkvArgs p) {
             const long long off = ((long long)((q >> 2) * p.nblk1 + (o >> 4)) * 16 + (o & 15)) * 32 + (q & 3) * 8;
             rwi[i] = *(const u32x4*)(w1 + off);
         }
-        if (tid < X_U) {
-            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (tid < BIN_U) {
-                if (p.b1) v = *(const f32x4*)(p.b1 + 64 * s + 4 * tid);
-            } else if (tid < BIN_U + 144) {
-                const int u = tid - BIN_U;
-                v = *(const f32x4*)(p.dw_w + (u >> 4) * C3 + 64 * s + 4 * (u & 15));
-            } else if (p.dw_b) {
-                v = *(const f32x4*)(p.dw_b + 64 * s + 4 * (tid - BIN_U - 144));
-            }
-            rx = __builtin_bit_cast(u32x4, v);
+        // One load per thread at a selected address (zeros for absent biases and threads
+        // >= X_U), so nothing waits for it before its use in put.
+        const float* src = reinterpret_cast<const float*>(g_zero16);
+        if (tid < BIN_U) {
+            if (p.b1) src = p.b1 + 64 * s + 4 * tid;
+        } else if (tid < BIN_U + 144) {
+            const int u = tid - BIN_U;
+            src = p.dw_w + (u >> 4) * C3 + 64 * s + 4 * (u & 15);
+        } else if (tid < X_U && p.dw_b) {
+            src = p.dw_b + 64 * s + 4 * (tid - BIN_U - 144);
         }
+        rx = *(const u32x4*)src;
     };
     auto put = [&](int s) {
 #pragma unroll

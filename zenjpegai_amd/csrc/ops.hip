@@ -232,8 +232,13 @@ __global__ void __launch_bounds__(256) k_depthwise3x3(View src, View dst, int N,
                 for (int k = 0; k < V; ++k) {
                     const float g = __shfl_xor(acc[j][k], 32);
                     const float v = acc[j][k];
-                    const float e = cephes_exp(v) - 1.0f;
-                    const float elu = v > 0.0f ? v : e;
+                    float elu;
+                    if constexpr (sizeof(T) == 4) {
+                        const float e = cephes_exp(v) - 1.0f;
+                        elu = v > 0.0f ? v : e;
+                    } else {
+                        elu = elu_fast16(v);  // the 16-bit paths' gate, as the fused kernel's
+                    }
                     acc[j][k] = elu * g;
                 }
         }

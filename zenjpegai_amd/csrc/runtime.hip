@@ -489,6 +489,12 @@ static TileCfg launch_tile_cfg(const Layer& L, int N, int OH, int OW) {
         if (L.dtype != DT_F32 && L.nblk_g % 8 == 0 && w0 >= 512) return TileCfg{4, 2, 2, 4};
         return c;
     }
+    if (L.kind == CK_2x2 && c.wc == 2 && c.wp == 2 && c.cf == 2 && c.pf == 4) {
+        // The SOP / BOP upsampling convs (2x2 + pixel shuffle) run on the latent grid or twice
+        // it, where the default tile leaves CUs idle: 160 -> 256 at 64^2 has 128 tiles.
+        const long long w0 = (long long)((OW + 15) / 16) * ((OH + 7) / 8) * N * nt4;
+        return w0 < 256 ? TileCfg{1, 4, 1, 2} : w0 < 512 ? TileCfg{1, 4, 2, 2} : c;
+    }
     if (L.kind == CK_T3 && L.wpk_m && c.wc == 2 && c.wp == 2 && c.cf == 2 && c.pf == 4) {
         // 3x3 transposed layers whose merged grid is small (see convT_merged_fills).
         const long long wm = (long long)(((OW + 1) / 2 + 15) / 16) * (((OH + 1) / 2 + 15) / 16) * N * nt4;
