@@ -148,6 +148,13 @@ conv_igemm(const ConvParams p) {
     const T* wg = (const T*)p.w + phase * p.phase_stride + (long long)bi * p.w_bstride;
     const long long xbase = (long long)p.x.c_off + (long long)g * p.cin_g;
 
+    // LDS slot of halo pixel (hy, hx). Stride-2 halos keep each row's even columns, then its odd
+    // ones: a fragment reads every other column (hx = 2 col + kx), which then fall on consecutive
+    // 64-byte slots and spread over all banks instead of half of them.
+    constexpr int HXE = (HX + 1) / 2;
+    auto hslot = [](int hy, int hx) __attribute__((always_inline)) {
+        return S == 2 ? hy * HX + ((hx & 1) ? HXE + (hx >> 1) : (hx >> 1)) : hy * HX + hx;
+    };
     auto compute = [&](const u32x4* s_halo, const u32x4* s_w) {
         for (int t = 0; t < ntap; ++t) {
             const int ky = tdy[t], kx = tdx[t];
@@ -157,7 +164,7 @@ conv_igemm(const ConvParams p) {
 #pragma unroll
             for (int pf = 0; pf < PF; ++pf) {
                 const int hy = (wp * PF + pf) * S + ky, hx = col * S + kx;
-                b[pf] = s_halo[(hy * HX + hx) * 4 + grp];
+                b[pf] = s_halo[hslot(hy, hx) * 4 + grp];
             }
 #pragma unroll
             for (int cf = 0; cf < CF; ++cf)
@@ -169,6 +176,7 @@ conv_igemm(const ConvParams p) {
     // Halo element offsets of this thread's units (u = tid + i * NT), -1 in the padding; the
     // same for every K chunk.
     long long hoff[HN];
+    int hdst[HN];  // LDS unit each halo unit is stored to
 #pragma unroll
     for (int i = 0; i < HN; ++i) {
         const int u = tid + i * NT, pix = u >> 2, q = u & 3;
@@ -177,6 +185,7 @@ conv_igemm(const ConvParams p) {
         hoff[i] = (u < HALO_U && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W)
                       ? (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + q * VEC
                       : -1;
+        hdst[i] = hslot(hy, hx) * 4 + q;
     }
     // One K chunk's halo and weight units into registers. Every load is unconditional, from the
     // unit's address or from a zeroed buffer (padding, channels past cin_g, units past the
@@ -204,7 +213,7 @@ conv_igemm(const ConvParams p) {
             const int u = tid + i * NT;
             u32x4 v = rh[i];
             if (p.relu6_in) v = relu6_vec<T>(v);
-            if (u < HALO_U) dst[u] = v;
+            if (u < HALO_U) dst[hdst[i]] = v;
         }
 #pragma unroll
         for (int i = 0; i < WN; ++i) {

@@ -294,7 +294,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
             const int pos = (pb1 * 4 + i) * 16 + col;
             const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
             const bool inside = iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
-            const int sw = ((pos >> 1) & 1) << 2;  // a/b unit swap of odd row pairs (see dw reads)
+            const int sw = pos & 7;  // unit swizzle of the position's row (see the dw reads)
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 typedef T t4 __attribute__((ext_vector_type(4)));
@@ -324,12 +324,13 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
                     wb[tp][k] = dww[tp * 64 + 32 + 2 * pg + k];
                 }
             }
-            // 16-byte unit (pg / 4) of the first half, 4 + pg / 4 of the second, swapped on odd
-            // row pairs: the 16 lanes of a position read 64 contiguous bytes, and four
-            // consecutive positions land on disjoint bank groups.
+            // 16-byte unit (pg / 4) of the first half, 4 + pg / 4 of the second, each XORed with
+            // pos & 7: the 16 lanes of a position read four units of its row, and the phase-a stores
+            // of 16 positions spread over all banks (measured faster than a swizzle that also keeps
+            // the reads of four neighbouring positions on disjoint banks, which spills registers).
             auto ld = [&](int hr, int kx, float (&oa)[2], float (&ob)[2]) {
                 const int pos = hr * FH + dc + kx;
-                const int sw = ((pos >> 1) & 1) << 2;
+                const int sw = pos & 7;
                 const T* row = (const T*)s_p + pos * 64 + 2 * (pg & 3);
                 unpack2<T>(*(const unsigned*)(row + ((pg >> 2) ^ sw) * 8), oa);
                 unpack2<T>(*(const unsigned*)(row + ((4 + (pg >> 2)) ^ sw) * 8), ob);
@@ -546,7 +547,10 @@ __global__ void __launch_bounds__(FTHREADS) k_qkv(const QkvArgs p) {
                     t4 v;
 #pragma unroll
                     for (int k = 0; k < 4; ++k) v[k] = inside ? (T)acc1[c][i][k] : (T)0.0f;
-                    *reinterpret_cast<t4*>(sp + pos * 64 + cb1 * 32 + c * 16 + 4 * grp) = v;
+                    // 16-byte units of a position's row XORed with pos & 7: the 16 positions of
+                    // one store spread over all banks (the depthwise reads use the same map).
+                    const int ch = cb1 * 32 + c * 16 + 4 * grp;
+                    *reinterpret_cast<t4*>(sp + pos * 64 + ((ch >> 3) ^ (pos & 7)) * 8 + (ch & 7)) = v;
                 }
             }
         }
@@ -562,10 +566,11 @@ __global__ void __launch_bounds__(FTHREADS) k_qkv(const QkvArgs p) {
 #pragma unroll
                 for (int tp = 0; tp < 9; ++tp) wv[tp][k] = dww[tp * 64 + 2 * pg + k];
             }
-            const T* sp = reinterpret_cast<const T*>(s_p) + dc * 64 + 2 * pg;
+            const T* sp = reinterpret_cast<const T*>(s_p) + 2 * (pg & 3);
             float xw[3][3][2];
             auto ld = [&](int hr, int kx, float (&o)[2]) {
-                unpack2<T>(*(const unsigned*)(sp + (hr * FH + kx) * 64), o);
+                const int pos = hr * FH + dc + kx;
+                unpack2<T>(*(const unsigned*)(sp + pos * 64 + ((pg >> 2) ^ (pos & 7)) * 8), o);
             };
 #pragma unroll
             for (int kx = 0; kx < 3; ++kx) {
@@ -943,6 +948,9 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
 // taps of every slice (17 KB at dim 128) are loaded once, with the first slice's weights.
 template <int DIM>
 __global__ void __launch_bounds__(FTHREADS) k_qkv_f32(const QkvArgs p) {
+    // p rows swizzled (16-byte units XORed with pos & 15) at dim 128 only: at dim 64 the
+    // compiler then renamed MFMA accumulator chains closer than the ISA guard allows.
+    constexpr int PSWZ = DIM == 128 ? 15 : 0;
     constexpr int C3 = 3 * DIM, NS = C3 / 64, NCH = DIM / 16;
     constexpr int W1_U = NCH * 4 * 64, P_U = FNP * 16, X_U = 11 * 16;
     constexpr int W1_W = NCH * 4 / 8;
@@ -1005,8 +1013,8 @@ __global__ void __launch_bounds__(FTHREADS) k_qkv_f32(const QkvArgs p) {
                 const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
                 const bool inside = iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
 #pragma unroll
-                for (int cb = 0; cb < 4; ++cb)
-                    *(f32x4*)(s_p + pos * 64 + cb * 16 + 4 * grp) =
+                for (int cb = 0; cb < 4; ++cb)  // the row's 16 units XORed with pos & 15 (bank spread)
+                    *(f32x4*)(s_p + pos * 64 + (((cb * 4 + grp) ^ (pos & PSWZ)) << 2)) =
                         inside ? acc1[cb][i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
         }
@@ -1021,10 +1029,10 @@ __global__ void __launch_bounds__(FTHREADS) k_qkv_f32(const QkvArgs p) {
 #pragma unroll
                 for (int tp = 0; tp < 9; ++tp) wv[tp][k] = dww[tp * 64 + 2 * pg + k];
             }
-            const float* sp = s_p + dc * 64 + 2 * pg;
             float xw[3][3][2];
             auto ld = [&](int hr, int kx, float (&o)[2]) {
-                const f32x2 v = *(const f32x2*)(sp + (hr * FH + kx) * 64);
+                const int pos = hr * FH + dc + kx;
+                const f32x2 v = *(const f32x2*)(s_p + pos * 64 + ((((pg >> 1) ^ (pos & PSWZ)) << 2) + 2 * (pg & 1)));
                 o[0] = v[0];
                 o[1] = v[1];
             };
