@@ -79,8 +79,9 @@ typedef struct zjai_picture zjai_picture;
  * ZJAI_CTX_COUNT_F16_RANGE (other bits are rejected). */
 /* Run the transformer blocks (src/model/attention.rs:328-372) as the reference's separate ops --
  * layer norm, 1x1, depthwise (+ ELU gate), 1x1 -- instead of the fused kernels every precision
- * uses by default for `prep_data` (LN + 1x1 + depthwise) and for the feed-forward half (the two
- * give bit-identical results). */
+ * uses by default for `prep_data` (LN + 1x1 + depthwise) and for the feed-forward half, and the
+ * 32- / 64-channel ResAUs (src/model/synthesis.rs:24-74) as their grouped 3x3 and gated 1x1
+ * instead of one fused kernel (each pair gives bit-identical results). */
 #define ZJAI_CTX_UNFUSED_BLOCKS 0x1u
 /* Run every 3x3 stride-2 transposed convolution (`conv3x3_t`, src/model/attention.rs:78-91) one
  * output phase per workgroup. By default a layer whose four-phase grid fills the chip (>= 256

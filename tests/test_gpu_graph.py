@@ -132,6 +132,44 @@ def test_fused_transformer_blocks_are_bit_identical_to_unfused(prec, comp):
     plain.close()
 
 
+# (op, component, fused ResAUs): the 32- and 64-channel ResAUs (16 channels per group) run as one
+# kernel; BOP's 96 / 128-channel and HOP luma's 128-channel ones stay two launches.
+RESAU_NETS = [("sop", "y", 3), ("sop", "uv", 2), ("bop", "y", 2), ("bop", "uv", 1), ("hop", "uv", 2)]
+
+
+@pytest.mark.parametrize("prec", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("op,comp,n_fused", RESAU_NETS)
+def test_fused_resau_is_bit_identical_to_unfused(prec, op, comp, n_fused):
+    """The fused ResAU kernel (relu6 halo, grouped 3x3, 1x1 and gate in one launch) against the
+    same net with the grouped 3x3 and the gated 1x1 as separate kernels (ZJAI_CTX_UNFUSED_BLOCKS).
+    Latent 7 x 5: every map has partial tiles at the right and bottom (and, for the small maps,
+    4-row tiles in 16-bit)."""
+    fused = nn.Engine(0, prec)
+    plain = nn.Engine(0, prec, flags=_lib.CTX_UNFUSED_BLOCKS)
+    p = synth.random_params(op, comp, seed=31, gain=0.5)
+    lh, lw = 7, 5
+    outs, names = [], []
+    for eng in (fused, plain):
+        eng.profile_begin()
+        y = synth.latent(31, "resau/y", 160, lh, lw)
+        if comp == "y":
+            net = model.SynthesisPrimary.load(p, op, eng)
+            out = net.forward(eng, nn.BTensor.from_planar(eng, y), 16 * lh, 16 * lw)
+        else:
+            uv = synth.latent(31, "resau/uv", 96, lh, lw)
+            net = model.SynthesisSecondary.load(p, op, eng)
+            out = net.forward(eng, nn.BTensor.from_planar(eng, y), nn.BTensor.from_planar(eng, uv),
+                              16 * lh, 16 * lw)
+        names.append([r[0] for r in eng.profile_end()])
+        outs.append(out)
+    assert sum(n.startswith("k_resau<") for n in names[0]) == n_fused, names[0]
+    assert not any(n.startswith("k_resau<") for n in names[1])
+    assert np.isfinite(outs[0]).all()
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    fused.close()
+    plain.close()
+
+
 @pytest.mark.parametrize("prec", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("comp", ["y", "uv"])
 def test_merged_phase_transposed_convs_are_bit_identical_to_phase_split(prec, comp):

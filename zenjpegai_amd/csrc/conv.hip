@@ -28,42 +28,6 @@ namespace zjai {
 // The 16x16 fragment of mfma.h (Mma16): 4 x 16x16x4 f32 steps or one 16x16x32 16-bit step.
 template <typename T> using Mma = Mma16<T>;
 
-// clamp(v, 0, 6) on a 16-byte vector of the storage type (ResAU's relu6 on load).
-template <typename T> __device__ __forceinline__ u32x4 relu6_vec(u32x4 v);
-template <> __device__ __forceinline__ u32x4 relu6_vec<float>(u32x4 v) {
-    f32x4 f = __builtin_bit_cast(f32x4, v);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float e = f[i];
-        e = e < 0.0f ? 0.0f : e;
-        e = e > 6.0f ? 6.0f : e;
-        f[i] = e;
-    }
-    return __builtin_bit_cast(u32x4, f);
-}
-template <> __device__ __forceinline__ u32x4 relu6_vec<_Float16>(u32x4 v) {
-    f16x8 h = __builtin_bit_cast(f16x8, v);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        _Float16 e = h[i];
-        e = e < (_Float16)0.0f ? (_Float16)0.0f : e;
-        e = e > (_Float16)6.0f ? (_Float16)6.0f : e;
-        h[i] = e;
-    }
-    return __builtin_bit_cast(u32x4, h);
-}
-template <> __device__ __forceinline__ u32x4 relu6_vec<__bf16>(u32x4 v) {
-    bf16x8 h = __builtin_bit_cast(bf16x8, v);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        float e = (float)h[i];
-        e = e < 0.0f ? 0.0f : e;
-        e = e > 6.0f ? 6.0f : e;
-        h[i] = (__bf16)e;
-    }
-    return __builtin_bit_cast(u32x4, h);
-}
-
 // SG: input-channel chunks staged per barrier. 1x1 layers do little matrix work per chunk, so
 // they stage several (SG = 4: the whole K of a 128-channel f16 layer) with every global load of
 // the stage issued before its LDS stores -- more bytes in flight per workgroup, fewer barriers.

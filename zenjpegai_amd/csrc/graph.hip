@@ -308,7 +308,49 @@ struct Fwd {
         return conv_forward(ctx, L(name), x, e, dst, plane);
     }
     // ResAu::forward (src/model/synthesis.rs:62-74); the gate overwrites x.
+    // The fused ResAU kernel applies to 32- / 64-channel ResAUs with 16-channel groups whose
+    // layers are packed as one K chunk and one 16-row block per group (the 3x3) and 16-row blocks
+    // (the 1x1), on a 16-byte-aligned input view.
+    bool res_au_fusable(const std::string& pfx, const TensorP& x) {
+        if (ctx.top().flags & ZJAI_CTX_UNFUSED_BLOCKS) return false;
+        const Layer& c1 = L(pfx + ".conv");
+        const Layer& c2 = L(pfx + ".conv2");
+        const int C = x->c;
+        if (!resau_fused_supported(C, c1.groups) || c1.kind != CK_3x3 || c1.cin != C || c1.cout != C ||
+            c1.depthwise || c1.nchunks != 1 || c1.nblk_g != 1 || c1.dtype != x->dtype || c1.extra[0] ||
+            c1.extra[1] || c1.extra[2] || c1.extra[3] || c1.pad_h != 1 || c1.pad_w != 1)
+            return false;
+        if (c2.kind != CK_1x1 || c2.groups != 1 || c2.cin != C || c2.cout != C || c2.nblk_g * 16 != C ||
+            c2.dtype != x->dtype || c2.bias)
+            return false;
+        const View& v = x->v;
+        return v.cs % 8 == 0 && v.c_off % 8 == 0 && v.row % 8 == 0 && v.bstride % 8 == 0;
+    }
     TensorP res_au(const std::string& pfx, const TensorP& x) {
+        if (res_au_fusable(pfx, x)) {
+            const Layer& c1 = L(pfx + ".conv");
+            const Layer& c2 = L(pfx + ".conv2");
+            TensorP y = ctx.alloc(x->n, x->c, x->h, x->w, x->dtype);
+            ResauArgs a{};
+            a.x = x->v;
+            a.y = y->v;
+            a.N = x->n;
+            a.h = x->h;
+            a.w = x->w;
+            a.w1 = c1.wpk;
+            a.w2 = c2.wpk;
+            a.nblk2 = c2.nblk_g;
+            const double npos = (double)x->n * x->h * x->w, C = x->c;
+            {
+                char name[48];
+                static const char* ty[] = {"float", "_Float16", "__bf16"};
+                snprintf(name, sizeof name, "k_resau<%s, %d, %d>", ty[x->dtype], x->c, resau_rows(x->dtype, x->n, x->h, x->w));
+                LaunchScope sc(ctx, name, 2.0 * npos * (C * 16 * 9 + C * C), 2.0 * dtype_size(x->dtype) * npos * C);
+                ZJAI_HIP(launch_resau(x->dtype, x->c, a, ctx.stream));
+            }
+            count_f16_range(ctx, *y);
+            return y;
+        }
         Epilogue e1;
         e1.relu6_in = 1;
         TensorP t = conv(pfx + ".conv", x, e1);

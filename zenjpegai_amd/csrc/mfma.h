@@ -53,4 +53,40 @@ template <> struct Mma32<__bf16> {
     }
 };
 
+// clamp(v, 0, 6) on a 16-byte vector of the storage type (ResAU's relu6 on load).
+template <typename T> __device__ __forceinline__ u32x4 relu6_vec(u32x4 v);
+template <> __device__ __forceinline__ u32x4 relu6_vec<float>(u32x4 v) {
+    f32x4 f = __builtin_bit_cast(f32x4, v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float e = f[i];
+        e = e < 0.0f ? 0.0f : e;
+        e = e > 6.0f ? 6.0f : e;
+        f[i] = e;
+    }
+    return __builtin_bit_cast(u32x4, f);
+}
+template <> __device__ __forceinline__ u32x4 relu6_vec<_Float16>(u32x4 v) {
+    f16x8 h = __builtin_bit_cast(f16x8, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        _Float16 e = h[i];
+        e = e < (_Float16)0.0f ? (_Float16)0.0f : e;
+        e = e > (_Float16)6.0f ? (_Float16)6.0f : e;
+        h[i] = e;
+    }
+    return __builtin_bit_cast(u32x4, h);
+}
+template <> __device__ __forceinline__ u32x4 relu6_vec<__bf16>(u32x4 v) {
+    bf16x8 h = __builtin_bit_cast(bf16x8, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float e = (float)h[i];
+        e = e < 0.0f ? 0.0f : e;
+        e = e > 6.0f ? 6.0f : e;
+        h[i] = (__bf16)e;
+    }
+    return __builtin_bit_cast(u32x4, h);
+}
+
 }  // namespace zjai

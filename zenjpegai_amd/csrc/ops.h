@@ -67,6 +67,20 @@ struct FfnArgs {
     const float* b_out;
 };
 bool ffn_fused_supported(int dtype, int dim);
+// ResAU (x * (1 + conv1x1(conv3x3_grouped(relu6(x))))) in one kernel for C = 32 or 64 channels in
+// groups of 16, every storage type; w1 / w2 are the two layers' implicit-GEMM packings (one K
+// chunk and one 16-row block per group for w1; nblk2 16-row blocks for w2). y must not alias x.
+struct ResauArgs {
+    View x, y;
+    int N, h, w;
+    int gx, gy;  // tile grid (set by the launcher)
+    const void* w1;
+    const void* w2;
+    int nblk2;
+};
+bool resau_fused_supported(int C, int groups);
+int resau_rows(int dtype, int N, int h, int w);
+hipError_t launch_resau(int dtype, int C, const ResauArgs& p, hipStream_t s);
 // The attention branch's qkv = depthwise3x3(conv1x1(LN(x))) (dim -> 3 dim) in one kernel
 // (every storage type, dim 64 or 128); weights as FfnArgs. y must not alias x.
 struct QkvArgs {
