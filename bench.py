@@ -4,14 +4,19 @@ Workload (``config.workload``): BASELINE config 5 -- HOP luma + chroma synthesis
 4:2:0 picture, 10-bit output, tiled as the reference's encoder signals it for independent
 regions (2x3 regions, tile 640, overlap 128: 24 tiles), He-normal random-init weights, latents
 round(Laplace(0, 1.5)) at /16 resolution. One step = one whole-picture synthesis with the
-latents already resident in HBM (``Picture.run``: every tile on one HIP stream, 10-bit planes
-written by the last layers' epilogues).
+latents already resident in HBM (``Picture.run``: the tiles in same-shape batches of up to 6 over
+``--lanes`` concurrent HIP streams, 4 by default; 10-bit planes written by the last layers'
+epilogues).
 
-``value`` is the fp32-MFMA parity path (the reference computes in f32). Extra lines in ``extra``:
-the host-to-host rate of the same picture (latent upload, synthesis, download of the 10-bit
-planes; ``host_to_host``), the device time of the last timed step, the same picture on the f16 /
-bf16 paths with the PSNR of their 10-bit planes against the f32 path's, BASELINE config 4 (SOP
-luma 1024x1024, 8-bit), a 4 MP HOP picture (2048x2048, 1 MP header tiles) and BASELINE configs 1-3
+``value`` is the fp32-MFMA parity path (the reference computes in f32). ``one_stream``: the same
+picture with every launch on one HIP stream. Extra lines in ``extra``: the host-to-host rate of
+the same picture (latent upload, synthesis, download of the 10-bit planes; ``host_to_host``), the
+device time of the last timed step, the same picture on the f16 / bf16 paths (timed on He x 0.5
+weights, whose activations stay inside f16's range) with the PSNR of their 10-bit planes against
+the f32 path's at gains 1 and 0.5, the number of f16 activations stored as non-finite at both
+gains (``ZJAI_CTX_COUNT_F16_RANGE``), the reference's f16-weight semantics (weights rounded to
+f16, f32 activations: time and PSNR at both gains), BASELINE config 4 (SOP luma 1024x1024,
+8-bit; f32 and bf16), a 4 MP HOP picture (2048x2048, 1 MP header tiles) and BASELINE configs 1-3
 as single layers (kernel time and TFLOP/s, f32 and bf16).
 
 ``roofline``: one profiled step (HIP events around every launch, all on one stream); the

@@ -75,8 +75,8 @@ typedef struct zjai_picture zjai_picture;
 
 /* Replaces `Engine` construction (src/nn/fast/mod.rs:128-172) for the HIP backend: binds a
  * device and creates its stream. flags: 0 or an OR of ZJAI_CTX_UNFUSED_BLOCKS,
- * ZJAI_CTX_PHASE_SPLIT_CONVT, ZJAI_CTX_MFMA16_CONV3X3, ZJAI_CTX_IGEMM_CONV1X1 and
- * ZJAI_CTX_COUNT_F16_RANGE (other bits are rejected). */
+ * ZJAI_CTX_PHASE_SPLIT_CONVT, ZJAI_CTX_MFMA16_CONV3X3, ZJAI_CTX_IGEMM_CONV1X1,
+ * ZJAI_CTX_COUNT_F16_RANGE and ZJAI_CTX_VALU_NARROW_CONVT (other bits are rejected). */
 /* Run the transformer blocks (src/model/attention.rs:328-372) as the reference's separate ops --
  * layer norm, 1x1, depthwise (+ ELU gate), 1x1 -- instead of the fused kernels every precision
  * uses by default for `prep_data` (LN + 1x1 + depthwise) and for the feed-forward half, and the
@@ -101,6 +101,13 @@ typedef struct zjai_picture zjai_picture;
  * weights only, src/weights/f16.rs:70-72, with f32 activations); it tells whether a 16-bit run of
  * a net stayed inside f16's range. Off by default: one extra pass over every f16 tensor. */
 #define ZJAI_CTX_COUNT_F16_RANGE 0x10u
+/* Run the f16 / bf16 3x3 stride-2 transposed convolutions with at most 8 outputs (the last
+ * synthesis layers) on the vector ALUs in the reference's (input channel, tap) FMA order
+ * instead of the matrix cores. The MFMA form sums the same exact products in another order, so
+ * the two differ by the summation order before the final rounding to the storage type; the fp32
+ * path always uses the vector form (bit-exact against the oracle). For A/B runs and the tests
+ * that compare the two. */
+#define ZJAI_CTX_VALU_NARROW_CONVT 0x20u
 ZJAI_API int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** out);
 ZJAI_API int32_t zjai_ctx_destroy(zjai_ctx* ctx);
 /* Copies the last failure message (NUL-terminated, truncated to len). Works with ctx == NULL

@@ -484,11 +484,12 @@ def _round_storage(a, prec):
 @pytest.mark.parametrize("prec", ["f16", "bf16"])
 @pytest.mark.parametrize("cout,op", [(1, 1), (2, 0)])
 def test_narrow_conv_transpose_3x3_16bit_is_exact(engines, prec, cout, op):
-    """The 3x3 narrow transposed conv (k_convT3_narrow) in a 16-bit precision computes in f32 on
-    the stored (rounded) inputs and weights in the reference's FMA order, so its output is the
-    oracle's f32 result on those rounded operands, rounded once to the storage type -- bit for
-    bit. 128 input channels (two 128-byte chunks in 16-bit), a map not a multiple of the tile."""
-    eng = engines[prec]
+    """The 3x3 narrow transposed conv on the vector ALUs (k_convT3_narrow, selected by
+    ZJAI_CTX_VALU_NARROW_CONVT in the 16-bit precisions) computes in f32 on the stored (rounded)
+    inputs and weights in the reference's FMA order, so its output is the oracle's f32 result on
+    those rounded operands, rounded once to the storage type -- bit for bit. 128 input channels
+    (two 128-byte chunks in 16-bit), a map not a multiple of the tile."""
+    eng = nn.Engine(0, prec, flags=_lib.CTX_VALU_NARROW_CONVT)
     x = synth.normal(11, "t3/x", (128, 19, 45), 1.0)
     w = synth.normal(11, f"t3/w{cout}", (128, cout, 3, 3), 0.1)
     b = synth.normal(11, f"t3/b{cout}", (cout,), 0.1)
@@ -497,10 +498,45 @@ def test_narrow_conv_transpose_3x3_16bit_is_exact(engines, prec, cout, op):
     eng.profile_begin()
     y = layer.forward(eng, nn.BTensor.from_planar(eng, x)).to_planar()
     names = [r[0] for r in eng.profile_end()]
+    eng.close()
     assert any(n.startswith("k_convT3_narrow") for n in names), names
     want = _round_storage(oracle.conv_transpose2d(_round_storage(x, prec), _round_storage(w, prec), b, 2, 1, op),
                           prec)
     assert np.array_equal(y, want)
+
+
+# (cin, cout, output padding, input h x w): HOP luma's last layer (128 -> 1), HOP chroma's
+# (64 -> 8), and 2 / 4 outputs (one 16-row block of (phase, output) rows, partly or fully used).
+MFMA_NARROW_CASES = [(128, 1, 1, 19, 45), (64, 8, 1, 23, 37), (128, 2, 0, 17, 33), (64, 4, 1, 9, 70)]
+
+
+@pytest.mark.parametrize("prec", ["f16", "bf16"])
+@pytest.mark.parametrize("cin,cout,op,h,w", MFMA_NARROW_CASES)
+def test_narrow_conv_transpose_3x3_16bit_mfma(engines, prec, cin, cout, op, h, w):
+    """The default 16-bit form of the same layers (k_convT3_mfma: one GEMM per phase-grid position
+    over the 2 x 2 input neighbourhood, 16x16x32 MFMAs) sums the same exact f32 products as the
+    vector kernel in another order: against the oracle's f32 result on the rounded operands,
+    rounded to the storage type, it is within two storage ulps of the largest output everywhere
+    (f16 2 x 2^-11, bf16 2 x 2^-8 of max|oracle|) and equal in most samples; relu6 on load too."""
+    eng = engines[prec]
+    x = synth.normal(16, f"tm16/x{cin}", (cin, h, w), 1.0)
+    wt = synth.normal(16, f"tm16/w{cin}{cout}", (cin, cout, 3, 3), 0.1)
+    b = synth.normal(16, f"tm16/b{cout}", (cout,), 0.1)
+    layer = nn.ConvTransposeLayer(nn.ConvTranspose2d(cin, cout, 3, 2, 1, op, wt, b), eng)
+    xr, wr = _round_storage(x, prec), _round_storage(wt, prec)
+    bound = 2.0 * (2.0 ** -11 if prec == "f16" else 2.0 ** -8)
+    for relu6 in (False, True):
+        eng.sync()
+        eng.profile_begin()
+        y = layer.forward_fused(eng, nn.BTensor.from_planar(eng, x), relu6_input=relu6).to_planar()
+        names = [r[0] for r in eng.profile_end()]
+        assert any(n.startswith("k_convT3_mfma") for n in names), names
+        want = _round_storage(oracle.conv_transpose2d(oracle.relu6(xr) if relu6 else xr, wr, b, 2, 1, op), prec)
+        assert y.shape == want.shape
+        err = rel_err(y, want)
+        same = float(np.mean(y == want))
+        print(f"{prec} {cin}->{cout} op {op} relu6 {relu6}: rel err {err:.2e}, equal {same:.4f}")
+        assert err <= bound and same >= 0.9, (err, same)
 
 
 @pytest.mark.parametrize("prec", ["f16", "bf16"])

@@ -38,6 +38,7 @@ CTX_PHASE_SPLIT_CONVT = 0x2
 CTX_MFMA16_CONV3X3 = 0x4
 CTX_IGEMM_CONV1X1 = 0x8
 CTX_COUNT_F16_RANGE = 0x10
+CTX_VALU_NARROW_CONVT = 0x20
 FAIL_NONE, FAIL_ALLOC, FAIL_LAUNCH = 0, 1, 2  # zjai_inject_failure kinds
 RESIZE_BICUBIC, RESIZE_BILINEAR = 0, 1
 PLANE_LATENT, PLANE_PSI, PLANE_HYPER_LATENT, PLANE_IMAGE = 0, 1, 2, 3

@@ -112,7 +112,7 @@ extern "C" int32_t zjai_ctx_create(int32_t device, uint32_t flags, zjai_ctx** ou
     if (!out) return ZJAI_E_INVALID_ARGUMENT;
     *out = nullptr;
     if (flags & ~(ZJAI_CTX_UNFUSED_BLOCKS | ZJAI_CTX_PHASE_SPLIT_CONVT | ZJAI_CTX_MFMA16_CONV3X3 |
-                  ZJAI_CTX_IGEMM_CONV1X1 | ZJAI_CTX_COUNT_F16_RANGE))
+                  ZJAI_CTX_IGEMM_CONV1X1 | ZJAI_CTX_COUNT_F16_RANGE | ZJAI_CTX_VALU_NARROW_CONVT))
         return guard(nullptr, [] { throw Error(ZJAI_E_INVALID_ARGUMENT, "zjai_ctx_create: unknown flags"); });
     zjai_ctx* ctx = new (std::nothrow) zjai_ctx();
     if (!ctx) return ZJAI_E_LIMIT;

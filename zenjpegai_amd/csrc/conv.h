@@ -100,5 +100,10 @@ int conv1x1_ring_nb(const ConvParams& p);
 bool convT_narrow_k3(int dtype, const ConvParams& p, int cin);
 hipError_t launch_convT_narrow(int dtype, int coutp, const ConvParams& p, const float* wn, int cin,
                                hipStream_t s);
+// The same layers in f16 / bf16 on 16x16x32 MFMAs when their taps are the 3x3 / padding-1 ones
+// and cin is 64 or 128 (convT_mfma_k3); wm is [cin / 32][neighbour][row block][16][32] in the
+// storage type (row = phase * coutp + output, zero where a phase does not read the neighbour).
+bool convT_mfma_k3(int dtype, const ConvParams& p, int cin);
+hipError_t launch_convT3_mfma(int dtype, int coutp, const ConvParams& p, const void* wm, int cin, hipStream_t s);
 
 }  // namespace zjai

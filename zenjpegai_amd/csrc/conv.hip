@@ -1020,6 +1020,121 @@ k_convT3_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// 16-bit 3x3 stride-2 transposed convs with at most 8 outputs and 64 or 128 input channels (the
+// last synthesis layers: HOP luma 128 -> 1, HOP chroma 64 -> 8) on the matrix cores. Output phase
+// (py, px) of phase-grid position (y', x') reads only the 2 x 2 input neighbourhood
+// (y' + a, x' + b), so the layer is one GEMM per position: K = 4 neighbours x CIN, M = 4 phases x
+// COUTP rows (row R = phase * COUTP + output; a phase's weight for a neighbour it does not read
+// is zero), N = positions. 16x16x32 MFMAs with the weights as A (MB 16-row blocks, packed
+// [CIN / 32][4][MB][16][32], held in registers) and the halo as B. A workgroup (4 waves) takes
+// 8 x 32 positions and stages its whole 9 x 33-pixel input halo, every channel, in one round
+// trip (direct LDS loads of whole 128- or 256-byte pixels, 16-byte slots XORed by pixel so that a
+// fragment's 16 pixels spread over the banks): the layer is one HBM read of its input, and its
+// 9 FMAs per input channel and output on the vector ALUs become one fragment read per 32
+// channels. Products of 16-bit operands are exact in f32, so the result differs from the vector
+// kernel's (input channel, tap) FMA chain by the summation order only, before the final rounding
+// to the storage type.
+template <typename T, int COUTP, int CIN>
+__global__ void __launch_bounds__(256)
+k_convT3_mfma(const ConvParams p, const u32x4* __restrict__ wm) {
+    constexpr int MB = (4 * COUTP + 15) / 16;  // 16-row blocks of (phase, output) rows
+    constexpr int TY = 8, TX = 32, HX = TX + 1, HY = TY + 1, HPIX = HX * HY;
+    constexpr int SL = CIN / 8;                // 16-byte slots per pixel
+    constexpr int HALO_U = HPIX * SL;
+    constexpr int HN = (HALO_U + 255) / 256;
+    constexpr int KC = CIN / 32;               // 32-channel K steps per neighbour
+    constexpr int WF = KC * 4 * MB;            // weight fragments
+    static_assert(sizeof(T) == 2 && (CIN == 64 || CIN == 128), "16-bit, 64 or 128 input channels");
+    __shared__ u32x4 s_halo[HALO_U];
+    // Slot swizzle: consecutive pixels' same slot lands in different banks.
+    auto swz = [](int pix) { return SL == 16 ? (pix & 15) : ((pix >> 1) & 7); };
+    const int gw = (p.OW + 1) / 2, gh = (p.OH + 1) / 2;
+    const int gx = (gw + TX - 1) / TX, gy = (gh + TY - 1) / TY;
+    int bid = (int)((blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8);
+    if (bid >= gx * gy * p.N) return;
+    const int tx = bid % gx;
+    bid /= gx;
+    const int ty = bid % gy, bi = bid / gy;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int y0 = ty * TY, x0 = tx * TX;
+    const T* xg = (const T*)p.x.p + (long long)bi * p.x.bstride + p.x.c_off;
+
+    // The whole halo: unit U = pixel * SL + slot holds the pixel's 16-byte unit slot ^ swz(pixel).
+#pragma unroll
+    for (int i = 0; i < HN; ++i) {
+        const int ub = wave * 64 + i * 256;
+        if (ub >= HALO_U) break;
+        const int U = ub + lane, pix = U / SL, slot = U % SL;
+        const int hy = pix / HX, hx = pix - hy * HX;
+        const int iy = y0 + hy, ix = x0 + hx;
+        const void* src = (U < HALO_U && iy < p.H && ix < p.W)
+                              ? (const void*)(xg + (long long)iy * p.x.row + (long long)ix * p.x.cs + (slot ^ swz(pix)) * 8)
+                              : (const void*)g_zero_unitsT;
+        if (U < HALO_U) __builtin_amdgcn_global_load_lds(src, (lds_addr_t_t)(s_halo + ub), 16, 0, 0);
+    }
+    u32x4 wa[WF];
+#pragma unroll
+    for (int f = 0; f < WF; ++f) wa[f] = wm[((long long)f * 16 + col) * 4 + grp];
+
+    // Wave w: position blocks j = 0..3 = tile row 2 w + j / 2, columns 16 (j % 2) .. + 15.
+    f32x4 acc[MB][4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        f32x4 bv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int R = 16 * mb + 4 * grp + r, ph = R / COUTP, oc = R % COUTP;
+            bv[r] = (ph < 4 && p.bias && oc < p.cout_g) ? p.bias[oc] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[mb][j] = bv;
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's halo loads are in LDS
+    __syncthreads();                     // ... and every other wave's
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            const int a = n >> 1, b = n & 1, slot = kc * 4 + grp;
+            u32x4 bv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int pix = (2 * wave + (j >> 1) + a) * HX + 16 * (j & 1) + col + b;
+                bv[j] = s_halo[pix * SL + (slot ^ swz(pix))];
+                if (p.relu6_in) bv[j] = relu6_vec<T>(bv[j]);
+            }
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) Mma16<T>::run(acc[mb][j], wa[(kc * 4 + n) * MB + mb], bv[j]);
+        }
+
+    // Row R = 16 mb + 4 grp + r of column col: phase R / COUTP, output R % COUTP.
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int yq = y0 + 2 * wave + (j >> 1), xq = x0 + 16 * (j & 1) + col;
+            if constexpr (COUTP >= 4) {
+                // The lane's four rows are four consecutive outputs of one phase.
+                const int R0 = 16 * mb + 4 * grp, ph = R0 / COUTP, oc0 = R0 % COUTP;
+                const int oy = 2 * yq + (ph >> 1), ox = 2 * xq + (ph & 1);
+                if (ph < 4 && oc0 < p.cout_g && oy < p.OH && ox < p.OW)
+                    epilogue_store<T>(p, bi, oy, ox, oc0, min(4, p.cout_g - oc0), acc[mb][j]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int R = 16 * mb + 4 * grp + r, ph = R / COUTP, oc = R % COUTP;
+                    const int oy = 2 * yq + (ph >> 1), ox = 2 * xq + (ph & 1);
+                    if (ph < 4 && oc < p.cout_g && oy < p.OH && ox < p.OW)
+                        epilogue_store<T>(p, bi, oy, ox, oc, 1, f32x4{acc[mb][j][r], 0.0f, 0.0f, 0.0f});
+                }
+            }
+        }
+}
+
 // Whether a layer's tap tables are the 3x3 / padding 1 ones k_convT3_narrow hard-codes
 // (halo offsets 1 = input row y', 2 = y' + 1).
 static bool taps_are_k3p1(const ConvParams& p) {
@@ -1054,6 +1169,42 @@ bool convT_narrow_k3(int dtype, const ConvParams& p, int cin) {
     const int vec = dtype == DT_F32 ? 4 : 8;
     return p.cout_g <= 2 && taps_are_k3p1(p) && cin % (8 * vec) == 0 && p.x.cs % vec == 0 &&
            p.x.c_off % vec == 0 && p.x.row % vec == 0 && p.x.bstride % vec == 0;
+}
+
+bool convT_mfma_k3(int dtype, const ConvParams& p, int cin) {
+    return dtype != DT_F32 && taps_are_k3p1(p) && (cin == 64 || cin == 128) && p.x.cs % 8 == 0 &&
+           p.x.c_off % 8 == 0 && p.x.row % 8 == 0 && p.x.bstride % 8 == 0;
+}
+
+template <typename T, int CIN>
+static hipError_t go_mfma3(int coutp, const ConvParams& p, const void* wm, hipStream_t s) {
+    const int gw = (p.OW + 1) / 2, gh = (p.OH + 1) / 2;
+    const long long blocks = ((long long)((gw + 31) / 32) * ((gh + 7) / 8) * p.N + 7) / 8 * 8;
+    if (blocks <= 0 || blocks > (1ll << 30) || p.N < 1 || p.N > MAXB) return hipErrorInvalidValue;
+    const dim3 g((unsigned)blocks);
+    const u32x4* w = (const u32x4*)wm;
+    switch (coutp) {
+        case 1: hipLaunchKernelGGL((k_convT3_mfma<T, 1, CIN>), g, dim3(256), 0, s, p, w); break;
+        case 2: hipLaunchKernelGGL((k_convT3_mfma<T, 2, CIN>), g, dim3(256), 0, s, p, w); break;
+        case 4: hipLaunchKernelGGL((k_convT3_mfma<T, 4, CIN>), g, dim3(256), 0, s, p, w); break;
+        case 8: hipLaunchKernelGGL((k_convT3_mfma<T, 8, CIN>), g, dim3(256), 0, s, p, w); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t go_mfma3_c(int coutp, const ConvParams& p, const void* wm, int cin, hipStream_t s) {
+    return cin == 128 ? go_mfma3<T, 128>(coutp, p, wm, s) : go_mfma3<T, 64>(coutp, p, wm, s);
+}
+
+hipError_t launch_convT3_mfma(int dtype, int coutp, const ConvParams& p, const void* wm, int cin, hipStream_t s) {
+    if (!convT_mfma_k3(dtype, p, cin)) return hipErrorInvalidValue;
+    switch (dtype) {
+        case DT_F16: return go_mfma3_c<_Float16>(coutp, p, wm, cin, s);
+        case DT_BF16: return go_mfma3_c<__bf16>(coutp, p, wm, cin, s);
+    }
+    return hipErrorInvalidValue;
 }
 
 template <typename T>

@@ -174,12 +174,14 @@ struct Layer {
     float* bias = nullptr;     // f32 [cout] or null
     float* dw_w = nullptr;     // depthwise [9][C]
     float* w_f32 = nullptr;    // f32 [cout][cin] copy (1x1 only, for attention folding)
-    float* wn = nullptr;       // narrow transposed conv: [phase][tap][cin][coutp] f32
+    float* wn = nullptr;       // narrow transposed conv: [cin][phase][tap][coutp] f32
     void* wpk_m = nullptr;     // 3x3 transposed conv, all phases per workgroup: [chunk][nblk][9][16][CK]
     size_t wpk_m_bytes = 0;
     void* wpk32 = nullptr;     // dense stride-1 3x3, 16-bit: [cin / 16][cout / mt32][9][mt32][16]
     int mt32 = 0;              // output channels per workgroup of conv3x3_m32 (0: not eligible)
     int coutp = 0;             // cout rounded up to 1, 2, 4 or 8 (narrow transposed conv)
+    void* wm16 = nullptr;      // narrow 3x3 transposed conv, 16-bit MFMA: [cin / 32][4][row block][16][32]
+    size_t wm16_bytes = 0;
     size_t wpk_bytes = 0;
     ~Layer();
 

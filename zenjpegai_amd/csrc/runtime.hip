@@ -262,6 +262,7 @@ Layer::~Layer() {
     if (dw_w) (void)hipFree(dw_w);
     if (w_f32) (void)hipFree(w_f32);
     if (wn) (void)hipFree(wn);
+    if (wm16) (void)hipFree(wm16);
     if (wpk_m) (void)hipFree(wpk_m);
     if (wpk32) (void)hipFree(wpk32);
 }
@@ -459,6 +460,29 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
                 }
         }
         L->wn = upload_f32(wn.data(), wn.size());
+        if (dtype != DT_F32 && k == 3 && (cin == 64 || cin == 128)) {
+            // The MFMA form (launch_convT3_mfma): row R = phase * coutp + output of 16-row block
+            // R / 16, K = (neighbour, input channel); tap t of phase ph reads input pixel
+            // (y' + tap_dy - 1, x' + tap_dx - 1), i.e. neighbour 2 (tap_dy - 1) + (tap_dx - 1)
+            // when both offsets are 1 or 2 (the 3x3 / padding-1 tables).
+            const int mbn = (4 * L->coutp + 15) / 16;
+            std::vector<float> wm((size_t)(cin / 32) * 4 * mbn * 16 * 32, 0.0f);
+            bool ok = true;
+            for (int ph = 0; ph < 4; ++ph)
+                for (int t = 0; t < L->ntaps[ph]; ++t) {
+                    const int dy = L->tap_dy[ph][t], dx = L->tap_dx[ph][t];
+                    if (dy < 1 || dy > 2 || dx < 1 || dx > 2) ok = false;
+                    if (!ok) continue;
+                    const int n = 2 * (dy - 1) + (dx - 1);
+                    for (int oc = 0; oc < cout; ++oc) {
+                        const int R = ph * L->coutp + oc, mb = R / 16, row = R % 16;
+                        for (int ic = 0; ic < cin; ++ic)
+                            wm[((((size_t)(ic / 32) * 4 + n) * mbn + mb) * 16 + row) * 32 + ic % 32] =
+                                wn[((size_t)ic * 16 + ph * 4 + t) * L->coutp + oc];
+                    }
+                }
+            if (ok) L->wm16 = upload_as(ctx, wm, dtype, &L->wm16_bytes);
+        }
     }
     return L;
 }
@@ -634,6 +658,15 @@ static TensorP conv_forward_impl(Context& ctx, const Layer& L, const TensorP& x,
                    (double)L.wpk_bytes * (e.w_batch ? N : 1);
     if (e.r1) bytes += es * N * (double)L.cout * OH * OW;
     if (e.r2) bytes += es * N * (double)L.cout * OH * OW;
+    if (L.wn && !e.w_batch && L.wm16 && !(ctx.top().flags & ZJAI_CTX_VALU_NARROW_CONVT) &&
+        convT_mfma_k3(L.dtype, p, L.cin)) {
+        static const char* ty[] = {"float", "_Float16", "__bf16"};
+        char name[64];
+        snprintf(name, sizeof name, "k_convT3_mfma<%s, %d>", ty[L.dtype], L.coutp);
+        LaunchScope sc(ctx, name, 2.0 * macs, bytes);
+        ZJAI_HIP(launch_convT3_mfma(L.dtype, L.coutp, p, L.wm16, L.cin, ctx.stream));
+        return y;
+    }
     if (L.wn && !e.w_batch) {
         static const char* ty[] = {"float", "_Float16", "__bf16"};
         char name[64];
