@@ -1112,6 +1112,26 @@ k_convT3_mfma(const ConvParams p, const u32x4* __restrict__ wm) {
         }
 
     // Row R = 16 mb + 4 grp + r of column col: phase R / COUTP, output R % COUTP.
+    if constexpr (COUTP == 1) {
+        // Only the lanes of K group 0 hold real rows (the four phases of their position). Lane
+        // (col, g) takes position block g's four phases from lane col, so that every lane stores
+        // four outputs instead of a quarter of the lanes storing sixteen.
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float t = __shfl(acc[0][j][r], col);
+                if (grp == j) v[r] = t;
+            }
+        const int yq = y0 + 2 * wave + (grp >> 1), xq = x0 + 16 * (grp & 1) + col;
+#pragma unroll
+        for (int ph = 0; ph < 4; ++ph) {
+            const int oy = 2 * yq + (ph >> 1), ox = 2 * xq + (ph & 1);
+            if (oy < p.OH && ox < p.OW) epilogue_store<T>(p, bi, oy, ox, 0, 1, f32x4{v[ph], 0.0f, 0.0f, 0.0f});
+        }
+        return;
+    }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll

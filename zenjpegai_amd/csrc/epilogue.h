@@ -14,6 +14,35 @@ __device__ __forceinline__ float apply_act(int act, float v) {
     return v;
 }
 
+// v / s and v % s for a subsampling factor s (uniform per launch; 1 and 2 without a division).
+// v >= 0 wherever the quotient is used; for v < 0 only whether the remainder is zero matters.
+__device__ __forceinline__ int sub_div(int v, int s) { return s == 1 ? v : s == 2 ? (v >> 1) : v / s; }
+__device__ __forceinline__ int sub_rem(int v, int s) { return s == 1 ? 0 : s == 2 ? (v & 1) : v % s; }
+
+// One sample of a planar picture output at plane offset o: denormalise, then f32 or quantised u16.
+__device__ __forceinline__ void plane_store(const ConvParams& p, long long o, float s) {
+    if (p.denorm) {
+        s = s * 128.0f;
+        s = s + 127.5f;
+        s = s < 0.0f ? 0.0f : s;
+        s = s > 255.0f ? 255.0f : s;
+    }
+    if (p.bit_depth == 0) {
+        ((float*)p.plane)[o] = s;
+    } else {
+        // quantize_plane (src/decoder/output.rs:330-342): rint(clamp(x,0,255)/255*max).
+        const float mx = (float)((1u << p.bit_depth) - 1u);
+        float q = s < 0.0f ? 0.0f : s;
+        q = q > 255.0f ? 255.0f : q;
+        q = q / 255.0f;
+        q = q * mx;
+        q = rintf(q);
+        q = q < 0.0f ? 0.0f : q;
+        q = q > mx ? mx : q;
+        ((uint16_t*)p.plane)[o] = (uint16_t)q;
+    }
+}
+
 template <typename T>
 __device__ __forceinline__ void epilogue_store(const ConvParams& p, int b, int oy, int ox, int oc0,
                                                int nvalid, f32x4 v) {
@@ -77,6 +106,18 @@ __device__ __forceinline__ void epilogue_store(const ConvParams& p, int b, int o
     // Planar picture output (last layer): pixel shuffle, denormalise, crop to the kept window,
     // chroma subsampling, f32 or quantised u16.
     const int r = p.ps, rr = r * r;
+    if (r == 1) {
+        // No pixel shuffle: the nvalid channels share one output pixel, so its subsampling and
+        // window tests and plane offset are computed once (the subsampling test first: with
+        // 4:2:0 planes it drops three of every four pixels, often a whole wave's).
+        const int wy = oy - p.win_y0[b], wx = ox - p.win_x0[b];
+        const int py = p.dst_y0[b] + wy, px = p.dst_x0[b] + wx;
+        if (sub_rem(py, p.sv) || sub_rem(px, p.sh)) return;
+        if (wy < 0 || wy >= p.win_h[b] || wx < 0 || wx >= p.win_w[b]) return;
+        const long long o0 = (long long)sub_div(py, p.sv) * p.pl_row + sub_div(px, p.sh);
+        for (int i = 0; i < nvalid; ++i) plane_store(p, (long long)(oc0 + i) * p.pl_cstride + o0, v[i]);
+        return;
+    }
     for (int i = 0; i < nvalid; ++i) {
         const int oc = oc0 + i, c = oc / rr, sub = oc - c * rr;
         const int Y = oy * r + sub / r, X = ox * r + sub % r;
@@ -84,28 +125,7 @@ __device__ __forceinline__ void epilogue_store(const ConvParams& p, int b, int o
         if (wy < 0 || wy >= p.win_h[b] || wx < 0 || wx >= p.win_w[b]) continue;
         const int py = p.dst_y0[b] + wy, px = p.dst_x0[b] + wx;
         if (py % p.sv || px % p.sh) continue;
-        float s = v[i];
-        if (p.denorm) {
-            s = s * 128.0f;
-            s = s + 127.5f;
-            s = s < 0.0f ? 0.0f : s;
-            s = s > 255.0f ? 255.0f : s;
-        }
-        const long long o = (long long)c * p.pl_cstride + (long long)(py / p.sv) * p.pl_row + px / p.sh;
-        if (p.bit_depth == 0) {
-            ((float*)p.plane)[o] = s;
-        } else {
-            // quantize_plane (src/decoder/output.rs:330-342): rint(clamp(x,0,255)/255*max).
-            const float mx = (float)((1u << p.bit_depth) - 1u);
-            float q = s < 0.0f ? 0.0f : s;
-            q = q > 255.0f ? 255.0f : q;
-            q = q / 255.0f;
-            q = q * mx;
-            q = rintf(q);
-            q = q < 0.0f ? 0.0f : q;
-            q = q > mx ? mx : q;
-            ((uint16_t*)p.plane)[o] = (uint16_t)q;
-        }
+        plane_store(p, (long long)c * p.pl_cstride + (long long)(py / p.sv) * p.pl_row + px / p.sh, v[i]);
     }
 }
 
