@@ -9,7 +9,8 @@ latents already resident in HBM (``Picture.run``: the tiles in same-shape batche
 epilogues).
 
 ``value`` is the fp32-MFMA parity path (the reference computes in f32). ``one_stream``: the same
-picture with every launch on one HIP stream. Extra lines in ``extra``: the host-to-host rate of
+picture with every launch on one HIP stream; ``replay``: the same picture in replay mode (its
+launch sequence captured once as a HIP graph and launched again each step). Extra lines in ``extra``: the host-to-host rate of
 the same picture (latent upload, synthesis, download of the 10-bit planes; ``host_to_host``), the
 device time of the last timed step, the same picture on the f16 / bf16 paths (timed on He x 0.5
 weights, whose activations stay inside f16's range) with the PSNR of their 10-bit planes against
@@ -480,6 +481,12 @@ def main():
     pic.set_lanes(args.lanes)
     one_stream = {"lanes": 1, "ms_per_step": round(ms_one, 3), "value": round(pixels / (ms_one / 1e3) / 1e6, 3)}
     log(f"[bench] one stream: {ms_one:.2f} ms/step -> {one_stream['value']:.2f} Mpixel/s")
+    # Replay mode (the same lanes, the launch sequence captured once as a HIP graph).
+    pic.set_replay(True)
+    ms_replay = time_steps(eng, pic, args.steps, args.warmup)
+    pic.set_replay(False)
+    replay = {"ms_per_step": round(ms_replay, 3), "value": round(pixels / (ms_replay / 1e3) / 1e6, 3)}
+    log(f"[bench] replayed: {ms_replay:.2f} ms/step -> {replay['value']:.2f} Mpixel/s")
     h2h = host_to_host(eng, pic, info, args.steps)
     log(f"[bench] host to host: {h2h}")
     planes_ref = pic.download() if args.precision == "f32" else None
@@ -584,7 +591,11 @@ def main():
                 ms3 = time_steps(e3, p3, max(args.steps, 10), args.warmup)
                 extra[f"cfg4_sop_1mp_{prec}_mpix_s"] = round(i3["h"] * i3["w"] / (ms3 / 1e3) / 1e6, 3)
                 extra[f"cfg4_sop_1mp_{prec}_ms"] = round(ms3, 4)
-                log(f"[bench] cfg4 {prec}: {ms3:.3f} ms/step")
+                # Replay mode: the picture's launches captured once as a HIP graph.
+                p3.set_replay(True)
+                ms3r = time_steps(e3, p3, max(args.steps, 10), args.warmup)
+                extra[f"cfg4_sop_1mp_{prec}_replay_ms"] = round(ms3r, 4)
+                log(f"[bench] cfg4 {prec}: {ms3:.3f} ms/step, replayed {ms3r:.3f}")
                 del p3, e3
         if args.workload == "cfg5":
             for prec in (args.precision, "bf16"):
@@ -619,6 +630,7 @@ def main():
         "metric": METRIC, "value": round(value, 3), "unit": "Mpixel/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
         "one_stream": one_stream,
+        "replay": replay,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": args.precision, "data": "synthetic (He-normal random-init weights, Laplace latents)",
         "config": {

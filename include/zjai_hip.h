@@ -308,6 +308,18 @@ ZJAI_API int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic);
  * reference's tile-parallel synthesis (rayon over tiles, src/decoder/reconstruct.rs:379-464):
  * tiles are independent and write disjoint core rectangles. */
 ZJAI_API int32_t zjai_picture_set_lanes(zjai_ctx* ctx, zjai_picture* pic, int32_t lanes);
+/* Replay mode (on = 1): the next zjai_picture_run captures the picture's whole launch sequence --
+ * every tile batch on every lane -- once as a HIP graph instead of issuing it launch by launch,
+ * then launches it; later runs launch the same graph again (one host call per picture). Mirrors
+ * the reference's GPU backend, which records a dispatch plan per tile geometry and replays it
+ * (gpu/src/synthesis.rs:1163-1185, plan built by gpu/src/plan.rs:877 `Graph::finish`). The graph
+ * reads the picture's latent buffers and writes its planes, so zjai_picture_upload between runs
+ * takes effect; the intermediate buffers it addresses are taken out of the context's pools for
+ * its lifetime. Changing the lane count captures again; on = 0 drops the graph and its buffers.
+ * Eager and replayed runs give the same bytes. Per-launch profiling must be off while capturing;
+ * the stop flag is checked before a replay, not inside it; launch counts (zjai_get_stats) include
+ * a replay's launches. */
+ZJAI_API int32_t zjai_picture_set_replay(zjai_ctx* ctx, zjai_picture* pic, int32_t on);
 /* Copies the planes out (synchronises): Y out_h*out_w, U/V ceil(out_h/sv)*ceil(out_w/sh)
  * samples each, as float (bit_depth 0) or uint16. u/v may be NULL without net_uv. */
 ZJAI_API int32_t zjai_picture_download(zjai_ctx* ctx, zjai_picture* pic, void* y, void* u, void* v);

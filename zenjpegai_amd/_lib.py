@@ -129,6 +129,7 @@ PROTOTYPES = {
     "zjai_picture_upload": [_vp, _vp, _f32p, _f32p],
     "zjai_picture_run": [_vp, _vp],
     "zjai_picture_set_lanes": [_vp, _vp, _i32],
+    "zjai_picture_set_replay": [_vp, _vp, _i32],
     "zjai_picture_download": [_vp, _vp, _vp, _vp, _vp],
     "zjai_host_alloc": [_vp, _sz, _pp],
     "zjai_host_free": [_vp, _vp],

@@ -757,7 +757,25 @@ struct zjai_picture {
     uint16_t* out_rgb = nullptr;  // [out_h][out_w][3] (zjai_picture_download_rgb)
     float* out_rgbf = nullptr;    // [3][out_h][out_w]
     bool uploaded = false;
+    // Replay (zjai_picture_set_replay): the run's launch sequence captured once as a HIP graph,
+    // the pool blocks its launches address, its launch count and the lane count it was captured
+    // with; fork is the event the lanes wait on inside the capture.
+    bool replay = false;
+    hipGraphExec_t gexec = nullptr;
+    std::vector<void*> gbufs;
+    long long glaunches = 0;
+    int glanes = 0;
+    hipEvent_t fork = nullptr;
+    void drop_graph() {
+        if (gexec) (void)hipGraphExecDestroy(gexec);
+        gexec = nullptr;
+        for (void* q : gbufs) (void)hipFree(q);
+        gbufs.clear();
+        glanes = 0;
+    }
     ~zjai_picture() {
+        drop_graph();
+        if (fork) (void)hipEventDestroy(fork);
         for (hipEvent_t e : lane_ev) (void)hipEventDestroy(e);
         if (y_hat) (void)hipFree(y_hat);
         if (uv_hat) (void)hipFree(uv_hat);
@@ -849,13 +867,123 @@ extern "C" int32_t zjai_picture_upload(zjai_ctx* ctx, zjai_picture* pic, const f
     });
 }
 
+// Issues every tile batch of the picture: batch i on lane i % nl (nl > 1: the lanes first wait
+// for `fork` on the root stream, and the root stream waits for every lane at the end).
+static void issue_picture(Context& root, zjai_picture* pic, int nl, hipEvent_t fork) {
+    const int dt = pic->net_y->dtype;
+    if (nl > 1) {
+        for (int i = 0; i < nl; ++i) ZJAI_HIP(hipStreamWaitEvent(root.lane(i).stream, fork, 0));
+    }
+    for (size_t bidx = 0; bidx < pic->batches.size(); ++bidx) {
+        const std::vector<int>& group = pic->batches[bidx];
+        Context& c = nl > 1 ? root.lane((int)bidx % nl) : root;
+        c.check_stop();
+        const zjai_tile& t0 = pic->tiles[group[0]];
+        const int N = (int)group.size();
+        Windows win{};
+        PlaneOut py;
+        py.plane = pic->out_y;
+        py.row = pic->out_w;
+        py.bit_depth = pic->bit_depth;
+        for (int b = 0; b < N; ++b) {
+            const zjai_tile& t = pic->tiles[group[b]];
+            win.x0[b] = t.latent_x;
+            win.y0[b] = t.latent_y;
+            // synthesize_luma_into (src/decoder/reconstruct.rs:379-411): core rows/cols that
+            // fall inside the displayed picture.
+            py.win_y0[b] = t.core_off_y;
+            py.win_x0[b] = t.core_off_x;
+            py.win_h[b] = std::min(t.core_h, std::max(pic->out_h - t.core_y, 0));
+            py.win_w[b] = std::min(t.core_w, std::max(pic->out_w - t.core_x, 0));
+            py.dst_y0[b] = t.core_y;
+            py.dst_x0[b] = t.core_x;
+        }
+        TensorP by = c.alloc(N, 160, t0.latent_h, t0.latent_w, dt);
+        {
+            LaunchScope sc(c, kname("k_planar_to_nhwc", dt), 0.0, (4.0 + dtype_size(dt)) * N * 160 * t0.latent_h * t0.latent_w);
+            ZJAI_HIP(launch_planar_to_nhwc(pic->y_hat, 160, pic->lh, pic->lw, win, N, t0.latent_h, t0.latent_w,
+                                           by->v, dt, c.stream));
+        }
+        primary_forward(c, *pic->net_y, by, t0.image_h, t0.image_w, py);
+        if (pic->net_uv) {
+            TensorP buv = c.alloc(N, 96, t0.latent_h, t0.latent_w, dt);
+            {
+                LaunchScope sc(c, kname("k_planar_to_nhwc", dt), 0.0, (4.0 + dtype_size(dt)) * N * 96 * t0.latent_h * t0.latent_w);
+                ZJAI_HIP(launch_planar_to_nhwc(pic->uv_hat, 96, pic->lh, pic->lw, win, N, t0.latent_h,
+                                               t0.latent_w, buv->v, dt, c.stream));
+            }
+            // synthesize_chroma_into (src/decoder/reconstruct.rs:416-464)
+            PlaneOut pu = py;
+            pu.plane = pic->out_uv;
+            pu.row = pic->cw();
+            pu.cstride = (long long)pic->ch() * pic->cw();
+            pu.sv = pic->sv;
+            pu.sh = pic->sh;
+            secondary_forward(c, *pic->net_uv, by, buv, t0.image_h, t0.image_w, pu);
+        }
+    }
+    if (nl > 1) {
+        for (int i = 0; i < nl; ++i) {
+            ZJAI_HIP(hipEventRecord(pic->lane_ev[i], root.lane(i).stream));
+            ZJAI_HIP(hipStreamWaitEvent(root.stream, pic->lane_ev[i], 0));
+        }
+    }
+}
+
+// Replay mode: captures issue_picture's launches on the root stream (and, through the fork
+// event, on every lane) as one HIP graph instead of running them. Nothing executes during the
+// capture, so the pools hand out and take back blocks exactly as in an eager run; afterwards the
+// blocks the graph addresses leave the pools (pic->gbufs) so that no later allocation can take
+// one while a replay writes it. Captures no memset or copy: only kernels and the fork / join
+// event dependencies.
+static void capture_picture(Context& root, zjai_picture* pic, int nl) {
+    pic->drop_graph();
+    need(!root.profiling, "replay: per-launch profiling is on (profile eager runs)");
+    if (!pic->fork) ZJAI_HIP(hipEventCreateWithFlags(&pic->fork, hipEventDisableTiming));
+    std::vector<Context*> ctxs{&root};
+    for (int i = 0; i < nl && nl > 1; ++i) ctxs.push_back(&root.lane(i));
+    std::vector<size_t> held;
+    for (Context* c : ctxs) {
+        range_slots_init(*c);
+        held.push_back(c->pool.in_use());
+    }
+    const long long l0 = root.launches;
+    ZJAI_HIP(hipStreamBeginCapture(root.stream, hipStreamCaptureModeRelaxed));
+    hipGraph_t g = nullptr;
+    try {
+        ZJAI_HIP(hipEventRecord(pic->fork, root.stream));
+        issue_picture(root, pic, nl, pic->fork);
+    } catch (...) {
+        // Join every lane back to the root stream so that the capture ends cleanly, then drop it.
+        for (int i = 0; i < nl && nl > 1; ++i) {
+            (void)hipEventRecord(pic->lane_ev[i], root.lane(i).stream);
+            (void)hipStreamWaitEvent(root.stream, pic->lane_ev[i], 0);
+        }
+        if (hipStreamEndCapture(root.stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+        root.launches = l0;
+        throw;
+    }
+    ZJAI_HIP(hipStreamEndCapture(root.stream, &g));
+    const hipError_t e = hipGraphInstantiate(&pic->gexec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    ZJAI_HIP(e);
+    pic->glaunches = root.launches - l0;
+    root.launches = l0;
+    pic->glanes = nl;
+    for (size_t i = 0; i < ctxs.size(); ++i) {
+        if (ctxs[i]->pool.in_use() != held[i]) {
+            pic->drop_graph();
+            throw Error(ZJAI_E_DEVICE, "replay: a buffer of the captured run is still held");
+        }
+        ctxs[i]->pool.surrender(pic->gbufs);
+    }
+}
+
 extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
     if (!ctx || !pic) return ZJAI_E_INVALID_ARGUMENT;
     return guard(ctx, [&] {
         need(pic->uploaded, "latents not uploaded");
         Context& root = ctx->c;
-        const int dt = pic->net_y->dtype;
-        ZJAI_HIP(hipEventRecord(root.ev0, root.stream));
         // Tiles of one image size share every layer shape: run them as one batch of up to MAXB
         // (each launch then covers all of them). Batches are independent (disjoint core
         // rectangles of the output planes, read-only latents), so with lanes > 1 batch i runs
@@ -866,9 +994,18 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
             ZJAI_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
             pic->lane_ev.push_back(e);
         }
-        if (nl > 1) {
-            for (int i = 0; i < nl; ++i) ZJAI_HIP(hipStreamWaitEvent(root.lane(i).stream, root.ev0, 0));
+        if (pic->replay) {
+            if (!pic->gexec || pic->glanes != nl) capture_picture(root, pic, nl);
+            root.check_stop();
+            ZJAI_HIP(hipEventRecord(root.ev0, root.stream));
+            ZJAI_HIP(hipGraphLaunch(pic->gexec, root.stream));
+            root.launches += pic->glaunches;
+            ZJAI_HIP(hipEventRecord(root.ev1, root.stream));
+            ZJAI_HIP(hipEventSynchronize(root.ev1));
+            ZJAI_HIP(hipEventElapsedTime(&root.last_ms, root.ev0, root.ev1));
+            return;
         }
+        ZJAI_HIP(hipEventRecord(root.ev0, root.stream));
         // A failure or cancellation part way through leaves the other lanes' batches queued:
         // drain every stream before reporting it, so the picture and the context are idle and
         // reusable when the call returns.
@@ -882,64 +1019,19 @@ extern "C" int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic) {
                 (void)hipStreamSynchronize(root.stream);
             }
         } drain{root, nl};
-        for (size_t bidx = 0; bidx < pic->batches.size(); ++bidx) {
-            const std::vector<int>& group = pic->batches[bidx];
-            Context& c = nl > 1 ? root.lane((int)bidx % nl) : root;
-            c.check_stop();
-            const zjai_tile& t0 = pic->tiles[group[0]];
-            const int N = (int)group.size();
-            Windows win{};
-            PlaneOut py;
-            py.plane = pic->out_y;
-            py.row = pic->out_w;
-            py.bit_depth = pic->bit_depth;
-            for (int b = 0; b < N; ++b) {
-                const zjai_tile& t = pic->tiles[group[b]];
-                win.x0[b] = t.latent_x;
-                win.y0[b] = t.latent_y;
-                // synthesize_luma_into (src/decoder/reconstruct.rs:379-411): core rows/cols that
-                // fall inside the displayed picture.
-                py.win_y0[b] = t.core_off_y;
-                py.win_x0[b] = t.core_off_x;
-                py.win_h[b] = std::min(t.core_h, std::max(pic->out_h - t.core_y, 0));
-                py.win_w[b] = std::min(t.core_w, std::max(pic->out_w - t.core_x, 0));
-                py.dst_y0[b] = t.core_y;
-                py.dst_x0[b] = t.core_x;
-            }
-            TensorP by = c.alloc(N, 160, t0.latent_h, t0.latent_w, dt);
-            {
-                LaunchScope sc(c, kname("k_planar_to_nhwc", dt), 0.0, (4.0 + dtype_size(dt)) * N * 160 * t0.latent_h * t0.latent_w);
-                ZJAI_HIP(launch_planar_to_nhwc(pic->y_hat, 160, pic->lh, pic->lw, win, N, t0.latent_h, t0.latent_w,
-                                               by->v, dt, c.stream));
-            }
-            primary_forward(c, *pic->net_y, by, t0.image_h, t0.image_w, py);
-            if (pic->net_uv) {
-                TensorP buv = c.alloc(N, 96, t0.latent_h, t0.latent_w, dt);
-                {
-                    LaunchScope sc(c, kname("k_planar_to_nhwc", dt), 0.0, (4.0 + dtype_size(dt)) * N * 96 * t0.latent_h * t0.latent_w);
-                    ZJAI_HIP(launch_planar_to_nhwc(pic->uv_hat, 96, pic->lh, pic->lw, win, N, t0.latent_h,
-                                                   t0.latent_w, buv->v, dt, c.stream));
-                }
-                // synthesize_chroma_into (src/decoder/reconstruct.rs:416-464)
-                PlaneOut pu = py;
-                pu.plane = pic->out_uv;
-                pu.row = pic->cw();
-                pu.cstride = (long long)pic->ch() * pic->cw();
-                pu.sv = pic->sv;
-                pu.sh = pic->sh;
-                secondary_forward(c, *pic->net_uv, by, buv, t0.image_h, t0.image_w, pu);
-            }
-        }
-        if (nl > 1) {
-            for (int i = 0; i < nl; ++i) {
-                ZJAI_HIP(hipEventRecord(pic->lane_ev[i], root.lane(i).stream));
-                ZJAI_HIP(hipStreamWaitEvent(root.stream, pic->lane_ev[i], 0));
-            }
-        }
+        issue_picture(root, pic, nl, root.ev0);
         drain.armed = false;
         ZJAI_HIP(hipEventRecord(root.ev1, root.stream));
         ZJAI_HIP(hipEventSynchronize(root.ev1));
         ZJAI_HIP(hipEventElapsedTime(&root.last_ms, root.ev0, root.ev1));
+    });
+}
+
+extern "C" int32_t zjai_picture_set_replay(zjai_ctx* ctx, zjai_picture* pic, int32_t on) {
+    if (!ctx || !pic || (on != 0 && on != 1)) return ZJAI_E_INVALID_ARGUMENT;
+    return guard(ctx, [&] {
+        pic->replay = on != 0;
+        if (!pic->replay) pic->drop_graph();
     });
 }
 

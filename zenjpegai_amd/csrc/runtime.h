@@ -58,6 +58,9 @@ public:
     void* alloc(size_t bytes);
     void release(void* p);
     void trim();
+    // Hands every cached (free) block to the caller, who frees it with hipFree: a captured HIP
+    // graph keeps the blocks its launches address out of later allocations.
+    void surrender(std::vector<void*>& out);
     size_t in_use() const { return in_use_; }
     size_t peak() const { return peak_; }
     size_t cached() const { return cached_; }
@@ -148,6 +151,9 @@ private:
 // ZJAI_CTX_COUNT_F16_RANGE: adds the non-finite samples of an f16 tensor just written on ctx's
 // stream to ctx's counters (no-op for other precisions or without the flag).
 void count_f16_range(Context& ctx, const Tensor& t);
+// Allocates and clears ctx's counters when the flag is set (count_f16_range does it on first use;
+// a HIP graph capture does it beforehand, so that the clearing is not part of the graph).
+void range_slots_init(Context& ctx);
 constexpr int RANGE_SLOTS = 256;
 // Sum of every lane's counters (synchronises the context's streams).
 unsigned long long f16_range_total(Context& root);

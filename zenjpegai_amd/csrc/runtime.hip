@@ -62,6 +62,14 @@ void Pool::trim() {
     free_.clear();
 }
 
+void Pool::surrender(std::vector<void*>& out) {
+    for (auto& kv : free_) {
+        out.push_back(kv.second);
+        cached_ -= kv.first;
+    }
+    free_.clear();
+}
+
 Pool::~Pool() {
     for (auto& kv : free_) (void)hipFree(kv.second);
     for (auto& kv : live_) (void)hipFree(kv.first);
@@ -130,12 +138,15 @@ Context::~Context() {
     if (range_slots) (void)hipFree(range_slots);
 }
 
+void range_slots_init(Context& ctx) {
+    if (ctx.range_slots || !(ctx.top().flags & ZJAI_CTX_COUNT_F16_RANGE)) return;
+    ZJAI_HIP(hipMalloc(&ctx.range_slots, sizeof(unsigned long long) * RANGE_SLOTS));
+    ZJAI_HIP(launch_zero(ctx.range_slots, sizeof(unsigned long long) * RANGE_SLOTS, ctx.stream));
+}
+
 void count_f16_range(Context& ctx, const Tensor& t) {
     if (t.dtype != DT_F16 || !(ctx.top().flags & ZJAI_CTX_COUNT_F16_RANGE)) return;
-    if (!ctx.range_slots) {
-        ZJAI_HIP(hipMalloc(&ctx.range_slots, sizeof(unsigned long long) * RANGE_SLOTS));
-        ZJAI_HIP(launch_zero(ctx.range_slots, sizeof(unsigned long long) * RANGE_SLOTS, ctx.stream));
-    }
+    range_slots_init(ctx);
     LaunchScope sc(ctx, "k_count_f16_nonfinite", 0.0, 2.0 * t.n * t.c * t.h * t.w);
     ZJAI_HIP(launch_count_f16_nonfinite(t.v, t.n, t.c, t.h, t.w, ctx.range_slots, RANGE_SLOTS, ctx.stream));
 }

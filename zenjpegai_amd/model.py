@@ -174,6 +174,11 @@ class Picture:
         check(lib().zjai_picture_set_lanes(self.eng.handle, self._h, lanes), self.eng.handle)
         self.lanes = lanes
 
+    def set_replay(self, on: bool):
+        """Replay mode: the next run captures the whole launch sequence as a HIP graph, later
+        runs replay it (``zjai_picture_set_replay``)."""
+        check(lib().zjai_picture_set_replay(self.eng.handle, self._h, 1 if on else 0), self.eng.handle)
+
     def upload(self, y_hat: np.ndarray, uv_hat: np.ndarray | None = None):
         self._y = _f32(y_hat)
         self._uv = _f32(uv_hat)
