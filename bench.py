@@ -129,11 +129,14 @@ def host_to_host(eng, pic, info, reps):
     pageable = timed(info["y"], info["uvl"], None)
     y = eng.host_array(info["y"].shape)
     y[...] = info["y"]
-    uv = eng.host_array(info["uvl"].shape)
-    uv[...] = info["uvl"]
+    uv = None
+    if info["uvl"] is not None:
+        uv = eng.host_array(info["uvl"].shape)
+        uv[...] = info["uvl"]
     dt = np.uint16 if pic.bit_depth else np.float32
     ch, cw = -(-pic.out_h // pic.sv), -(-pic.out_w // pic.sh)
-    out = (eng.host_array((pic.out_h, pic.out_w), dt), eng.host_array((ch, cw), dt), eng.host_array((ch, cw), dt))
+    planes_uv = (eng.host_array((ch, cw), dt), eng.host_array((ch, cw), dt)) if uv is not None else (None, None)
+    out = (eng.host_array((pic.out_h, pic.out_w), dt),) + planes_uv
     ms = timed(y, uv, out)
     return {"ms_per_picture": round(ms, 3), "mpix_s": round(info["h"] * info["w"] / (ms / 1e3) / 1e6, 3),
             "pageable_ms_per_picture": round(pageable, 3)}
