@@ -318,7 +318,8 @@ ZJAI_API int32_t zjai_picture_set_lanes(zjai_ctx* ctx, zjai_picture* pic, int32_
  * its lifetime. Changing the lane count captures again; on = 0 drops the graph and its buffers.
  * Eager and replayed runs give the same bytes. Per-launch profiling must be off while capturing;
  * the stop flag is checked before a replay, not inside it; launch counts (zjai_get_stats) include
- * a replay's launches. */
+ * a replay's launches; injected launch failures (zjai_inject_failure) count launches issued from
+ * the host, i.e. eager runs and the capture, not the kernels of a replay. */
 ZJAI_API int32_t zjai_picture_set_replay(zjai_ctx* ctx, zjai_picture* pic, int32_t on);
 /* Copies the planes out (synchronises): Y out_h*out_w, U/V ceil(out_h/sv)*ceil(out_w/sh)
  * samples each, as float (bit_depth 0) or uint16. u/v may be NULL without net_uv. */

@@ -10,7 +10,7 @@ holds no memset or copy, only kernels and fork / join event dependencies.
 import numpy as np
 import pytest
 
-from zenjpegai_amd import model, nn, synth
+from zenjpegai_amd import _lib, model, nn, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -102,6 +102,37 @@ def test_replay_refuses_capture_while_profiling():
     with pytest.raises(nn.HipError):
         pic.run()
     eng.profile_end()
+    pic.run()
+    assert _same(pic.download(), want)
+    eng.close()
+
+
+@pytest.mark.parametrize("lanes", [1, 3])
+def test_a_failure_during_the_capture_leaves_the_picture_usable(lanes):
+    """An injected launch failure (host side, before the launch is queued) part way through the
+    capture: the run reports the device error, the capture is abandoned with every lane joined
+    back and nothing launched, and the next run captures again and replays the eager bytes; an
+    eager run afterwards gives them too. (Injected launch failures count the launches issued from
+    the host -- eager runs and captures; a replay is one graph launch.)"""
+    eng = nn.Engine(0, "f32")
+    pic, keep, (lh, lw) = _picture(eng, "hop", lanes)
+    pic.upload(*_latents(5, lh, lw, True))
+    before = eng.stats()["kernel_launches"]
+    pic.run()
+    per_run = eng.stats()["kernel_launches"] - before
+    want = pic.download()
+    for after in (0, per_run // 2):
+        pic.set_replay(False)  # drops any graph, so the next run captures
+        pic.set_replay(True)
+        eng.inject_failure(_lib.FAIL_LAUNCH, after)
+        with pytest.raises(nn.HipError) as e:
+            pic.run()
+        assert e.value.kind == "Device" and "injected launch failure" in str(e.value)
+        pic.run()  # captures again (the plan disarmed itself), then replays
+        assert _same(pic.download(), want), after
+        pic.run()  # a replay of the graph just captured
+        assert _same(pic.download(), want), after
+    pic.set_replay(False)
     pic.run()
     assert _same(pic.download(), want)
     eng.close()
