@@ -328,12 +328,20 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
             // pos & 7: the 16 lanes of a position read four units of its row, and the phase-a stores
             // of 16 positions spread over all banks (measured faster than a swizzle that also keeps
             // the reads of four neighbouring positions on disjoint banks, which spills registers).
+            // The swizzle pos & 7 of halo position (hr, dc + kx) is (dc + kx) & 7 (FH is a
+            // multiple of 8), so each read is a per-kx offset plus hr rows.
+            static_assert(FH % 8 == 0, "row swizzle");
+            int offa[3], offb[3];
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                const int c = dc + kx, sw = c & 7;
+                offa[kx] = c * 64 + 2 * (pg & 3) + ((pg >> 2) ^ sw) * 8;
+                offb[kx] = c * 64 + 2 * (pg & 3) + ((4 + (pg >> 2)) ^ sw) * 8;
+            }
             auto ld = [&](int hr, int kx, float (&oa)[2], float (&ob)[2]) {
-                const int pos = hr * FH + dc + kx;
-                const int sw = pos & 7;
-                const T* row = (const T*)s_p + pos * 64 + 2 * (pg & 3);
-                unpack2<T>(*(const unsigned*)(row + ((pg >> 2) ^ sw) * 8), oa);
-                unpack2<T>(*(const unsigned*)(row + ((4 + (pg >> 2)) ^ sw) * 8), ob);
+                const T* rows = (const T*)s_p + hr * (FH * 64);
+                unpack2<T>(*(const unsigned*)(rows + offa[kx]), oa);
+                unpack2<T>(*(const unsigned*)(rows + offb[kx]), ob);
             };
             float xa[3][3][2], xb[3][3][2];
             const int r0 = rh * (FT / 2);
@@ -568,9 +576,14 @@ __global__ void __launch_bounds__(FTHREADS) k_qkv(const QkvArgs p) {
             }
             const T* sp = reinterpret_cast<const T*>(s_p) + 2 * (pg & 3);
             float xw[3][3][2];
+            // The swizzle pos & 7 of halo position (hr, dc + kx) is (dc + kx) & 7 (FH is a
+            // multiple of 8), so each read is a per-kx offset plus hr rows.
+            static_assert(FH % 8 == 0, "row swizzle");
+            int off[3];
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) off[kx] = (dc + kx) * 64 + ((pg >> 2) ^ ((dc + kx) & 7)) * 8;
             auto ld = [&](int hr, int kx, float (&o)[2]) {
-                const int pos = hr * FH + dc + kx;
-                unpack2<T>(*(const unsigned*)(sp + pos * 64 + ((pg >> 2) ^ (pos & 7)) * 8), o);
+                unpack2<T>(*(const unsigned*)(sp + hr * (FH * 64) + off[kx]), o);
             };
 #pragma unroll
             for (int kx = 0; kx < 3; ++kx) {
@@ -858,10 +871,20 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
                 wa[tp] = dww[tp * 64 + pg];
                 wb[tp] = dww[tp * 64 + 32 + pg];
             }
+            // p row of halo position (hr, dc + kx): hr * FH + dc + kx, its two 32-channel halves
+            // swapped on odd positions. FH is even, so the swap depends on dc + kx only and each
+            // read is a fixed per-kx offset plus hr rows (immediate offsets once the rows unroll).
+            int offa[3], offb[3];
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                const int c = dc + kx, odd = c & 1;
+                offa[kx] = c * 64 + odd * 32 + pg;
+                offb[kx] = c * 64 + (odd ^ 1) * 32 + pg;
+            }
+            static_assert(FH % 2 == 0, "row parity");
             auto ld = [&](int hr, int kx, float& oa, float& ob) {
-                const int pos = hr * FH + dc + kx, odd = pos & 1;
-                oa = s_p[pos * 64 + odd * 32 + pg];
-                ob = s_p[pos * 64 + (odd ^ 1) * 32 + pg];
+                oa = s_p[hr * (FH * 64) + offa[kx]];
+                ob = s_p[hr * (FH * 64) + offb[kx]];
             };
             float xa[3][3], xq[3][3];
 #pragma unroll
@@ -869,7 +892,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
                 ld(0, kx, xa[0][kx], xq[0][kx]);
                 ld(1, kx, xa[1][kx], xq[1][kx]);
             }
-#pragma unroll 2
+#pragma unroll
             for (int oy = 0; oy < FT; ++oy) {
 #pragma unroll
                 for (int kx = 0; kx < 3; ++kx) ld(oy + 2, kx, xa[2][kx], xq[2][kx]);
@@ -1030,9 +1053,15 @@ __global__ void __launch_bounds__(FTHREADS) k_qkv_f32(const QkvArgs p) {
                 for (int tp = 0; tp < 9; ++tp) wv[tp][k] = dww[tp * 64 + 2 * pg + k];
             }
             float xw[3][3][2];
+            // The swizzle pos & PSWZ of halo position (hr, dc + kx) is (dc + kx) & PSWZ (PSWZ < FH,
+            // FH a power of two), so each read is a per-kx offset plus hr rows.
+            static_assert(PSWZ < FH && (FH & (FH - 1)) == 0, "row swizzle");
+            int off[3];
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx)
+                off[kx] = (dc + kx) * 64 + ((((pg >> 1) ^ ((dc + kx) & PSWZ)) << 2) + 2 * (pg & 1));
             auto ld = [&](int hr, int kx, float (&o)[2]) {
-                const int pos = hr * FH + dc + kx;
-                const f32x2 v = *(const f32x2*)(s_p + pos * 64 + ((((pg >> 1) ^ (pos & PSWZ)) << 2) + 2 * (pg & 1)));
+                const f32x2 v = *(const f32x2*)(s_p + hr * (FH * 64) + off[kx]);
                 o[0] = v[0];
                 o[1] = v[1];
             };
