@@ -12,15 +12,18 @@ epilogues).
 picture's launch sequence captured once as a HIP graph and launched again each step, as a
 decoder of many pictures of one geometry runs it (the reference's GPU backend replays a dispatch
 plan per tile geometry the same way). ``eager``: the same picture with every launch issued from
-the host; ``one_stream``: eager with every launch on one HIP stream. Extra lines in ``extra``: the host-to-host rate of
-the same picture (latent upload, synthesis, download of the 10-bit planes; ``host_to_host``), the
-device time of the last timed step, the same picture on the f16 / bf16 paths (timed on He x 0.5
-weights, whose activations stay inside f16's range) with the PSNR of their 10-bit planes against
-the f32 path's at gains 1 and 0.5, the number of f16 activations stored as non-finite at both
-gains (``ZJAI_CTX_COUNT_F16_RANGE``), the reference's f16-weight semantics (weights rounded to
-f16, f32 activations: time and PSNR at both gains), BASELINE config 4 (SOP luma 1024x1024,
-8-bit; f32 and bf16), a 4 MP HOP picture (2048x2048, 1 MP header tiles) and BASELINE configs 1-3
-as single layers (kernel time and TFLOP/s, f32 and bf16).
+the host; ``one_stream``: eager with every launch on one HIP stream.
+
+Extra lines in ``extra``: the host-to-host rate of the same picture (latent upload, synthesis,
+download of the 10-bit planes; ``host_to_host``), the device time of the last timed step, the
+same picture on the bf16 path and on the f16 path (the latter timed on He x 0.5 weights, whose
+activations stay inside f16's range), eager and replayed (``*_replay_mpix_s``), with the PSNR of
+their 10-bit planes against the f32 path's at gains 1 and 0.5, the number of f16 activations
+stored as non-finite at both gains (``ZJAI_CTX_COUNT_F16_RANGE``), the reference's f16-weight
+semantics (weights rounded to f16, f32 activations: time and PSNR at both gains), BASELINE
+config 4 (SOP luma 1024x1024, 8-bit; f32 and bf16, eager and replayed), a 4 MP HOP picture
+(2048x2048, 1 MP header tiles) and BASELINE configs 1-3 as single layers (kernel time and
+TFLOP/s, f32 and bf16).
 
 ``roofline``: one profiled step (HIP events around every launch, all on one stream); the
 dominant kernel is the one with the largest summed time; bound by its arithmetic intensity
@@ -554,7 +557,10 @@ def main():
             extra[f"{args.workload}_{prec}_mpix_s"] = round(pixels / (ms2 / 1e3) / 1e6, 3)
             extra[f"{args.workload}_{prec}_weights_he_gain"] = gain
             extra[f"{args.workload}_{prec}_conv_tflops"] = round(cf / (cm / 1e3) / 1e12, 3)
-            log(f"[bench] {prec}: {ms2:.2f} ms/step (He x {gain})")
+            p2.set_replay(True)
+            ms2r = time_steps(e2, p2, args.steps, args.warmup)
+            extra[f"{args.workload}_{prec}_replay_mpix_s"] = round(pixels / (ms2r / 1e3) / 1e6, 3)
+            log(f"[bench] {prec}: {ms2:.2f} ms/step, replayed {ms2r:.2f} (He x {gain})")
             del p2, e2
         if args.precision == "f32" and args.workload == "cfg5":
             # PSNR of the 16-bit paths against the f32 planes on the benchmarked nets (gain 1)
