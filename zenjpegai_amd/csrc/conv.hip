@@ -79,6 +79,9 @@ conv_igemm(const ConvParams p) {
     const int gb = nt * NB;
     const int g = gb / p.nblk_g, nb0 = gb - g * p.nblk_g;
     const int ox0 = tx * 16, oy0 = ty * TY;
+    // A channel tile of padding blocks only (a narrow tile past cout_g: the packing rounds the
+    // blocks up to the layer's default tile) has nothing to compute or store (uniform exit).
+    if (nb0 * 16 >= p.cout_g) return;
 
     int ntap = NTAP;
     int tdy[NTAP], tdx[NTAP];
