@@ -252,10 +252,8 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
     const int pg = tid & 15, dc = (tid >> 4) % FT, rh = (tid >> 4) / FT;
     const bool dw_thread = tid < 2 * FT * 16;
 
-    for (int s = 0; s < NS; ++s) {
-        __syncthreads();  // u, W_in(s), W_out(s) ready; g and p free
-        if (s + 1 < NS) fetch_w(s + 1);
-
+    // Phase a of slice s: p slice = bias + u x W_in into LDS.
+    auto phase_a = [&](int s) __attribute__((always_inline)) {
         // a. p slice = bias + u x W_in: the two 16-channel blocks of half cb1 (0: channels
         //    32 s .., 1: hid + 32 s ..) x position blocks 4 pb1 .. 4 pb1 + 3.
         //    16x16x32 MFMAs with K in 32-channel chunks, bias first: the unfused 1x1 conv's
@@ -306,9 +304,9 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
                 *reinterpret_cast<t4*>(dst) = v;
             }
         }
-        __syncthreads();  // p ready; W_in(s) consumed
-        if (s + 1 < NS) put_w(s + 1);
-
+    };
+    // Phase b of slice s: depthwise 3x3 + gate, p -> g.
+    auto phase_b = [&](int s) __attribute__((always_inline)) {
         // b. depthwise 3x3 + gate: rows 7 rh .. 7 rh + 6 of column dc, pairs 32 s + 2 pg + {0, 1}.
         if (dw_thread) {
             // Local channel 2 pg + k (first half) and 32 + 2 pg + k (second half).
@@ -381,8 +379,9 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
                     }
             }
         }
-        __syncthreads();  // g ready
-
+    };
+    // Phase c of slice s: y += W_out(s) x g.
+    auto phase_c = [&](int s) __attribute__((always_inline)) {
         // c. y += W_out(s) x g (output-channel block cb2, position blocks pw2 + WPC * i).
         const u32x4 a = s_wo[(s & 1) * WO_U + (cb2 * 16 + col) * 4 + grp];
 #pragma unroll
@@ -390,6 +389,23 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
             const int pb = pw2 + WPC * i;
             if (pb < FPB) Mma16<T>::run(acc2[i], a, s_g[(pb * 16 + col) * 4 + grp]);
         }
+    };
+
+    // Two barriers per slice: phase c of slice s and phase a of slice s + 1 share one barrier
+    // interval (c reads g and W_out(s); a reads u, W_in(s + 1) and writes p, which every wave
+    // finished reading before the barrier ahead of c). Per accumulator the MFMAs run in the same
+    // order as with a barrier between them.
+    __syncthreads();  // u, W_in(0), W_out(0) ready
+    if (NS > 1) fetch_w(1);
+    phase_a(0);
+    for (int s = 0; s < NS; ++s) {
+        __syncthreads();  // p(s) ready; W_in(s) consumed; g and W_out(s - 1) free
+        if (s + 1 < NS) put_w(s + 1);
+        phase_b(s);
+        __syncthreads();  // g(s) ready; W(s + 1) in LDS; p free
+        if (s + 2 < NS) fetch_w(s + 2);
+        phase_c(s);
+        if (s + 1 < NS) phase_a(s + 1);
     }
 
     // ---- 3. y = acc + x through an LDS transpose.
