@@ -28,6 +28,16 @@ namespace zjai {
 // The 16x16 fragment of mfma.h (Mma16): 4 x 16x16x4 f32 steps or one 16x16x32 16-bit step.
 template <typename T> using Mma = Mma16<T>;
 
+// Staged operands keep 4 16-byte units (one K group each) per row: a halo slot or a weight row,
+// unit q of row r at q ^ qswz(r). A fragment read (ds_read_b128) takes 16 consecutive rows x 4
+// K groups, lane (row, group) = (lane % 16, lane / 16). gfx950 serves such a read in four
+// passes of 16 lanes, lane l in pass (l / 32, parity of bits 2..4 of l), 16 bytes per bank
+// quad, 64 banks: unswizzled, each pass holds two lanes per bank quad (2-way conflicts);
+// flipping bit 1 of the unit index in rows with bit 2 set spreads every pass over all banks,
+// for any first row, and keeps the 8-lane passes of the register-staged 16-byte stores
+// conflict-free too (measured with rocprofv3's SQ_LDS_BANK_CONFLICT on lane-pattern probes).
+__device__ __forceinline__ int qswz(int r) { return (r & 4) >> 1; }
+
 // SG: input-channel chunks staged per barrier. 1x1 layers do little matrix work per chunk, so
 // they stage several (SG = 4: the whole K of a 128-channel f16 layer) with every global load of
 // the stage issued before its LDS stores -- more bytes in flight per workgroup, fewer barriers.
@@ -127,11 +137,11 @@ conv_igemm(const ConvParams p) {
             const int ky = tdy[t], kx = tdx[t];
             u32x4 a[CF], b[PF];
 #pragma unroll
-            for (int cf = 0; cf < CF; ++cf) a[cf] = s_w[((wc * CF + cf) * NTAP + t) * 64 + col * 4 + grp];
+            for (int cf = 0; cf < CF; ++cf) a[cf] = s_w[((wc * CF + cf) * NTAP + t) * 64 + col * 4 + (grp ^ qswz(col))];
 #pragma unroll
             for (int pf = 0; pf < PF; ++pf) {
-                const int hy = (wp * PF + pf) * S + ky, hx = col * S + kx;
-                b[pf] = s_halo[hslot(hy, hx) * 4 + grp];
+                const int hy = (wp * PF + pf) * S + ky, hx = col * S + kx, hs = hslot(hy, hx);
+                b[pf] = s_halo[hs * 4 + (grp ^ qswz(hs))];
             }
 #pragma unroll
             for (int cf = 0; cf < CF; ++cf)
@@ -152,7 +162,8 @@ conv_igemm(const ConvParams p) {
         hoff[i] = (u < HALO_U && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W)
                       ? (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + q * VEC
                       : -1;
-        hdst[i] = hslot(hy, hx) * 4 + q;
+        const int hs = hslot(hy, hx);
+        hdst[i] = hs * 4 + (q ^ qswz(hs));
     }
     // One K chunk's halo and weight units into registers. Every load is unconditional, from the
     // unit's address or from a zeroed buffer (padding, channels past cin_g, units past the
@@ -185,7 +196,7 @@ conv_igemm(const ConvParams p) {
 #pragma unroll
         for (int i = 0; i < WN; ++i) {
             const int u = tid + i * NT;
-            if (u < W_U) dst[HALO_U + u] = rw[i];
+            if (u < W_U) dst[HALO_U + (u & ~3) + ((u & 3) ^ qswz(u >> 2))] = rw[i];
         }
     };
 
@@ -292,8 +303,6 @@ conv_igemm(const ConvParams p) {
 // CF x PF accumulators, so that dependent MFMAs are CF x PF instructions apart.
 // ---------------------------------------------------------------------------------------------
 __device__ u32x4 g_zero_units[4];
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <int KH, int KW, int S, bool TR, int WC, int WP, int CF, int PF, int SG>
 __global__ void __launch_bounds__(WC * WP * 64)
@@ -404,7 +413,7 @@ conv_dma_f32(const ConvParams p) {
                 if (ub + lane < HALO_U) {
                     const void* src = (hoff[i] >= 0 && cl0 + qv < p.cin_g) ? (const void*)(xg + hoff[i] + cl0)
                                                                           : (const void*)g_zero_units;
-                    __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)(dst + ub), 16, 0, 0);
+                    lds_dma16(src, dst + ub);
                 }
             }
             const u32x4* wsrc = (const u32x4*)(wg + ((long long)(g * p.nchunks + chunk) * p.nblk_g + nb0) *
@@ -414,8 +423,7 @@ conv_dma_f32(const ConvParams p) {
                 const int ub = wave * 64 + i * NT;
                 if (ub >= W_U) break;
                 if (ub + lane < W_U)
-                    __builtin_amdgcn_global_load_lds((const void*)(wsrc + ub + lane), (lds_ptr_t)(dst + HALO_U + ub),
-                                                     16, 0, 0);
+                    lds_dma16(wsrc + ub + lane, dst + HALO_U + ub);
             }
         }
     };
@@ -626,7 +634,7 @@ conv_tr_merged(const ConvParams p) {
             if (ub + lane < HALO_U) {
                 const void* src = (hoff[i] >= 0 && cl0 + qv < cin_g) ? (const void*)(xg + hoff[i] + cl0)
                                                                       : (const void*)g_zero_units;
-                __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)(dst + ub), 16, 0, 0);
+                lds_dma16(src, dst + ub);
             }
         }
         const u32x4* wsrc = wg + chunk * wchunk;
@@ -635,8 +643,7 @@ conv_tr_merged(const ConvParams p) {
             const int ub = wave * 64 + i * NT;
             if (ub >= W_U) break;
             if (ub + lane < W_U)
-                __builtin_amdgcn_global_load_lds((const void*)(wsrc + ub + lane), (lds_ptr_t)(dst + HALO_U + ub), 16,
-                                                 0, 0);
+                lds_dma16(wsrc + ub + lane, dst + HALO_U + ub);
         }
     };
 
@@ -892,8 +899,6 @@ k_convT_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
 // (ky, kx) order), so the results are identical to it bit for bit.
 __device__ u32x4 g_zero_unitsT[4];  // 64 zero bytes: the source of halo pixels off the map
 
-typedef __attribute__((address_space(3))) void* lds_addr_t_t;
-
 template <typename T>
 __device__ __forceinline__ void unpack16(u32x4 u, float (&v)[16 / sizeof(T)]) {
     if constexpr (sizeof(T) == 4) {
@@ -954,7 +959,7 @@ k_convT3_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
             if (ub >= HALO_U) break;
             if (ub + lane < HALO_U) {
                 const void* src = hoff[i] >= 0 ? (const void*)(xg + hoff[i] + c0) : (const void*)g_zero_unitsT;
-                __builtin_amdgcn_global_load_lds(src, (lds_addr_t_t)(s_halo + buf * HALO_U + ub), 16, 0, 0);
+                lds_dma16(src, s_halo + buf * HALO_U + ub);
             }
         }
     };
@@ -1075,7 +1080,7 @@ k_convT3_mfma(const ConvParams p, const u32x4* __restrict__ wm) {
         const void* src = (U < HALO_U && iy < p.H && ix < p.W)
                               ? (const void*)(xg + (long long)iy * p.x.row + (long long)ix * p.x.cs + (slot ^ swz(pix)) * 8)
                               : (const void*)g_zero_unitsT;
-        if (U < HALO_U) __builtin_amdgcn_global_load_lds(src, (lds_addr_t_t)(s_halo + ub), 16, 0, 0);
+        if (U < HALO_U) lds_dma16(src, s_halo + ub);
     }
     u32x4 wa[WF];
 #pragma unroll

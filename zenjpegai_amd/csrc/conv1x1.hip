@@ -29,8 +29,6 @@
 
 namespace zjai {
 
-typedef __attribute__((address_space(3))) void* lds_addr_1x1_t;
-
 __device__ u32x4 g_zero_units1x1[4];  // 64 zero bytes: the source of positions past the map
 
 // s_waitcnt with vmcnt(n) (expcnt and lgkmcnt not waited for): gfx9 keeps vmcnt's low four
@@ -118,13 +116,12 @@ conv1x1_ring(const ConvParams p) {
 #pragma unroll
         for (int i = 0; i < BN; ++i) {
             const void* src = boff[i] >= 0 ? (const void*)(xg + boff[i] + c0) : (const void*)g_zero_units1x1;
-            __builtin_amdgcn_global_load_lds(src, (lds_addr_1x1_t)(dst + wave * 64 + i * NT), 16, 0, 0);
+            lds_dma16(src, dst + wave * 64 + i * NT);
         }
 #pragma unroll
         for (int i = 0; i < AN; ++i) {
             const int u = wave * 64 + i * NT;
-            __builtin_amdgcn_global_load_lds((const void*)(wg + c * wchunk + u + lane),
-                                             (lds_addr_1x1_t)(dst + B_U + u), 16, 0, 0);
+            lds_dma16(wg + c * wchunk + u + lane, dst + B_U + u);
         }
     };
 

@@ -25,8 +25,6 @@
 
 namespace zjai {
 
-typedef __attribute__((address_space(3))) void* lds_addr_t;
-
 __device__ u32x4 g_zero_units32[4];  // 64 zero bytes: the source of padding units
 
 template <typename T, int MT, int TW, int S>
@@ -101,7 +99,7 @@ conv3x3_m32(const ConvParams p) {
             const void* src = (iy >= 0 && iy < p.H && ix >= 0 && ix < p.W)
                                   ? (const void*)(xg + (long long)iy * p.x.row + (long long)ix * p.x.cs + cu * 8)
                                   : (const void*)g_zero_units32;
-            __builtin_amdgcn_global_load_lds(src, (lds_addr_t)(s_halo + ub), 16, 0, 0);
+            lds_dma16(src, s_halo + ub);
         }
     }
     auto issue_w = [&](int chunk, int buf) __attribute__((always_inline)) {
@@ -112,7 +110,7 @@ conv3x3_m32(const ConvParams p) {
             const int ub = wave * 64 + i * NT;
             if (ub >= W_U) break;
             if (ub + lane < W_U)
-                __builtin_amdgcn_global_load_lds((const void*)(wsrc + ub + lane), (lds_addr_t)(dst + ub), 16, 0, 0);
+                lds_dma16(wsrc + ub + lane, dst + ub);
         }
     };
 

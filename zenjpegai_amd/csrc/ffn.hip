@@ -65,6 +65,21 @@ __device__ __forceinline__ void unpack2(unsigned v, float (&o)[2]) {
     o[1] = (float)hv[1];
 }
 
+// Unit swizzle of a p-slice row in k_ffn (a position's 64 channels = 8 16-byte units; unit q
+// sits at q ^ pswz(column), column = position % 16). gfx950 serves a ds_read_b32 in two passes
+// of 32 lanes over 32 banks (128 bytes): the 32 lanes of a pass are two neighbouring columns'
+// 16 lanes, each reading 64 bytes (one half) of its 128-byte row, so bit 2 of the swizzle -- the
+// half the column's 64 bytes land in -- is the column's parity. Over 16 columns the swizzle
+// takes every value twice: the project_in stores (ds_write_b64, 16 lanes per pass) stay at the
+// two passes a fixed 8-byte half needs.
+__device__ __forceinline__ int pswz(int c) { return ((c & 1) << 2) | ((c >> 1) & 3); }
+
+// Unit swizzle of the rows of 4 16-byte units that one 16x16x32 fragment read takes 16 of
+// (g and W_out in k_ffn): unit q of row r at q ^ gswz(r). A ds_read_b128 runs in four passes of
+// 16 lanes (lane l in pass (l / 32, parity of bits 2..4 of l)) over 64 banks; flipping bit 1
+// of the unit in rows with bit 2 set puts each pass's 16 rows on distinct bank quads.
+__device__ __forceinline__ int gswz(int r) { return (r & 4) >> 1; }
+
 // u rows (halo positions, DIM channels of the storage type, UPR = DIM / 8 16-byte units): unit
 // q of row r sits at q ^ ukey(r), so that the 16 rows one half-wave reads for an MFMA fragment
 // cover all 16 four-bank groups.
@@ -226,7 +241,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
             const int u = tid + i * FTHREADS, r = u / UPR, q = u % UPR;
             s_win[r * UPR + (q ^ key(r))] = rwi[i];
         }
-        if (tid < WO_U) s_wo[(s & 1) * WO_U + tid] = rwo;
+        if (tid < WO_U) s_wo[(s & 1) * WO_U + (tid & ~3) + ((tid & 3) ^ gswz(tid >> 2))] = rwo;
         if (tid < X_U) s_x[(s & 1) * X_U + tid] = rx;
     };
 
@@ -292,7 +307,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
             const int pos = (pb1 * 4 + i) * 16 + col;
             const int iy = y0 - 1 + pos / FH, ix = x0 - 1 + pos % FH;
             const bool inside = iy >= 0 && iy < p.h && ix >= 0 && ix < p.w;
-            const int sw = pos & 7;  // unit swizzle of the position's row (see the dw reads)
+            const int sw = pswz(pos & (FH - 1));  // unit swizzle of the position's row (see the dw reads)
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 typedef T t4 __attribute__((ext_vector_type(4)));
@@ -323,16 +338,15 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
                 }
             }
             // 16-byte unit (pg / 4) of the first half, 4 + pg / 4 of the second, each XORed with
-            // pos & 7: the 16 lanes of a position read four units of its row, and the phase-a stores
-            // of 16 positions spread over all banks (measured faster than a swizzle that also keeps
-            // the reads of four neighbouring positions on disjoint banks, which spills registers).
-            // The swizzle pos & 7 of halo position (hr, dc + kx) is (dc + kx) & 7 (FH is a
-            // multiple of 8), so each read is a per-kx offset plus hr rows.
-            static_assert(FH % 8 == 0, "row swizzle");
+            // pswz(column): the 16 lanes of a position read four units of its row, and the two
+            // neighbouring positions of one read pass sit on disjoint banks. The swizzle of halo
+            // position (hr, dc + kx) depends on its column dc + kx only (FH = 16), so each read is
+            // a per-kx offset plus hr rows.
+            static_assert(FH == 16, "row swizzle");
             int offa[3], offb[3];
 #pragma unroll
             for (int kx = 0; kx < 3; ++kx) {
-                const int c = dc + kx, sw = c & 7;
+                const int c = dc + kx, sw = pswz(c);
                 offa[kx] = c * 64 + 2 * (pg & 3) + ((pg >> 2) ^ sw) * 8;
                 offb[kx] = c * 64 + 2 * (pg & 3) + ((4 + (pg >> 2)) ^ sw) * 8;
             }
@@ -367,7 +381,9 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
                     g[k] = elu_fast16(a) * bq;
                 }
                 typedef T t2 __attribute__((ext_vector_type(2)));
-                *reinterpret_cast<t2*>((T*)s_g + (oy * FT + dc) * 32 + 2 * pg) = t2{(T)g[0], (T)g[1]};
+                const int gp = oy * FT + dc;  // g row; its unit pg / 4 swizzled by gswz
+                *reinterpret_cast<t2*>((T*)s_g + gp * 32 + ((pg >> 2) ^ gswz(gp)) * 8 + 2 * (pg & 3)) =
+                    t2{(T)g[0], (T)g[1]};
 #pragma unroll
                 for (int kx = 0; kx < 3; ++kx)
 #pragma unroll
@@ -383,11 +399,11 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn(const FfnArgs p) {
     // Phase c of slice s: y += W_out(s) x g.
     auto phase_c = [&](int s) __attribute__((always_inline)) {
         // c. y += W_out(s) x g (output-channel block cb2, position blocks pw2 + WPC * i).
-        const u32x4 a = s_wo[(s & 1) * WO_U + (cb2 * 16 + col) * 4 + grp];
+        const u32x4 a = s_wo[(s & 1) * WO_U + (cb2 * 16 + col) * 4 + (grp ^ gswz(col))];
 #pragma unroll
         for (int i = 0; i < NPB; ++i) {
             const int pb = pw2 + WPC * i;
-            if (pb < FPB) Mma16<T>::run(acc2[i], a, s_g[(pb * 16 + col) * 4 + grp]);
+            if (pb < FPB) Mma16<T>::run(acc2[i], a, s_g[(pb * 16 + col) * 4 + (grp ^ gswz(col))]);
         }
     };
 
@@ -657,18 +673,11 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 __device__ u32x4 g_zero_ffn32[8];  // 128 zero bytes: the source of absent biases
 
-typedef __attribute__((address_space(3))) void* lds_addr_ffn_t;
-
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited for); gfx9 splits vmcnt over [3:0] and [15:14].
 template <int N>
 __device__ __forceinline__ void ffn_wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt");
     __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-
-// 16 bytes per lane from global memory to LDS (lane i lands at dst + 16 i; dst wave-uniform).
-__device__ __forceinline__ void ffn_dma(const void* src, u32x4* dst) {
-    __builtin_amdgcn_global_load_lds(src, (lds_addr_ffn_t)dst, 16, 0, 0);
 }
 
 // LayerNorm of this wave's halo positions into B fragments: u[i][c] holds channels
@@ -807,14 +816,14 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
         for (int j = 0; j < WIN_W; ++j) {
             const int blk = wave + 8 * j, c = blk >> 2, cb = blk & 3;
             const int gb = cb < 2 ? 2 * s + cb : HID / 16 + 2 * s + (cb - 2);
-            ffn_dma(w_in + ((long long)c * p.nblk_in + gb) * 64 + lane, s_win + blk * 64);
+            lds_dma16(w_in + ((long long)c * p.nblk_in + gb) * 64 + lane, s_win + blk * 64);
         }
     };
     auto issue_wout = [&](int s) {  // K chunks 2 s, 2 s + 1: 2 CB2 contiguous KB
 #pragma unroll
         for (int j = 0; j < WO_W; ++j) {
             const int blk = wave + 8 * j;
-            ffn_dma(w_out + ((long long)2 * s * p.nblk_out + blk) * 64 + lane, s_wo + blk * 64);
+            lds_dma16(w_out + ((long long)2 * s * p.nblk_out + blk) * 64 + lane, s_wo + blk * 64);
         }
     };
     // Unit u of X (176): run u / 8 of 32 floats; runs 0-1 b_in, 2-19 tap (run - 2) / 2, 20-21 the
@@ -829,7 +838,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
                 if (run < 2) src = p.b_in ? (const void*)(p.b_in + ch) : (const void*)(g_zero_ffn32 + q);
                 else if (run < 20) src = p.dw_w + ((run - 2) >> 1) * C2 + ch;
                 else src = p.dw_b ? (const void*)(p.dw_b + ch) : (const void*)(g_zero_ffn32 + q);
-                ffn_dma(src, s_x + buf * X_U + wave * 64);
+                lds_dma16(src, s_x + buf * X_U + wave * 64);
             }
         }
     };
@@ -1012,7 +1021,7 @@ __global__ void __launch_bounds__(FTHREADS) k_qkv_f32(const QkvArgs p) {
 #pragma unroll
         for (int j = 0; j < W1_W; ++j) {
             const int blk = wave + 8 * j, c = blk >> 2, cb = blk & 3;
-            ffn_dma(w1 + ((long long)c * p.nblk1 + 4 * s + cb) * 64 + lane, s_w1 + blk * 64);
+            lds_dma16(w1 + ((long long)c * p.nblk1 + 4 * s + cb) * 64 + lane, s_w1 + blk * 64);
         }
     };
     // Unit u of slice s's X (176): run u / 16 of 64 floats; run 0 b1, 1-9 tap run - 1, 10 the
@@ -1027,7 +1036,7 @@ __global__ void __launch_bounds__(FTHREADS) k_qkv_f32(const QkvArgs p) {
             if (run == 0) src = p.b1 ? (const void*)(p.b1 + ch) : (const void*)(g_zero_ffn32 + (q & 7));
             else if (run < 10) src = p.dw_w + (run - 1) * C3 + ch;
             else src = p.dw_b ? (const void*)(p.dw_b + ch) : (const void*)(g_zero_ffn32 + (q & 7));
-            ffn_dma(src, s_x + j * 64);
+            lds_dma16(src, s_x + j * 64);
         }
     }
     issue_w1(0);

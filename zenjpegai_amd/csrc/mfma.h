@@ -53,6 +53,22 @@ template <> struct Mma32<__bf16> {
     }
 };
 
+// Direct global -> LDS load of 16 bytes per lane (global_load_lds_dwordx4): lane i's bytes land
+// at wave_dst + 16 i (wave_dst is the wave's base; its value in lane 0 is used). Written as
+// inline assembly because the compiler counts its own form of this load as LDS work still in
+// flight and then waits for every outstanding LDS read (lgkmcnt(0)) wherever a kernel first uses
+// the result of any one of them, which serialises the fragment reads a tap loop issues ahead of
+// its MFMAs; hidden from it, each use waits only for the reads it needs. The compiler does not
+// count these loads in its own vmcnt waits either: the caller waits for them (s_waitcnt
+// vmcnt(0), then the barrier that publishes the LDS data) before any wave reads the bytes.
+// (The s_nop is the wait state a write of M0 needs before an LDS DMA instruction reads it.)
+__device__ __forceinline__ void lds_dma16(const void* src, void* wave_dst) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(
+        (unsigned)(size_t)(__attribute__((address_space(3))) void*)wave_dst);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0)
+                 : "memory", "m0");
+}
+
 // clamp(v, 0, 6) on a 16-byte vector of the storage type (ResAU's relu6 on load).
 template <typename T> __device__ __forceinline__ u32x4 relu6_vec(u32x4 v);
 template <> __device__ __forceinline__ u32x4 relu6_vec<float>(u32x4 v) {
