@@ -747,8 +747,9 @@ __device__ __forceinline__ void ln_frags_f32(const float* xb, const View& xv, in
     }
 }
 
-// acc[cb][i] = bias + W (64 rows: four 16-row blocks in LDS as [chunk][block][16][4 units]) x u
-// for this wave's two position blocks, the 1x1's f32 instruction sequence.
+// acc[cb][i] = bias + W (64 rows: four 16-row blocks in LDS as [chunk][block][16][4 units], unit q
+// of row r at q ^ gswz(r)) x u for this wave's two position blocks, the 1x1's f32 instruction
+// sequence.
 template <int NCH>
 __device__ __forceinline__ void slice_gemm_f32(const u32x4* s_w, const float* bias64, const f32x4 (&u)[2][NCH],
                                                int col, int grp, f32x4 (&acc)[4][2]) {
@@ -765,7 +766,7 @@ __device__ __forceinline__ void slice_gemm_f32(const u32x4* s_w, const float* bi
         __builtin_amdgcn_sched_barrier(0);
         f32x4 a[4];
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) a[cb] = __builtin_bit_cast(f32x4, s_w[(c * 4 + cb) * 64 + col * 4 + grp]);
+        for (int cb = 0; cb < 4; ++cb) a[cb] = __builtin_bit_cast(f32x4, s_w[(c * 4 + cb) * 64 + col * 4 + (grp ^ gswz(col))]);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
 #pragma unroll
@@ -780,8 +781,11 @@ __device__ __forceinline__ void slice_gemm_f32(const u32x4* s_w, const float* bi
 
 // Feed-forward, f32: as k_ffn, slices of 32 gate pairs (64 p channels). LDS: W_in slice
 // [chunk][4 blocks][16][4] (32 KB at dim 128), p [256 positions][64] (a and b halves swapped on
-// odd positions), g [208 positions][32] (16-byte units XOR-swizzled by position pair), W_out
-// slice [2 chunks][dim / 16 blocks][16][4], and per slice b_in, the depthwise taps and biases.
+// odd positions, 16-byte units XORed with pos & 7 so that the project_in stores of 8
+// neighbouring positions -- one 8-lane ds_write_b128 pass over 128 bytes of banks -- are
+// conflict-free), g [208 positions][32] (units XORed with 2 ((pos >> 1) & 3): conflict-free
+// fragment reads), W_out slice [2 chunks][dim / 16 blocks][16][4], and per slice b_in, the
+// depthwise taps and biases. The weight rows take gswz.
 template <int DIM>
 __global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
     constexpr int HID = 4 * DIM, C2 = 2 * HID, NS = HID / 32, NCH = DIM / 16;
@@ -816,14 +820,14 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
         for (int j = 0; j < WIN_W; ++j) {
             const int blk = wave + 8 * j, c = blk >> 2, cb = blk & 3;
             const int gb = cb < 2 ? 2 * s + cb : HID / 16 + 2 * s + (cb - 2);
-            lds_dma16(w_in + ((long long)c * p.nblk_in + gb) * 64 + lane, s_win + blk * 64);
+            lds_dma16(w_in + ((long long)c * p.nblk_in + gb) * 64 + (lane ^ gswz(lane >> 2)), s_win + blk * 64);
         }
     };
     auto issue_wout = [&](int s) {  // K chunks 2 s, 2 s + 1: 2 CB2 contiguous KB
 #pragma unroll
         for (int j = 0; j < WO_W; ++j) {
             const int blk = wave + 8 * j;
-            lds_dma16(w_out + ((long long)2 * s * p.nblk_out + blk) * 64 + lane, s_wo + blk * 64);
+            lds_dma16(w_out + ((long long)2 * s * p.nblk_out + blk) * 64 + (lane ^ gswz(lane >> 2)), s_wo + blk * 64);
         }
     };
     // Unit u of X (176): run u / 8 of 32 floats; runs 0-1 b_in, 2-19 tap (run - 2) / 2, 20-21 the
@@ -880,7 +884,8 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
                 for (int cb = 0; cb < 4; ++cb) {
                     const int half = (cb >> 1) ^ (col & 1);  // pos & 1 == col & 1
                     const f32x4 v = inside ? acc1[cb][i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    *(f32x4*)(s_p + pos * 64 + half * 32 + (cb & 1) * 16 + 4 * grp) = v;
+                    const int unit = (half * 8 + (cb & 1) * 4 + grp) ^ (col & 7);  // pos & 7 == col & 7
+                    *(f32x4*)(s_p + pos * 64 + unit * 4) = v;
                 }
             }
         }
@@ -897,16 +902,17 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
                 wb[tp] = dww[tp * 64 + 32 + pg];
             }
             // p row of halo position (hr, dc + kx): hr * FH + dc + kx, its two 32-channel halves
-            // swapped on odd positions. FH is even, so the swap depends on dc + kx only and each
-            // read is a fixed per-kx offset plus hr rows (immediate offsets once the rows unroll).
+            // swapped on odd positions and its 16-byte units XORed with pos & 7. FH = 16, so both
+            // depend on dc + kx only and each read is a fixed per-kx offset plus hr rows
+            // (immediate offsets once the rows unroll).
             int offa[3], offb[3];
 #pragma unroll
             for (int kx = 0; kx < 3; ++kx) {
-                const int c = dc + kx, odd = c & 1;
-                offa[kx] = c * 64 + odd * 32 + pg;
-                offb[kx] = c * 64 + (odd ^ 1) * 32 + pg;
+                const int c = dc + kx, odd = c & 1, sw = c & 7;
+                offa[kx] = c * 64 + ((odd * 8 + (pg >> 2)) ^ sw) * 4 + (pg & 3);
+                offb[kx] = c * 64 + (((odd ^ 1) * 8 + (pg >> 2)) ^ sw) * 4 + (pg & 3);
             }
-            static_assert(FH % 2 == 0, "row parity");
+            static_assert(FH == 16, "row swizzle");
             auto ld = [&](int hr, int kx, float& oa, float& ob) {
                 oa = s_p[hr * (FH * 64) + offa[kx]];
                 ob = s_p[hr * (FH * 64) + offb[kx]];
@@ -932,7 +938,7 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
                 const float e = cephes_exp(a) - 1.0f;
                 const float elu = a > 0.0f ? a : e;
                 const int o = oy * FT + dc;
-                s_g[o * 32 + (((pg >> 2) ^ (((o >> 1) & 1) << 2)) << 2) + (pg & 3)] = elu * bq;
+                s_g[o * 32 + (((pg >> 2) ^ (((o >> 1) & 3) << 1)) << 2) + (pg & 3)] = elu * bq;
 #pragma unroll
                 for (int kx = 0; kx < 3; ++kx) {
                     xa[0][kx] = xa[1][kx];
@@ -952,9 +958,9 @@ __global__ void __launch_bounds__(FTHREADS) k_ffn_f32(const FfnArgs p) {
         // c. y += W_out(s) x g: K chunks 2 s, 2 s + 1 (channel 16 cc + 4 grp + k of the slice).
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-            const f32x4 a = __builtin_bit_cast(f32x4, s_wo[(cc * CB2 + cb2) * 64 + col * 4 + grp]);
-            // The g swizzle depends on bit 1 of the position, i.e. of col: one base address.
-            const float* gq = s_g + (pw2 * 16 + col) * 32 + (((cc * 4 + grp) ^ (((col >> 1) & 1) << 2)) << 2);
+            const f32x4 a = __builtin_bit_cast(f32x4, s_wo[(cc * CB2 + cb2) * 64 + col * 4 + (grp ^ gswz(col))]);
+            // The g swizzle depends on bits 1-2 of the position, i.e. of col: one base address.
+            const float* gq = s_g + (pw2 * 16 + col) * 32 + (((cc * 4 + grp) ^ (((col >> 1) & 3) << 1)) << 2);
             // Position blocks in groups of GB (fewer live fragment registers).
             constexpr int GB = 7;
 #pragma unroll
@@ -1021,7 +1027,7 @@ __global__ void __launch_bounds__(FTHREADS) k_qkv_f32(const QkvArgs p) {
 #pragma unroll
         for (int j = 0; j < W1_W; ++j) {
             const int blk = wave + 8 * j, c = blk >> 2, cb = blk & 3;
-            lds_dma16(w1 + ((long long)c * p.nblk1 + 4 * s + cb) * 64 + lane, s_w1 + blk * 64);
+            lds_dma16(w1 + ((long long)c * p.nblk1 + 4 * s + cb) * 64 + (lane ^ gswz(lane >> 2)), s_w1 + blk * 64);
         }
     };
     // Unit u of slice s's X (176): run u / 16 of 64 floats; run 0 b1, 1-9 tap run - 1, 10 the
