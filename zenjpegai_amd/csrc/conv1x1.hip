@@ -9,7 +9,7 @@
 // base + 16 i) through a ring of NS chunk slots, one barrier per chunk, NS - 2 chunks in flight
 // behind the one being consumed. A position's 64 bytes are read by 4 consecutive lanes as one
 // contiguous run; its 4 16-byte slots are XOR-swizzled by the position index so that the
-// fragment reads are free of bank conflicts. The weight blocks are the implicit-GEMM packing
+// fragment reads are free of bank conflicts (as are the weight rows'). The weight blocks are the implicit-GEMM packing
 // ([chunk][16-channel block][16][64 bytes]), one contiguous NB-block run per chunk.
 //
 // Numerics are those of the implicit-GEMM kernels for a 1x1 layer, so the two agree bit for
@@ -94,12 +94,15 @@ conv1x1_ring(const ConvParams p) {
 
     // Element offset of each of this thread's position units (u = tid + i * NT), -1 past the
     // map: unit u = position * 4 + slot holds the position's 16-byte unit slot ^ swz(position),
-    // swz(position) = (position / 4) % 4.
+    // swz(position) = 2 (bit 2 of the position). A fragment read (ds_read_b128, lane (col, grp))
+    // runs in four passes of 16 lanes (lane l in pass (l / 32, parity of bits 2..4 of l)) over
+    // 64 banks; with this swizzle each pass's 16 units sit on distinct bank quads. The weight
+    // rows take the same swizzle (unit q of row r at q ^ swz(r)).
     long long boff[BN];
 #pragma unroll
     for (int i = 0; i < BN; ++i) {
         const int u = tid + i * NT, pos = u >> 2, slot = u & 3;
-        const int q = slot ^ ((pos >> 2) & 3);
+        const int q = slot ^ ((pos & 4) >> 1);
         const int pg = pos0 + pos;
         if (pg < P) {
             const int oy = pg / p.OW, ox = pg - oy * p.OW;
@@ -121,7 +124,8 @@ conv1x1_ring(const ConvParams p) {
 #pragma unroll
         for (int i = 0; i < AN; ++i) {
             const int u = wave * 64 + i * NT;
-            lds_dma16(wg + c * wchunk + u + lane, dst + B_U + u);
+            const int U = u + lane;
+            lds_dma16(wg + c * wchunk + (U ^ ((U >> 3) & 2)), dst + B_U + u);
         }
     };
 
@@ -145,11 +149,11 @@ conv1x1_ring(const ConvParams p) {
         const u32x4* sa = sb + B_U;
         u32x4 av[CF], bv[PF];
 #pragma unroll
-        for (int cf = 0; cf < CF; ++cf) av[cf] = sa[(wc * CF + cf) * 64 + col * 4 + grp];
+        for (int cf = 0; cf < CF; ++cf) av[cf] = sa[(wc * CF + cf) * 64 + col * 4 + (grp ^ ((col & 4) >> 1))];
 #pragma unroll
         for (int pf = 0; pf < PF; ++pf) {
             const int pos = bpos[pf];
-            bv[pf] = sb[pos * 4 + (grp ^ ((pos >> 2) & 3))];
+            bv[pf] = sb[pos * 4 + (grp ^ ((pos & 4) >> 1))];
         }
         if constexpr (sizeof(T) == 4) {
             // k outermost: the four dependent MFMAs of an accumulator are CF x PF apart.
