@@ -544,6 +544,10 @@ conv_dma_f32(const ConvParams p) {
 template <typename T, int N0, int N1, int N2, int N3>
 __global__ void __launch_bounds__(512)
 conv_tr_merged(const ConvParams p) {
+    // 16-bit weights come packed with unit q of each 16-row block's row r at q ^ qswz(r) (the
+    // launcher's merged packing), so the fragment reads are conflict-free; f32 keeps the plain
+    // layout (under the swizzled addressing the compiler renamed this kernel's f32 MFMA chains).
+    auto wswz = [](int r) __attribute__((always_inline)) { return sizeof(T) == 2 ? qswz(r) : 0; };
     constexpr int WC = 2, WP = 4, CF = 2, PF = 4;
     constexpr int NT = WC * WP * 64;
     constexpr int TY = WP * PF;
@@ -663,7 +667,7 @@ conv_tr_merged(const ConvParams p) {
                 const int dy = tdy[ph][t], dx = tdx[ph][t];
                 u32x4 a[CF], b[PF];
 #pragma unroll
-                for (int cf = 0; cf < CF; ++cf) a[cf] = s_w[((wc * CF + cf) * NTALL + e) * 64 + col * 4 + grp];
+                for (int cf = 0; cf < CF; ++cf) a[cf] = s_w[((wc * CF + cf) * NTALL + e) * 64 + col * 4 + (grp ^ wswz(col))];
 #pragma unroll
                 for (int pf = 0; pf < PF; ++pf) {
                     b[pf] = s_halo[((wp * PF + pf + dy) * HX + col + dx) * 4 + grp];

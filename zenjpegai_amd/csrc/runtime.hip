@@ -448,7 +448,16 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
                         const float* src = pk.data() + (size_t)ph * L->phase_stride +
                                            (((size_t)ch * L->nblk_g + nb) * 4 + t) * 16 * CK;
                         float* dst = pm.data() + (((size_t)ch * L->nblk_g + nb) * TR_MERGED_TAPS + e) * 16 * CK;
-                        std::copy(src, src + 16 * CK, dst);
+                        if (dtype != DT_F32) {
+                            // 16-bit: 16-byte unit q of row r at q ^ 2 (bit 2 of r), the layout
+                            // conv_tr_merged's fragment reads expect (conflict-free ds_read_b128).
+                            for (int r = 0; r < 16; ++r)
+                                for (int q = 0; q < 4; ++q)
+                                    std::copy(src + r * CK + q * (CK / 4), src + r * CK + (q + 1) * (CK / 4),
+                                              dst + r * CK + (q ^ ((r & 4) >> 1)) * (CK / 4));
+                        } else {
+                            std::copy(src, src + 16 * CK, dst);
+                        }
                     }
             }
         L->wpk_m = upload_as(ctx, pm, dtype, &L->wpk_m_bytes);
