@@ -383,19 +383,22 @@ conv_dma_f32(const ConvParams p) {
     const T* wg = (const T*)p.w + phase * p.phase_stride + (long long)bi * p.w_bstride;
     const long long xbase = (long long)p.x.c_off + (long long)g * p.cin_g;
 
-    // Halo element offset of each of this thread's units (u = tid + i * NT), -1 in the padding.
-    // NT is a multiple of 4, so every unit of a thread holds the same channel quad.
+    // Halo element offset of each of this thread's units (u = tid + i * NT), -1 in the padding,
+    // and the first channel of the quad it holds. Stride 2: unit q of halo pixel s holds channel
+    // quad q ^ qswz(s); a fragment then reads every other pixel with two lanes per bank quad in
+    // each ds_read_b128 pass instead of four. Stride 1 keeps the plain layout.
     long long hoff[HN];
+    int hqv[HN];
 #pragma unroll
     for (int i = 0; i < HN; ++i) {
         const int u = tid + i * NT, pix = u >> 2, q = u & 3;
         const int hy = pix / HX, hx = pix - hy * HX;
         const int iy = iy0 + hy, ix = ix0 + hx;
+        hqv[i] = (S == 2 ? (q ^ qswz(pix)) : q) * VEC;
         hoff[i] = (u < HALO_U && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W)
-                      ? (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + q * VEC
+                      ? (long long)iy * p.x.row + (long long)ix * p.x.cs + xbase + hqv[i]
                       : -1;
     }
-    const int qv = (tid & 3) * VEC;
 
     // Direct LDS loads of stage st into buffer buf. Each wave covers whole 64-unit rows of the
     // chunk's layout; its M0 base is the row start, lanes past the end are masked off.
@@ -411,8 +414,8 @@ conv_dma_f32(const ConvParams p) {
                 const int ub = wave * 64 + i * NT;
                 if (ub >= HALO_U) break;
                 if (ub + lane < HALO_U) {
-                    const void* src = (hoff[i] >= 0 && cl0 + qv < p.cin_g) ? (const void*)(xg + hoff[i] + cl0)
-                                                                          : (const void*)g_zero_units;
+                    const void* src = (hoff[i] >= 0 && cl0 + hqv[i] < p.cin_g) ? (const void*)(xg + hoff[i] + cl0)
+                                                                              : (const void*)g_zero_units;
                     lds_dma16(src, dst + ub);
                 }
             }
@@ -448,8 +451,8 @@ conv_dma_f32(const ConvParams p) {
                     for (int cf = 0; cf < CF; ++cf) a[cf] = s_w[((wc * CF + cf) * NTAP + t) * 64 + col * 4 + grp];
 #pragma unroll
                     for (int pf = 0; pf < PF; ++pf) {
-                        const int hy = (wp * PF + pf) * S + ky, hx = col * S + kx;
-                        b[pf] = s_halo[(hy * HX + hx) * 4 + grp];
+                        const int hy = (wp * PF + pf) * S + ky, hx = col * S + kx, hs = hy * HX + hx;
+                        b[pf] = s_halo[hs * 4 + (S == 2 ? (grp ^ qswz(hs)) : grp)];
                         if constexpr (decltype(relu6)::value) b[pf] = relu6_vec<T>(b[pf]);
                     }
 #pragma unroll
