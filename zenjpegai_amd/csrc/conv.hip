@@ -1043,18 +1043,22 @@ k_convT3_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
 // COUTP rows (row R = phase * COUTP + output; a phase's weight for a neighbour it does not read
 // is zero), N = positions. 16x16x32 MFMAs with the weights as A (MB 16-row blocks, packed
 // [CIN / 32][4][MB][16][32], held in registers) and the halo as B. A workgroup (4 waves) takes
-// 8 x 32 positions and stages its whole 9 x 33-pixel input halo, every channel, in one round
-// trip (direct LDS loads of whole 128- or 256-byte pixels, 16-byte slots XORed by pixel so that a
+// 8 x TX positions (TX = 32, or 16 for 128 input channels: a 39 KB halo, four workgroups per CU
+// instead of two, so more halo loads fly while other workgroups compute) and stages its whole
+// 9 x (TX + 1)-pixel input halo, every channel, in one round trip (direct LDS loads of whole 128- or 256-byte pixels, 16-byte slots XORed by pixel so that a
 // fragment's 16 pixels spread over the banks): the layer is one HBM read of its input, and its
 // 9 FMAs per input channel and output on the vector ALUs become one fragment read per 32
 // channels. Products of 16-bit operands are exact in f32, so the result differs from the vector
 // kernel's (input channel, tap) FMA chain by the summation order only, before the final rounding
 // to the storage type.
-template <typename T, int COUTP, int CIN>
+template <typename T, int COUTP, int CIN, int TX>
 __global__ void __launch_bounds__(256)
 k_convT3_mfma(const ConvParams p, const u32x4* __restrict__ wm) {
     constexpr int MB = (4 * COUTP + 15) / 16;  // 16-row blocks of (phase, output) rows
-    constexpr int TY = 8, TX = 32, HX = TX + 1, HY = TY + 1, HPIX = HX * HY;
+    constexpr int TY = 8, HX = TX + 1, HY = TY + 1, HPIX = HX * HY;
+    constexpr int NJ = TX / 8;                 // 16-position blocks per wave (two tile rows)
+    constexpr int BR = TX / 16;                // blocks per tile row
+    static_assert(TX == 16 || TX == 32, "tile width");
     constexpr int SL = CIN / 8;                // 16-byte slots per pixel
     constexpr int HALO_U = HPIX * SL;
     constexpr int HN = (HALO_U + 255) / 256;
@@ -1093,8 +1097,8 @@ k_convT3_mfma(const ConvParams p, const u32x4* __restrict__ wm) {
 #pragma unroll
     for (int f = 0; f < WF; ++f) wa[f] = wm[((long long)f * 16 + col) * 4 + grp];
 
-    // Wave w: position blocks j = 0..3 = tile row 2 w + j / 2, columns 16 (j % 2) .. + 15.
-    f32x4 acc[MB][4];
+    // Wave w: position blocks j < NJ = tile row 2 w + j / BR, columns 16 (j % BR) .. + 15.
+    f32x4 acc[MB][NJ];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
         f32x4 bv;
@@ -1104,7 +1108,7 @@ k_convT3_mfma(const ConvParams p, const u32x4* __restrict__ wm) {
             bv[r] = (ph < 4 && p.bias && oc < p.cout_g) ? p.bias[oc] : 0.0f;
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[mb][j] = bv;
+        for (int j = 0; j < NJ; ++j) acc[mb][j] = bv;
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's halo loads are in LDS
     __syncthreads();                     // ... and every other wave's
@@ -1113,45 +1117,52 @@ k_convT3_mfma(const ConvParams p, const u32x4* __restrict__ wm) {
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
             const int a = n >> 1, b = n & 1, slot = kc * 4 + grp;
-            u32x4 bv[4];
+            u32x4 bv[NJ];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int pix = (2 * wave + (j >> 1) + a) * HX + 16 * (j & 1) + col + b;
+            for (int j = 0; j < NJ; ++j) {
+                const int pix = (2 * wave + j / BR + a) * HX + 16 * (j % BR) + col + b;
                 bv[j] = s_halo[pix * SL + (slot ^ swz(pix))];
                 if (p.relu6_in) bv[j] = relu6_vec<T>(bv[j]);
             }
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) Mma16<T>::run(acc[mb][j], wa[(kc * 4 + n) * MB + mb], bv[j]);
+                for (int j = 0; j < NJ; ++j) Mma16<T>::run(acc[mb][j], wa[(kc * 4 + n) * MB + mb], bv[j]);
         }
 
     // Row R = 16 mb + 4 grp + r of column col: phase R / COUTP, output R % COUTP.
     if constexpr (COUTP == 1) {
         // Only the lanes of K group 0 hold real rows (the four phases of their position). Lane
-        // (col, g) takes position block g's four phases from lane col, so that every lane stores
-        // four outputs instead of a quarter of the lanes storing sixteen.
-        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        // (col, g) takes NJ of them from lane col -- position block jb = g NJ / 4, phases
+        // r0 = g NJ % 4 .. r0 + NJ - 1 -- so that every lane stores NJ outputs instead of a
+        // quarter of the lanes storing 4 NJ.
+        const int jb = (grp * NJ) >> 2, r0 = (grp * NJ) & 3;
+        float v[NJ];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int k = 0; k < NJ; ++k) v[k] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float t = __shfl(acc[0][j][r], col);
-                if (grp == j) v[r] = t;
-            }
-        const int yq = y0 + 2 * wave + (grp >> 1), xq = x0 + 16 * (grp & 1) + col;
 #pragma unroll
-        for (int ph = 0; ph < 4; ++ph) {
+                for (int k = 0; k < NJ; ++k)
+                    if (jb == j && r0 + k == r) v[k] = t;
+            }
+        const int yq = y0 + 2 * wave + jb / BR, xq = x0 + 16 * (jb % BR) + col;
+#pragma unroll
+        for (int k = 0; k < NJ; ++k) {
+            const int ph = r0 + k;
             const int oy = 2 * yq + (ph >> 1), ox = 2 * xq + (ph & 1);
-            if (oy < p.OH && ox < p.OW) epilogue_store<T>(p, bi, oy, ox, 0, 1, f32x4{v[ph], 0.0f, 0.0f, 0.0f});
+            if (oy < p.OH && ox < p.OW) epilogue_store<T>(p, bi, oy, ox, 0, 1, f32x4{v[k], 0.0f, 0.0f, 0.0f});
         }
         return;
     }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int yq = y0 + 2 * wave + (j >> 1), xq = x0 + 16 * (j & 1) + col;
+        for (int j = 0; j < NJ; ++j) {
+            const int yq = y0 + 2 * wave + j / BR, xq = x0 + 16 * (j % BR) + col;
             if constexpr (COUTP >= 4) {
                 // The lane's four rows are four consecutive outputs of one phase.
                 const int R0 = 16 * mb + 4 * grp, ph = R0 / COUTP, oc0 = R0 % COUTP;
@@ -1213,16 +1224,17 @@ bool convT_mfma_k3(int dtype, const ConvParams& p, int cin) {
 
 template <typename T, int CIN>
 static hipError_t go_mfma3(int coutp, const ConvParams& p, const void* wm, hipStream_t s) {
+    constexpr int TX = CIN == 128 ? 16 : 32;
     const int gw = (p.OW + 1) / 2, gh = (p.OH + 1) / 2;
-    const long long blocks = ((long long)((gw + 31) / 32) * ((gh + 7) / 8) * p.N + 7) / 8 * 8;
+    const long long blocks = ((long long)((gw + TX - 1) / TX) * ((gh + 7) / 8) * p.N + 7) / 8 * 8;
     if (blocks <= 0 || blocks > (1ll << 30) || p.N < 1 || p.N > MAXB) return hipErrorInvalidValue;
     const dim3 g((unsigned)blocks);
     const u32x4* w = (const u32x4*)wm;
     switch (coutp) {
-        case 1: hipLaunchKernelGGL((k_convT3_mfma<T, 1, CIN>), g, dim3(256), 0, s, p, w); break;
-        case 2: hipLaunchKernelGGL((k_convT3_mfma<T, 2, CIN>), g, dim3(256), 0, s, p, w); break;
-        case 4: hipLaunchKernelGGL((k_convT3_mfma<T, 4, CIN>), g, dim3(256), 0, s, p, w); break;
-        case 8: hipLaunchKernelGGL((k_convT3_mfma<T, 8, CIN>), g, dim3(256), 0, s, p, w); break;
+        case 1: hipLaunchKernelGGL((k_convT3_mfma<T, 1, CIN, TX>), g, dim3(256), 0, s, p, w); break;
+        case 2: hipLaunchKernelGGL((k_convT3_mfma<T, 2, CIN, TX>), g, dim3(256), 0, s, p, w); break;
+        case 4: hipLaunchKernelGGL((k_convT3_mfma<T, 4, CIN, TX>), g, dim3(256), 0, s, p, w); break;
+        case 8: hipLaunchKernelGGL((k_convT3_mfma<T, 8, CIN, TX>), g, dim3(256), 0, s, p, w); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
