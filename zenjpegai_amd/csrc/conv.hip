@@ -894,12 +894,12 @@ k_convT_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
 // The same layer for the 3x3 kernel with padding 1 (the synthesis nets' conv3x3_t): its taps
 // are fixed, phase (py, px) reading input (y' + a, x' + b) for a <= py, b <= px, so a position
 // needs only the 2 x 2 input neighbourhood (y', x') .. (y' + 1, x' + 1). A workgroup of 256
-// threads takes 8 x 32 positions; per chunk of 128 bytes of input channels (32 f32 or 64
-// f16 / bf16) the 9 x 33 input halo goes global -> LDS with direct loads (whole 128-byte
-// channel runs per pixel, each fetched once; halo overhead 1.16x), double-buffered (two
-// workgroups per CU keep four chunks in flight), 16-byte
-// slots XOR-swizzled by pixel so that each thread's 16-byte neighbour reads are free of bank
-// conflicts. Weights come through scalar loads ([cin][phase][tap][COUT], uniform). Against the
+// threads takes 8 x 32 positions; per chunk of 64 bytes of input channels (16 f32 or 32
+// f16 / bf16) the 9 x 33 input halo goes global -> LDS with direct loads (halo overhead 1.16x),
+// double-buffered in 38 KB, so that four workgroups share a CU and one's loads fly while the
+// others run their FMAs (128-byte chunks, 76 KB and two workgroups per CU: f32 127 -> 107 us
+// per config-5 launch), 16-byte slots XOR-swizzled by pixel so that each thread's 16-byte
+// neighbour reads are free of bank conflicts. Weights come through scalar loads ([cin][phase][tap][COUT], uniform). Against the
 // generic kernel on HOP luma's 128 -> 1 layer (862 x 862 positions): f32 153 vs 270 us, bf16
 // 122 vs 226 us. FMA order
 // per output is the generic kernel's (input channel ascending, then the phase's taps in
@@ -925,7 +925,8 @@ __global__ void __launch_bounds__(256)
 k_convT3_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
     constexpr int TY = 8, TX = 32, HX = TX + 1, HY = TY + 1, HPIX = HX * HY;
     constexpr int VEC = 16 / (int)sizeof(T);
-    constexpr int HALO_U = HPIX * 8;                  // [pixel][8 swizzled 16-byte slots]
+    constexpr int CPU = 4;                            // 16-byte units per pixel and chunk
+    constexpr int HALO_U = HPIX * CPU;                // [pixel][CPU swizzled 16-byte slots]
     constexpr int HN = (HALO_U + 255) / 256;
     __shared__ u32x4 s_halo[2 * HALO_U];
     const int gw = (p.OW + 1) / 2, gh = (p.OH + 1) / 2;
@@ -947,19 +948,21 @@ k_convT3_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
 #pragma unroll
         for (int oc = 0; oc < COUT; ++oc) acc[ph][oc] = (p.bias && oc < p.cout_g) ? p.bias[oc] : 0.0f;
 
-    // Halo unit U = pixel * 8 + slot holds the pixel's 16-byte unit slot ^ ((pixel / 2) % 8).
+    // Halo unit U = pixel * CPU + slot holds the pixel's 16-byte unit slot ^ ((pixel / 4) % 4):
+    // the 16 lanes of each ds_read_b128 pass (32 neighbouring pixels per wave row) then sit on
+    // distinct bank quads for any first pixel.
     long long hoff[HN];
 #pragma unroll
     for (int i = 0; i < HN; ++i) {
-        const int U = wave * 64 + i * 256 + lane, pix = U >> 3, slot = U & 7;
+        const int U = wave * 64 + i * 256 + lane, pix = U >> 2, slot = U & 3;
         const int hy = pix / HX, hx = pix - hy * HX;
         const int iy = y0 + hy, ix = x0 + hx;
         hoff[i] = (U < HALO_U && iy < p.H && ix < p.W)
-                      ? (long long)iy * p.x.row + (long long)ix * p.x.cs + (slot ^ ((pix >> 1) & 7)) * VEC
+                      ? (long long)iy * p.x.row + (long long)ix * p.x.cs + (slot ^ ((pix >> 2) & 3)) * VEC
                       : -1;
     }
     auto issue = [&](int chunk, int buf) __attribute__((always_inline)) {
-        const long long c0 = (long long)chunk * 8 * VEC;
+        const long long c0 = (long long)chunk * CPU * VEC;
 #pragma unroll
         for (int i = 0; i < HN; ++i) {
             const int ub = wave * 64 + i * 256;
@@ -976,7 +979,7 @@ k_convT3_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) npix[2 * a + b] = (r + a) * HX + c + b;
 
-    const int nch = cin / (8 * VEC);
+    const int nch = cin / (CPU * VEC);
     issue(0, 0);
     for (int ch = 0; ch < nch; ++ch) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of chunk ch are in LDS
@@ -984,12 +987,12 @@ k_convT3_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
         if (ch + 1 < nch) issue(ch + 1, (ch + 1) & 1);
         const u32x4* hb = s_halo + (ch & 1) * HALO_U;
 #pragma unroll 2
-        for (int q = 0; q < 8; ++q) {
+        for (int q = 0; q < CPU; ++q) {
             float x[4][VEC];
 #pragma unroll
             for (int n = 0; n < 4; ++n) {
                 const int pix = npix[n];
-                unpack16<T>(hb[pix * 8 + (q ^ ((pix >> 1) & 7))], x[n]);
+                unpack16<T>(hb[pix * CPU + (q ^ ((pix >> 2) & 3))], x[n]);
                 if (p.relu6_in) {
 #pragma unroll
                     for (int i = 0; i < VEC; ++i) {
@@ -1001,7 +1004,7 @@ k_convT3_narrow(const ConvParams p, const float* __restrict__ wn, int cin) {
             }
 #pragma unroll
             for (int i = 0; i < VEC; ++i) {
-                const float* w = wn + (long long)((ch * 8 + q) * VEC + i) * 16 * COUT;
+                const float* w = wn + (long long)((ch * CPU + q) * VEC + i) * 16 * COUT;
                 // Phase taps in (ky, kx) order: (0,0): x00; (0,1): x01, x00; (1,0): x10, x00;
                 // (1,1): x11, x10, x01, x00.
 #pragma unroll
