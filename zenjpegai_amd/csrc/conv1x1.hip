@@ -9,8 +9,9 @@
 // base + 16 i) through a ring of NS chunk slots, one barrier per chunk, NS - 2 chunks in flight
 // behind the one being consumed. A position's 64 bytes are read by 4 consecutive lanes as one
 // contiguous run; its 4 16-byte slots are XOR-swizzled by the position index so that the
-// fragment reads are free of bank conflicts (as are the weight rows'). The weight blocks are the implicit-GEMM packing
-// ([chunk][16-channel block][16][64 bytes]), one contiguous NB-block run per chunk.
+// fragment reads are free of bank conflicts (as are the weight rows'). The weight blocks are
+// the implicit-GEMM packing ([chunk][16-channel block][16][64 bytes]), one contiguous NB-block
+// run per chunk.
 //
 // Numerics are those of the implicit-GEMM kernels for a 1x1 layer, so the two agree bit for
 // bit: the bias first, then chunk by chunk in ascending order; f32 as four
@@ -124,7 +125,7 @@ conv1x1_ring(const ConvParams p) {
 #pragma unroll
         for (int i = 0; i < AN; ++i) {
             const int u = wave * 64 + i * NT;
-            const int U = u + lane;
+            const int U = u + lane;  // LDS unit U holds weight unit U ^ swz(row U / 4)
             lds_dma16(wg + c * wchunk + (U ^ ((U >> 3) & 2)), dst + B_U + u);
         }
     };
