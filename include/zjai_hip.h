@@ -124,8 +124,8 @@ typedef struct zjai_stats {
     float last_run_ms;        /* device time of the last zjai_picture_run (HIP events) */
     int64_t kernel_launches;  /* launches issued by the context so far */
     uint64_t pool_in_use;     /* device bytes held by live tensors */
-    uint64_t pool_peak;       /* high-water mark of pool_in_use */
-    uint64_t pool_cached;     /* device bytes held by the pool in total */
+    uint64_t pool_peak;       /* high-water mark of pool_in_use since the last zjai_release_buffers */
+    uint64_t pool_cached;     /* device bytes held by the pools in total (live + cached blocks) */
     uint64_t f16_nonfinite;   /* ZJAI_CTX_COUNT_F16_RANGE: non-finite f16 samples stored so far */
 } zjai_stats;
 /* Replaces the reference's `DecodeStats` probe (src/decoder/stats.rs:301) for device work. With
@@ -156,7 +156,9 @@ typedef struct zjai_prof_record {
 } zjai_prof_record;
 ZJAI_API int32_t zjai_profile_begin(zjai_ctx* ctx);
 ZJAI_API int32_t zjai_profile_end(zjai_ctx* ctx, zjai_prof_record* out, int32_t cap, int32_t* n);
-/* Returns cached pool blocks to the device (`release_buffers`, src/nn/fast/tensor.rs:122). */
+/* Returns cached pool blocks to the device (`release_buffers`, src/nn/fast/tensor.rs:122), the
+ * lanes' included, and starts a new pool_peak. The pool figures of zjai_get_stats cover the
+ * context's own pool and every lane's (pool_peak: the sum of the pools' high-water marks). */
 ZJAI_API int32_t zjai_release_buffers(zjai_ctx* ctx);
 
 /* ----------------------------------------------------------------------- device tensors */
@@ -260,6 +262,10 @@ ZJAI_API int32_t zjai_net_create(zjai_ctx* ctx, int32_t op, int32_t component, i
 ZJAI_API int32_t zjai_net_destroy(zjai_net* net);
 /* Output plane size of a net for an h x w target (>= h x w; the caller crops). */
 ZJAI_API int32_t zjai_net_out_size(const zjai_net* net, int32_t h, int32_t w, int32_t* oh, int32_t* ow);
+/* Device bytes a net's packed weights, biases and vectors hold (any net kind). With the
+ * estimate of zjai_picture_estimate_memory it sizes a decode's device memory, as the reference's
+ * `estimate_memory` counts the packed networks in its fixed term (src/decoder/limits.rs:164). */
+ZJAI_API int32_t zjai_net_device_bytes(const zjai_net* net, uint64_t* bytes);
 /* `SynthesisPrimary::forward_with` (src/model/synthesis.rs:262): y_hat [160][lh][lw] device
  * tensor -> host planar [1][oh][ow] in [0, 255] (capacity `len` floats). */
 ZJAI_API int32_t zjai_primary_forward(zjai_ctx* ctx, const zjai_net* net, const zjai_tensor* y_hat,
@@ -300,6 +306,36 @@ ZJAI_API int32_t zjai_picture_destroy(zjai_picture* pic);
 /* Uploads the decoded latents once (planar f32; uv_hat may be NULL without net_uv). */
 ZJAI_API int32_t zjai_picture_upload(zjai_ctx* ctx, zjai_picture* pic, const float* y_hat,
                             const float* uv_hat);
+/* Device memory of one picture before anything is allocated, the counterpart of the reference's
+ * `estimate_memory` (src/decoder/limits.rs:164-245; host only, no device needed). Arguments as
+ * zjai_picture_create's, with the nets given by operating point, precision and whether a chroma
+ * net runs, and the lane count of zjai_picture_set_lanes. Figures:
+ *   picture_bytes: the latents and output planes zjai_picture_create allocates (exact);
+ *   live_bytes: the buffer-pool blocks the tile batches hold at once (lanes run together), the
+ *     decode's working set (the reference's `live_bytes`);
+ *   pool_bytes: the blocks the pools keep cached after the run on a released context
+ *     (zjai_release_buffers returns them; a pool also frees them and retries when the device runs
+ *     out), >= live_bytes.
+ * live and pool are models calibrated on measured pool use that bound it from above (bytes per
+ * sample of each tile batch's 16 x latent window, +8 %). The nets' own bytes
+ * (zjai_net_device_bytes) and the buffers of zjai_picture_download_rgb (6 bytes per displayed
+ * pixel, 18 with float planes) are not included. */
+typedef struct zjai_memory_estimate {
+    uint64_t picture_bytes;
+    uint64_t live_bytes;
+    uint64_t pool_bytes;
+} zjai_memory_estimate;
+ZJAI_API int32_t zjai_picture_estimate_memory(int32_t op, int32_t precision, int32_t with_uv, int32_t lh,
+                                              int32_t lw, int32_t height, int32_t width,
+                                              const zjai_tile* tiles, int32_t n_tiles, int32_t sv,
+                                              int32_t sh, int32_t out_h, int32_t out_w, int32_t bit_depth,
+                                              int32_t lanes, zjai_memory_estimate* out);
+/* Admission bound (`Limits::max_memory_bytes`, src/decoder/limits.rs:30-34, checked by
+ * `check_header` :106-111): with bytes > 0, zjai_picture_create and zjai_picture_set_lanes refuse
+ * with ZJAI_E_LIMIT, before allocating anything, a picture whose nets (zjai_net_device_bytes)
+ * plus picture_bytes and live_bytes of zjai_picture_estimate_memory at its lane count exceed
+ * `bytes`. 0 (the default) disables the check. */
+ZJAI_API int32_t zjai_ctx_set_memory_limit(zjai_ctx* ctx, uint64_t bytes);
 /* Runs every tile, on the context's stream or spread over lanes (see zjai_picture_set_lanes),
  * and waits for the picture (latents must be uploaded). */
 ZJAI_API int32_t zjai_picture_run(zjai_ctx* ctx, zjai_picture* pic);

@@ -65,6 +65,11 @@ class ZjaiStats(ctypes.Structure):
                 ("pool_cached", ctypes.c_uint64), ("f16_nonfinite", ctypes.c_uint64)]
 
 
+class ZjaiMemoryEstimate(ctypes.Structure):
+    _fields_ = [("picture_bytes", ctypes.c_uint64), ("live_bytes", ctypes.c_uint64),
+                ("pool_bytes", ctypes.c_uint64)]
+
+
 class ZjaiProfRecord(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 96), ("flops", ctypes.c_double),
                 ("bytes", ctypes.c_double), ("ms", ctypes.c_float)]
@@ -119,6 +124,7 @@ PROTOTYPES = {
                         _i32p, ctypes.POINTER(_f32p), _pp],
     "zjai_net_destroy": [_vp],
     "zjai_net_out_size": [_vp, _i32, _i32, _i32p, _i32p],
+    "zjai_net_device_bytes": [_vp, ctypes.POINTER(ctypes.c_uint64)],
     "zjai_primary_forward": [_vp, _vp, _vp, _i32, _i32, _f32p, ctypes.c_size_t],
     "zjai_secondary_forward": [_vp, _vp, _vp, _vp, _i32, _i32, _f32p, ctypes.c_size_t],
     "zjai_synthesis_tiles": [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
@@ -126,6 +132,10 @@ PROTOTYPES = {
     "zjai_picture_create": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, ctypes.POINTER(ZjaiTile),
                             _i32, _i32, _i32, _i32, _i32, _i32, _pp],
     "zjai_picture_destroy": [_vp],
+    "zjai_picture_estimate_memory": [_i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                     ctypes.POINTER(ZjaiTile), _i32, _i32, _i32, _i32, _i32, _i32,
+                                     _i32, ctypes.POINTER(ZjaiMemoryEstimate)],
+    "zjai_ctx_set_memory_limit": [_vp, ctypes.c_uint64],
     "zjai_picture_upload": [_vp, _vp, _f32p, _f32p],
     "zjai_picture_run": [_vp, _vp],
     "zjai_picture_set_lanes": [_vp, _vp, _i32],

@@ -3,7 +3,9 @@
 
 #include <algorithm>
 #include <array>
+#include <cmath>
 #include <map>
+#include <set>
 #include <cstring>
 #include <mutex>
 
@@ -181,9 +183,15 @@ extern "C" int32_t zjai_get_stats(zjai_ctx* ctx, zjai_stats* out) {
     if (!ctx || !out) return ZJAI_E_INVALID_ARGUMENT;
     out->last_run_ms = ctx->c.last_ms;
     out->kernel_launches = ctx->c.launches;
+    // The root context's pool and every lane's (lanes run at once, so their peaks can coincide).
     out->pool_in_use = ctx->c.pool.in_use();
     out->pool_peak = ctx->c.pool.peak();
     out->pool_cached = ctx->c.pool.cached();
+    for (const auto& l : ctx->c.lanes) {
+        out->pool_in_use += l->pool.in_use();
+        out->pool_peak += l->pool.peak();
+        out->pool_cached += l->pool.cached();
+    }
     out->f16_nonfinite = 0;
     if (!(ctx->c.flags & ZJAI_CTX_COUNT_F16_RANGE)) return ZJAI_OK;
     return guard(ctx, [&] { out->f16_nonfinite = f16_range_total(ctx->c); });
@@ -234,6 +242,12 @@ extern "C" int32_t zjai_release_buffers(zjai_ctx* ctx) {
     return guard(ctx, [&] {
         ZJAI_HIP(hipStreamSynchronize(ctx->c.stream));
         ctx->c.pool.trim();
+        ctx->c.pool.reset_peak();
+        for (const auto& l : ctx->c.lanes) {
+            ZJAI_HIP(hipStreamSynchronize(l->stream));
+            l->pool.trim();
+            l->pool.reset_peak();
+        }
     });
 }
 
@@ -577,6 +591,12 @@ extern "C" int32_t zjai_net_out_size(const zjai_net* net, int32_t h, int32_t w, 
     return ZJAI_OK;
 }
 
+extern "C" int32_t zjai_net_device_bytes(const zjai_net* net, uint64_t* bytes) {
+    if (!net || !bytes) return ZJAI_E_INVALID_ARGUMENT;
+    *bytes = net->n->device_bytes();
+    return ZJAI_OK;
+}
+
 static void run_to_host(zjai_ctx* ctx, const zjai_net* net, const TensorP& a, const TensorP& b, int h, int w,
                         float* out, size_t len) {
     const bool primary = net->n->comp == COMP_Y;
@@ -742,6 +762,150 @@ extern "C" int32_t zjai_synthesis_tiles(int32_t height, int32_t width, int32_t l
     });
 }
 
+// ------------------------------------------------------------------- picture plan and memory
+// A picture's tiles checked and grouped into batches: tiles of one image and latent window size
+// share every layer shape and run as one batch of up to MAXB, in the order of their sizes; with
+// lanes > 1 batch i runs on lane i % lanes. Host only.
+struct PicturePlan {
+    std::vector<std::vector<int>> batches;
+    std::vector<zjai_tile> tiles;
+    int op = 0, dtype = DT_F32, lh = 0, lw = 0, out_h = 0, out_w = 0, sv = 1, sh = 1, bit_depth = 0;
+    bool uv = false;
+};
+
+static PicturePlan plan_picture(int op, int dtype, bool uv, int lh, int lw, int height, int width,
+                                const zjai_tile* tiles, int n_tiles, int sv, int sh, int out_h, int out_w,
+                                int bit_depth) {
+    need(op >= OP_SOP && op <= OP_HOP, "operating point");
+    need(dtype >= DT_F32 && dtype <= DT_BF16, "precision");
+    need(tiles && n_tiles > 0, "no tiles");
+    need(lh > 0 && lw > 0 && height > 0 && width > 0, "sizes");
+    need(sv >= 1 && sv <= 2 && sh >= 1 && sh <= 2, "chroma subsampling");
+    need(out_h > 0 && out_w > 0 && out_h <= height && out_w <= width, "displayed size");
+    need(bit_depth == 0 || (bit_depth >= 8 && bit_depth <= 16), "bit depth");
+    PicturePlan p;
+    p.op = op; p.dtype = dtype; p.uv = uv; p.lh = lh; p.lw = lw; p.out_h = out_h; p.out_w = out_w;
+    p.sv = sv; p.sh = sh; p.bit_depth = bit_depth;
+    p.tiles.assign(tiles, tiles + n_tiles);
+    for (const zjai_tile& t : p.tiles) {
+        need(t.latent_x >= 0 && t.latent_y >= 0 && t.latent_w > 0 && t.latent_h > 0 &&
+                 t.latent_x + t.latent_w <= lw && t.latent_y + t.latent_h <= lh,
+             "tile latent window outside the latent");
+        need(t.image_w > 0 && t.image_h > 0 && t.core_w > 0 && t.core_h > 0, "tile sizes");
+        // latent_extent (src/tools/tiles.rs:22-24): a tile's latent window is ceil(len / 16).
+        need(t.latent_h == ceil_div(t.image_h, 16) && t.latent_w == ceil_div(t.image_w, 16),
+             "tile latent window is not ceil(image size / 16)");
+        int oh, ow;
+        primary_out_size(op, t.image_h, t.image_w, &oh, &ow);
+        need(t.core_off_y >= 0 && t.core_off_x >= 0 && t.core_off_y + t.core_h <= oh &&
+                 t.core_off_x + t.core_w <= ow,
+             "synthesis tile smaller than its core");
+        need(t.core_x >= 0 && t.core_y >= 0, "tile core position");
+    }
+    std::map<std::array<int, 4>, std::vector<int>> by_size;
+    for (int i = 0; i < n_tiles; ++i) {
+        const zjai_tile& t = p.tiles[i];
+        by_size[{t.image_h, t.image_w, t.latent_h, t.latent_w}].push_back(i);
+    }
+    for (auto& kv : by_size)
+        for (size_t i = 0; i < kv.second.size(); i += MAXB)
+            p.batches.emplace_back(kv.second.begin() + i, kv.second.begin() + std::min(kv.second.size(), i + MAXB));
+    return p;
+}
+
+// Device memory of one picture, the counterpart of the reference's `estimate_memory`
+// (src/decoder/limits.rs:164-245), which sizes a decode from its header before anything runs as
+// fixed buffers plus bytes per sample of the synthesis tiles.
+//  * picture: the latents and output planes zjai_picture_create allocates (exact).
+//  * live: the pool blocks in use at once (a model). A batch of N tiles of one latent window holds
+//    at most KL x N x 256 x latent_h x latent_w bytes (16 x 16 samples per latent position: the
+//    extent every layer's map scales with) and frees them all at its end; lanes run their batches
+//    at the same time, so live = sum over lanes of the largest batch each runs.
+//  * pool: the blocks the pools keep (a model). A pool reuses a cached block only for a request of
+//    the same size up to 1.5x larger, so a lane keeps the blocks of every (tile shape, batch size)
+//    it ran: sum over those of KP x N x 256 x latent_h x latent_w.
+// KL and KP are measured (pool_peak and pool_cached after one 1024 x 1024 untiled picture on a
+// released context; the same per-sample figures from 256 x 256 up), plus 8 %, and 256 KiB per
+// term for the pool's size rounding on small tiles.
+struct MemEstimate {
+    uint64_t picture = 0, live = 0, pool = 0;
+};
+
+static MemEstimate estimate_picture(const PicturePlan& p, int lanes) {
+    // Measured bytes per sample and batch item: [op][16-bit storage][with a chroma net].
+    static const double KL[3][2][2] = {
+        {{18.5, 18.5}, {9.2, 9.2}},        // SOP
+        {{50.5, 50.5}, {25.2, 25.2}},      // BOP
+        {{290.5, 290.5}, {145.2, 145.2}},  // HOP
+    };
+    static const double KP[3][2][2] = {
+        {{29.0, 32.5}, {14.5, 16.2}},
+        {{93.0, 110.5}, {46.5, 55.2}},
+        {{517.0, 630.0}, {260.8, 318.7}},
+    };
+    const int s16 = p.dtype == DT_F32 ? 0 : 1, u = p.uv ? 1 : 0;
+    const double kl = KL[p.op][s16][u] * 1.08, kp = KP[p.op][s16][u] * 1.08, slack = 256.0 * 1024.0;
+    MemEstimate e;
+    const uint64_t lat = (uint64_t)p.lh * p.lw, sb = p.bit_depth ? 2 : 4;
+    e.picture = 4 * 160 * lat + sb * (uint64_t)p.out_h * p.out_w;
+    if (p.uv) e.picture += 4 * 96 * lat + sb * 2 * (uint64_t)ceil_div(p.out_h, p.sv) * ceil_div(p.out_w, p.sh);
+    const int nl = std::max(1, std::min<int>(lanes, (int)p.batches.size()));
+    std::vector<std::set<std::array<int, 3>>> held(nl);
+    for (size_t i = 0; i < p.batches.size(); ++i) {
+        const zjai_tile& t = p.tiles[p.batches[i][0]];
+        held[i % nl].insert({t.latent_h, t.latent_w, (int)p.batches[i].size()});
+    }
+    double live = 0.0, pool = 0.0;
+    for (const auto& lane : held) {
+        double top = 0.0;
+        for (const auto& s : lane) {
+            const double samples = (double)s[2] * 256.0 * s[0] * s[1];
+            top = std::max(top, kl * samples);
+            pool += kp * samples + slack;
+        }
+        live += top + slack;
+    }
+    e.live = (uint64_t)std::ceil(live);
+    e.pool = (uint64_t)std::ceil(pool);
+    return e;
+}
+
+// Admission: with a memory limit set on the context, a picture whose nets, buffers and modelled
+// live pool blocks exceed it is refused before anything is allocated (the reference checks its
+// estimate's live bytes against `max_memory_bytes` the same way, src/decoder/limits.rs:106-111).
+static void admit(const Context& c, const PicturePlan& p, int lanes, const Net& net_y, const Net* net_uv) {
+    if (!c.mem_limit) return;
+    const MemEstimate e = estimate_picture(p, lanes);
+    const uint64_t total = e.picture + e.live + net_y.device_bytes() + (net_uv ? net_uv->device_bytes() : 0);
+    if (total > c.mem_limit)
+        throw Error(ZJAI_E_LIMIT, "estimated device memory of the picture (" + std::to_string(total) +
+                                      " bytes) exceeds the context's limit (" + std::to_string(c.mem_limit) +
+                                      " bytes)");
+}
+
+extern "C" int32_t zjai_picture_estimate_memory(int32_t op, int32_t precision, int32_t with_uv, int32_t lh,
+                                                int32_t lw, int32_t height, int32_t width,
+                                                const zjai_tile* tiles, int32_t n_tiles, int32_t sv,
+                                                int32_t sh, int32_t out_h, int32_t out_w, int32_t bit_depth,
+                                                int32_t lanes, zjai_memory_estimate* out) {
+    if (!out || !tiles || n_tiles <= 0 || lanes < 1 || lanes > MAXB || (with_uv != 0 && with_uv != 1))
+        return ZJAI_E_INVALID_ARGUMENT;
+    return guard(nullptr, [&] {
+        const PicturePlan p = plan_picture(op, precision, with_uv != 0, lh, lw, height, width, tiles, n_tiles,
+                                           sv, sh, out_h, out_w, bit_depth);
+        const MemEstimate e = estimate_picture(p, lanes);
+        out->picture_bytes = e.picture;
+        out->live_bytes = e.live;
+        out->pool_bytes = e.pool;
+    });
+}
+
+extern "C" int32_t zjai_ctx_set_memory_limit(zjai_ctx* ctx, uint64_t bytes) {
+    if (!ctx) return ZJAI_E_INVALID_ARGUMENT;
+    ctx->c.mem_limit = bytes;
+    return ZJAI_OK;
+}
+
 // --------------------------------------------------------------------------------- picture
 struct zjai_picture {
     NetP net_y, net_uv;
@@ -800,10 +964,9 @@ extern "C" int32_t zjai_picture_create(zjai_ctx* ctx, const zjai_net* net_y, con
                          net_uv->n->op == net_y->n->op),
              "net_uv mismatch");
         need(!net_uv || net_uv->n->dtype == net_y->n->dtype, "nets differ in precision");
-        need(lh > 0 && lw > 0 && height > 0 && width > 0, "sizes");
-        need(sv >= 1 && sv <= 2 && sh >= 1 && sh <= 2, "chroma subsampling");
-        need(out_h > 0 && out_w > 0 && out_h <= height && out_w <= width, "displayed size");
-        need(bit_depth == 0 || (bit_depth >= 8 && bit_depth <= 16), "bit depth");
+        PicturePlan plan = plan_picture(net_y->n->op, net_y->n->dtype, net_uv != nullptr, lh, lw, height, width,
+                                        tiles, n_tiles, sv, sh, out_h, out_w, bit_depth);
+        admit(ctx->c, plan, 1, *net_y->n, net_uv ? net_uv->n.get() : nullptr);
         auto* p = new zjai_picture();
         std::unique_ptr<zjai_picture> own(p);
         p->net_y = net_y->n;
@@ -811,31 +974,7 @@ extern "C" int32_t zjai_picture_create(zjai_ctx* ctx, const zjai_net* net_y, con
         p->lh = lh; p->lw = lw; p->height = height; p->width = width; p->sv = sv; p->sh = sh;
         p->out_h = out_h; p->out_w = out_w; p->bit_depth = bit_depth;
         p->tiles.assign(tiles, tiles + n_tiles);
-        for (const zjai_tile& t : p->tiles) {
-            need(t.latent_x >= 0 && t.latent_y >= 0 && t.latent_w > 0 && t.latent_h > 0 &&
-                     t.latent_x + t.latent_w <= lw && t.latent_y + t.latent_h <= lh,
-                 "tile latent window outside the latent");
-            need(t.image_w > 0 && t.image_h > 0 && t.core_w > 0 && t.core_h > 0, "tile sizes");
-            // latent_extent (src/tools/tiles.rs:22-24): a tile's latent window is ceil(len / 16).
-            need(t.latent_h == ceil_div(t.image_h, 16) && t.latent_w == ceil_div(t.image_w, 16),
-                 "tile latent window is not ceil(image size / 16)");
-            int oh, ow;
-            primary_out_size(p->net_y->op, t.image_h, t.image_w, &oh, &ow);
-            need(t.core_off_y >= 0 && t.core_off_x >= 0 && t.core_off_y + t.core_h <= oh &&
-                     t.core_off_x + t.core_w <= ow,
-                 "synthesis tile smaller than its core");
-            need(t.core_x >= 0 && t.core_y >= 0, "tile core position");
-        }
-        // One batch shares every layer shape: key on the image and the latent window size.
-        std::map<std::array<int, 4>, std::vector<int>> by_size;
-        for (int i = 0; i < n_tiles; ++i) {
-            const zjai_tile& t = p->tiles[i];
-            by_size[{t.image_h, t.image_w, t.latent_h, t.latent_w}].push_back(i);
-        }
-        for (auto& kv : by_size)
-            for (size_t i = 0; i < kv.second.size(); i += MAXB)
-                p->batches.emplace_back(kv.second.begin() + i,
-                                        kv.second.begin() + std::min(kv.second.size(), i + MAXB));
+        p->batches = std::move(plan.batches);
         ZJAI_HIP(hipMalloc(&p->y_hat, sizeof(float) * 160 * (size_t)lh * lw));
         if (p->net_uv) ZJAI_HIP(hipMalloc(&p->uv_hat, sizeof(float) * 96 * (size_t)lh * lw));
         ZJAI_HIP(hipMalloc(&p->out_y, p->sample_bytes() * (size_t)out_h * out_w));
@@ -1037,7 +1176,18 @@ extern "C" int32_t zjai_picture_set_replay(zjai_ctx* ctx, zjai_picture* pic, int
 
 extern "C" int32_t zjai_picture_set_lanes(zjai_ctx* ctx, zjai_picture* pic, int32_t lanes) {
     if (!ctx || !pic || lanes < 1 || lanes > MAXB) return ZJAI_E_INVALID_ARGUMENT;
-    return guard(ctx, [&] { pic->lanes = lanes; });
+    return guard(ctx, [&] {
+        if (ctx->c.mem_limit) {
+            PicturePlan plan;
+            plan.op = pic->net_y->op; plan.dtype = pic->net_y->dtype; plan.uv = (bool)pic->net_uv;
+            plan.lh = pic->lh; plan.lw = pic->lw; plan.out_h = pic->out_h; plan.out_w = pic->out_w;
+            plan.sv = pic->sv; plan.sh = pic->sh; plan.bit_depth = pic->bit_depth;
+            plan.tiles = pic->tiles;
+            plan.batches = pic->batches;
+            admit(ctx->c, plan, lanes, *pic->net_y, pic->net_uv.get());
+        }
+        pic->lanes = lanes;
+    });
 }
 
 extern "C" int32_t zjai_picture_download(zjai_ctx* ctx, zjai_picture* pic, void* y, void* u, void* v) {

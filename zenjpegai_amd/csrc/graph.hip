@@ -67,8 +67,9 @@ struct Builder {
         const Param& p = get(name, shape);
         float* d = nullptr;
         ZJAI_HIP(hipMalloc(&d, sizeof(float) * n));
-        ZJAI_HIP(hipMemcpy(d, p.data, sizeof(float) * n, hipMemcpyHostToDevice));
         net.vec[name] = d;
+        net.vec_bytes += sizeof(float) * n;
+        ZJAI_HIP(hipMemcpy(d, p.data, sizeof(float) * n, hipMemcpyHostToDevice));
     }
     // ResAu::load (src/model/synthesis.rs:33-60): the weight's dim 1 decides the groups.
     void res_au(const std::string& pfx, int chs) {
@@ -142,8 +143,9 @@ struct Builder {
         for (auto* q : {&lo, &hi}) {
             float* d = nullptr;
             ZJAI_HIP(hipMalloc(&d, sizeof(float) * n));
-            ZJAI_HIP(hipMemcpy(d, (*q)->second.data, sizeof(float) * n, hipMemcpyHostToDevice));
             net.vec[(*q)->first] = d;
+            net.vec_bytes += sizeof(float) * n;
+            ZJAI_HIP(hipMemcpy(d, (*q)->second.data, sizeof(float) * n, hipMemcpyHostToDevice));
         }
         net.clip_n[stage] = n;
     }

@@ -64,6 +64,8 @@ public:
     size_t in_use() const { return in_use_; }
     size_t peak() const { return peak_; }
     size_t cached() const { return cached_; }
+    // Starts a new high-water mark at the bytes now in use.
+    void reset_peak() { peak_ = in_use_; }
     std::shared_ptr<FaultPlan> faults;  // the root context's plan (shared with its lanes)
     ~Pool();
 
@@ -109,6 +111,7 @@ struct Context {
     unsigned long long* range_slots = nullptr;
     std::string last_error;
     volatile int stop = 0;
+    uint64_t mem_limit = 0;  // zjai_ctx_set_memory_limit: device bytes a picture may need (0: none)
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     float last_ms = 0.0f;
     long long launches = 0;
@@ -189,6 +192,7 @@ struct Layer {
     void* wm16 = nullptr;      // narrow 3x3 transposed conv, 16-bit MFMA: [cin / 32][4][row block][16][32]
     size_t wm16_bytes = 0;
     size_t wpk_bytes = 0;
+    size_t dev_bytes = 0;      // device bytes of every array above
     ~Layer();
 
     void out_size(int h, int w, int* oh, int* ow) const;
@@ -264,6 +268,12 @@ struct Net {
     int clip_n[6] = {};    // analysis nets: channels clipped after conv k (0: no clip_thres)
     std::map<std::string, LayerP> L;
     std::map<std::string, float*> vec;  // device f32 vectors (layer norm, temperature)
+    size_t vec_bytes = 0;                // device bytes of vec
+    size_t device_bytes() const {
+        size_t b = vec_bytes;
+        for (const auto& kv : L) b += kv.second->dev_bytes;
+        return b;
+    }
     ~Net();
 };
 using NetP = std::shared_ptr<Net>;

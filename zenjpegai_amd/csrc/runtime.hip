@@ -241,7 +241,8 @@ static float storage_value(float v, int dtype) {
 }
 
 // Converts an f32 staging vector to the storage dtype and uploads it.
-static void* upload_as(Context& ctx, const std::vector<float>& host, int dtype, size_t* bytes_out) {
+static void* upload_as(Context& ctx, const std::vector<float>& host, int dtype, size_t* bytes_out,
+                       size_t* total) {
     const size_t n = host.size();
     void* dev = nullptr;
     if (dtype == DT_F32) {
@@ -256,12 +257,14 @@ static void* upload_as(Context& ctx, const std::vector<float>& host, int dtype, 
         ZJAI_HIP(hipMemcpy(dev, h.data(), n * 2, hipMemcpyHostToDevice));
         *bytes_out = n * 2;
     }
+    *total += *bytes_out;
     (void)ctx;
     return dev;
 }
 
-static float* upload_f32(const float* p, size_t n) {
+static float* upload_f32(const float* p, size_t n, size_t* total) {
     float* dev = nullptr;
+    *total += n * 4;
     ZJAI_HIP(hipMalloc(&dev, n * 4));
     ZJAI_HIP(hipMemcpy(dev, p, n * 4, hipMemcpyHostToDevice));
     return dev;
@@ -324,8 +327,8 @@ LayerP make_conv(Context& ctx, int cin, int cout, int kh, int kw, int stride, in
         std::vector<float> t((size_t)9 * cin);
         for (int c = 0; c < cin; ++c)
             for (int k = 0; k < 9; ++k) t[(size_t)k * cin + c] = weight[(size_t)c * 9 + k];
-        L->dw_w = upload_f32(t.data(), t.size());
-        if (bias) L->bias = upload_f32(bias, cout);
+        L->dw_w = upload_f32(t.data(), t.size(), &L->dev_bytes);
+        if (bias) L->bias = upload_f32(bias, cout, &L->dev_bytes);
         return L;
     }
     if (kh == 1 && kw == 1 && stride == 1) L->kind = CK_1x1;
@@ -353,7 +356,7 @@ LayerP make_conv(Context& ctx, int cin, int cout, int kh, int kw, int stride, in
                                            (size_t)r * CK + kk;
                         pk[dst] = weight[(((size_t)(g * cout_g + ocl) * cin_g + icl) * kh + ky) * kw + kx];
                     }
-    L->wpk = upload_as(ctx, pk, dtype, &L->wpk_bytes);
+    L->wpk = upload_as(ctx, pk, dtype, &L->wpk_bytes, &L->dev_bytes);
     if (dtype != DT_F32 && L->kind == CK_3x3 && groups == 1 && (cin == 64 || cin == 128) && cout % 64 == 0 && no_extra &&
         pad_h == 1 && pad_w == 1) {
         // conv3x3_m32's packing: [cin / 16][cout / mt][tap][channel half][mt][8].
@@ -365,11 +368,11 @@ LayerP make_conv(Context& ctx, int cin, int cout, int kh, int kw, int stride, in
                     p32[(((((size_t)(ic / 16) * nmt + oc / mt) * 9 + t) * 2 + (ic % 16) / 8) * mt + oc % mt) * 8 +
                         ic % 8] = weight[((size_t)oc * cin + ic) * 9 + t];
         size_t bytes = 0;
-        L->wpk32 = upload_as(ctx, p32, dtype, &bytes);
+        L->wpk32 = upload_as(ctx, p32, dtype, &bytes, &L->dev_bytes);
         L->mt32 = mt;
     }
-    if (bias) L->bias = upload_f32(bias, cout);
-    if (keep_f32 && L->kind == CK_1x1 && groups == 1) L->w_f32 = upload_f32(weight, (size_t)cout * cin);
+    if (bias) L->bias = upload_f32(bias, cout, &L->dev_bytes);
+    if (keep_f32 && L->kind == CK_1x1 && groups == 1) L->w_f32 = upload_f32(weight, (size_t)cout * cin, &L->dev_bytes);
     return L;
 }
 
@@ -434,8 +437,8 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
                     }
             }
     }
-    L->wpk = upload_as(ctx, pk, dtype, &L->wpk_bytes);
-    if (bias) L->bias = upload_f32(bias, cout);
+    L->wpk = upload_as(ctx, pk, dtype, &L->wpk_bytes, &L->dev_bytes);
+    if (bias) L->bias = upload_f32(bias, cout, &L->dev_bytes);
     if (k == 3 && cout > 8 && conv_tr_merged_taps_supported(L->ntaps) && L->nblk_g % TR_MERGED_NB == 0) {
         // All four phases per workgroup (launch_conv_tr_merged): the nine taps side by side per
         // K chunk and block, phase by phase, each phase's taps in its table order.
@@ -460,7 +463,7 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
                         }
                     }
             }
-        L->wpk_m = upload_as(ctx, pm, dtype, &L->wpk_m_bytes);
+        L->wpk_m = upload_as(ctx, pm, dtype, &L->wpk_m_bytes, &L->dev_bytes);
     }
     if (cout <= 8) {
         // Narrow layers run on the vector ALUs (launch_convT_narrow) from an f32 copy of the
@@ -479,7 +482,7 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
                                 storage_value(weight[(((size_t)ic * cout + oc) * k + ky) * k + kx], dtype);
                 }
         }
-        L->wn = upload_f32(wn.data(), wn.size());
+        L->wn = upload_f32(wn.data(), wn.size(), &L->dev_bytes);
         if (dtype != DT_F32 && k == 3 && (cin == 64 || cin == 128)) {
             // The MFMA form (launch_convT3_mfma): row R = phase * coutp + output of 16-row block
             // R / 16, K = (neighbour, input channel); tap t of phase ph reads input pixel
@@ -501,7 +504,7 @@ LayerP make_conv_transpose(Context& ctx, int cin, int cout, int k, int stride, i
                                 wn[((size_t)ic * 16 + ph * 4 + t) * L->coutp + oc];
                     }
                 }
-            if (ok) L->wm16 = upload_as(ctx, wm, dtype, &L->wm16_bytes);
+            if (ok) L->wm16 = upload_as(ctx, wm, dtype, &L->wm16_bytes, &L->dev_bytes);
         }
     }
     return L;

@@ -64,6 +64,12 @@ class _Net:
               self.eng.handle)
         return oh.value, ow.value
 
+    def device_bytes(self) -> int:
+        """Device bytes of the net's packed weights, biases and vectors."""
+        n = ctypes.c_uint64()
+        check(lib().zjai_net_device_bytes(self._h, ctypes.byref(n)), self.eng.handle)
+        return n.value
+
     def __del__(self):
         try:
             if self._h:
@@ -144,6 +150,23 @@ def _tile_array(tiles):
                                t.core.x, t.core.y, t.core.width, t.core.height,
                                t.core_offset[0], t.core_offset[1])
     return arr
+
+
+def estimate_picture_memory(op: str, precision: str, with_uv: bool, lh: int, lw: int, height: int,
+                            width: int, tiles, sv: int = 1, sh: int = 1, out_h: int | None = None,
+                            out_w: int | None = None, bit_depth: int = 0, lanes: int = 1) -> dict:
+    """Device bytes of a picture before it is created (``estimate_memory``,
+    src/decoder/limits.rs:164-245; ``zjai_picture_estimate_memory``, host only):
+    ``picture_bytes`` (latents and planes, exact), ``live_bytes`` (the tile batches' buffer-pool
+    blocks in use at once over all lanes) and ``pool_bytes`` (the blocks the pools keep after the
+    run), both modelled from above. The nets' bytes (``device_bytes()``) come on top."""
+    arr = _tile_array(list(tiles))
+    e = _lib.ZjaiMemoryEstimate()
+    check(lib().zjai_picture_estimate_memory(
+        _lib.OPS[op], _lib.PRECISIONS[precision], 1 if with_uv else 0, lh, lw, height, width, arr,
+        len(arr), sv, sh, height if out_h is None else out_h, width if out_w is None else out_w,
+        bit_depth, lanes, ctypes.byref(e)), None)
+    return {k: getattr(e, k) for k, _ in e._fields_}
 
 
 class Picture:

@@ -136,6 +136,12 @@ class Engine:
     def release_buffers(self):
         check(lib().zjai_release_buffers(self._h), self._h)
 
+    def set_memory_limit(self, nbytes: int):
+        """Admission bound (``Limits::max_memory_bytes``): pictures whose nets plus
+        ``model.estimate_picture_memory`` exceed ``nbytes`` are refused with ``E_LIMIT`` before
+        anything is allocated; 0 disables the check (``zjai_ctx_set_memory_limit``)."""
+        check(lib().zjai_ctx_set_memory_limit(self._h, nbytes), self._h)
+
     def inject_failure(self, what: int, after: int = 0):
         """Fail the next allocation (``_lib.FAIL_ALLOC``) or launch (``_lib.FAIL_LAUNCH``)
         after ``after`` successful ones, from the host (``zjai_inject_failure``)."""
