@@ -25,18 +25,46 @@ __device__ __forceinline__ Idx4 split(long long i, int h, int w, int q) {
 }
 
 // ------------------------------------------------------------------------------ layout moves
+// One workgroup per run of PT_X positions of a row: every channel plane's PT_X floats are read
+// as contiguous row segments into LDS (PT_C channels per pass, all of a pass's loads in flight
+// before the first is used), then each thread writes one position's 4 channels, so consecutive
+// threads write consecutive bytes of the NHWC row. Reading 4 channel planes per position
+// instead (one 4-byte access per plane and lane) fetched each 128-byte line of the planes three
+// times over.
+constexpr int PT_X = 8, PT_C = 256, PT_L = PT_C * PT_X / 256;
+// LDS holds a pass as [channel quad][PT_X + 1 positions][4 channels]: the position's quad is one
+// 16-byte read, and the odd quad stride (PT_X + 1 units) spreads a pass's lanes over the banks.
 template <typename T>
-__global__ void k_planar_to_nhwc(const float* src, int C, int LH, int LW, Windows win, int N, int h,
-                                 int w, View dst) {
-    const int q = C / 4;
-    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)N * h * w * q) return;
-    const Idx4 d = split(i, h, w, q);
-    f32x4 v;
+__global__ void __launch_bounds__(256) k_planar_to_nhwc(const float* src, int C, int LH, int LW, Windows win,
+                                                        int N, int h, int w, View dst) {
+    __shared__ f32x4 s_t[PT_C / 4 * (PT_X + 1)];
+    const int ntx = (w + PT_X - 1) / PT_X;
+    const int bx = (int)blockIdx.x % ntx, by = ((int)blockIdx.x / ntx) % h, b = (int)blockIdx.x / (ntx * h);
+    const int x0 = bx * PT_X, nx = min(PT_X, w - x0), tid = threadIdx.x;
+    const float* row = src + (long long)(win.y0[b] + by) * LW + win.x0[b] + x0;
+    const long long plane = (long long)LH * LW;
+    for (int c0 = 0; c0 < C; c0 += PT_C) {
+        const int cc = min(PT_C, C - c0);
+        float v[PT_L];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-        v[k] = src[((long long)(d.cq * 4 + k) * LH + (win.y0[d.b] + d.y)) * LW + (win.x0[d.b] + d.x)];
-    store4<T>(at_mut<T>(dst, d.b, d.y, d.x, d.cq * 4), v);
+        for (int k = 0; k < PT_L; ++k) {
+            // Clamped (in-window) address, so the loads issue back to back without branches.
+            const int i = tid + k * 256, c = min(i / PT_X, cc - 1), x = min(i % PT_X, nx - 1);
+            v[k] = row[(c0 + c) * plane + x];
+        }
+#pragma unroll
+        for (int k = 0; k < PT_L; ++k) {
+            const int i = tid + k * 256, c = i / PT_X, x = i % PT_X;
+            if (c < cc) s_t[(c / 4) * (PT_X + 1) + x][c % 4] = v[k];
+        }
+        __syncthreads();
+        const int q = cc / 4;
+        for (int i = tid; i < nx * q; i += 256) {
+            const int x = i / q, cq = i % q;
+            store4<T>(at_mut<T>(dst, b, by, x0 + x, c0 + cq * 4), s_t[cq * (PT_X + 1) + x]);
+        }
+        __syncthreads();
+    }
 }
 
 template <typename T>
@@ -626,9 +654,10 @@ hipError_t launch_planar_to_nhwc(const float* src, int C, int LH, int LW, const 
     if (C % 4 || N < 1 || N > MAXB) return hipErrorInvalidValue;
     for (int b = 0; b < N; ++b)
         if (win.y0[b] < 0 || win.x0[b] < 0 || win.y0[b] + h > LH || win.x0[b] + w > LW) return hipErrorInvalidValue;
-    const long long n = (long long)N * h * w * (C / 4);
-    if (n == 0) return hipSuccess;
-    ZJAI_DISPATCH(dtype, k_planar_to_nhwc, <<<grid_for(n), 256, 0, s>>>(src, C, LH, LW, win, N, h, w, dst))
+    const long long n = (long long)N * h * ((w + PT_X - 1) / PT_X);
+    if (n == 0 || C == 0) return hipSuccess;
+    if (n > 0x7fffffffLL) return hipErrorInvalidValue;
+    ZJAI_DISPATCH(dtype, k_planar_to_nhwc, <<<dim3((unsigned)n), 256, 0, s>>>(src, C, LH, LW, win, N, h, w, dst))
     return hipGetLastError();
 }
 
