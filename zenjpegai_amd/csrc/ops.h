@@ -2,6 +2,8 @@
 // channel attention). Host-callable launchers; every one runs over N batch items (tiles).
 #pragma once
 
+#include <string>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -115,6 +117,9 @@ int attention_gram_chunks(int h, int w);
 // Whether the Gram kernel's LDS stage (64 16-bit or 32 f32 positions of 2 dim channels) fits the
 // 160 KB of a CU for this dim: callers check it before their first launch.
 bool attention_gram_fits(int dtype, int dim);
+// Profile name of the Gram kernel launch_attention_gram runs for these operands, as the kernel
+// symbol reads (k_attention_gram<__bf16, true>: the fixed-offset staging form).
+std::string attention_gram_name(const View& qkv, int dtype, int dim, int w);
 hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads, int h, int w,
                                  float* partial, hipStream_t s);
 hipError_t launch_attention_softmax(const float* partial, int N, int nchunk, int dim, int heads,

@@ -376,7 +376,16 @@ template <typename T>
 constexpr int GRAM_SUB = 128 / (int)sizeof(T);
 constexpr int GRAM_PAD = 16;
 
+constexpr int GRAM_UNR = 8;
+// Whether the staging takes fixed per-thread offsets (see the kernel): one round of loads per
+// sub-chunk, dense positions, and 16-byte units per position dividing the workgroup.
 template <typename T>
+static bool gram_fast(const View& qkv, int dim, int w) {
+    const int upp = 2 * dim / (16 / (int)sizeof(T));
+    return upp > 0 && GRAM_SUB<T> * upp <= GRAM_UNR * 256 && qkv.row == (long long)w * qkv.cs && 256 % upp == 0;
+}
+
+template <typename T, bool FAST>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 k_attention_gram(View qkv, int dim, int heads, int n, int w, float* partial) {
     extern __shared__ __align__(16) unsigned char s_raw[];
@@ -395,28 +404,32 @@ k_attention_gram(View qkv, int dim, int heads, int n, int w, float* partial) {
     // sub-chunk is one round of them (units <= UNR * 256: dim <= 128), positions are dense
     // (row = w * cs) and upp divides 256, thread t's unit is t % upp of positions t / upp + k * pst
     // of the sub-chunk, k < UNR (pst = 256 / upp): fixed offsets, computed once.
-    constexpr int UNR = 8;
+    constexpr int UNR = GRAM_UNR;
     const int units = SUB * upp;
-    const bool fast = units <= UNR * 256 && qkv.row == (long long)w * qkv.cs && 256 % upp == 0;
+    constexpr bool fast = FAST;
     const int pst = fast ? 256 / upp : 0, fpl = fast ? threadIdx.x / upp : 0;
     const int fq = threadIdx.x - fpl * upp;
     const int fg = fpl * qkv.cs + fq * VEC, fs = fpl * ld + fq * VEC;
+    // Fast path: the next sub-chunk's loads go out before this one's sums, so they fly meanwhile.
+    u32x4 raw[UNR];
+    auto fetch = [&](int ps) __attribute__((always_inline)) {
+        const T* bp = base + (long long)ps * qkv.cs + fg;
+        const int np = min(ps + SUB, p1) - ps;
+#pragma unroll
+        for (int k = 0; k < UNR; ++k) {
+            raw[k] = u32x4{0u, 0u, 0u, 0u};
+            if (fpl + k * pst < np) raw[k] = *(const u32x4*)(bp + k * pst * qkv.cs);
+        }
+    };
     for (int h0 = 0; h0 < heads; h0 += 4) {
         const int hd = h0 + wave;  // a wave past the last head only stages
         f32x4 g[2][2] = {{z, z}, {z, z}};
         float sq[2] = {0.0f, 0.0f}, sk[2] = {0.0f, 0.0f};
+        if constexpr (FAST) fetch(p0);
         for (int ps = p0; ps < p1; ps += SUB) {
             const int pe = min(ps + SUB, p1);
             __syncthreads();  // the previous sub-chunk's reads are done
-            if (fast) {
-                const T* bp = base + (long long)ps * qkv.cs + fg;
-                const int np = pe - ps;
-                u32x4 raw[UNR];
-#pragma unroll
-                for (int k = 0; k < UNR; ++k) {
-                    raw[k] = u32x4{0u, 0u, 0u, 0u};
-                    if (fpl + k * pst < np) raw[k] = *(const u32x4*)(bp + k * pst * qkv.cs);
-                }
+            if constexpr (FAST) {
 #pragma unroll
                 for (int k = 0; k < UNR; ++k)
                     if (fpl + k * pst < SUB) *reinterpret_cast<u32x4*>(s_qk + fs + k * pst * ld) = raw[k];
@@ -443,6 +456,8 @@ k_attention_gram(View qkv, int dim, int heads, int n, int w, float* partial) {
                 }
             }
             __syncthreads();
+            if constexpr (FAST)
+                if (ps + SUB < p1) fetch(ps + SUB);
             if (hd >= heads) continue;  // uniform per wave
             for (int p = ps; p < pe; p += 4) {
                 float aq[2], ak[2];
@@ -728,6 +743,14 @@ bool attention_gram_fits(int dtype, int dim) {
     return lds <= 160 * 1024;
 }
 
+std::string attention_gram_name(const View& qkv, int dtype, int dim, int w) {
+    static const char* ty[] = {"float", "_Float16", "__bf16"};
+    if (dtype < DT_F32 || dtype > DT_BF16) return "k_attention_gram";
+    const bool f = dtype == DT_F32 ? gram_fast<float>(qkv, dim, w)
+                                   : dtype == DT_F16 ? gram_fast<_Float16>(qkv, dim, w) : gram_fast<__bf16>(qkv, dim, w);
+    return std::string("k_attention_gram<") + ty[dtype] + (f ? ", true>" : ", false>");
+}
+
 hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads, int h, int w,
                                  float* partial, hipStream_t s) {
     const int c = heads > 0 ? dim / heads : 0;
@@ -739,7 +762,22 @@ hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads,
     if (nchunk == 0 || N == 0) return hipSuccess;
     if (!attention_gram_fits(dtype, dim)) return hipErrorInvalidValue;
     const size_t lds = (size_t)(dtype == DT_F32 ? 4 * GRAM_SUB<float> : 2 * GRAM_SUB<__bf16>) * (2 * dim + GRAM_PAD);
-    ZJAI_DISPATCH(dtype, k_attention_gram, <<<dim3(nchunk, N), 256, lds, s>>>(qkv, dim, heads, h * w, w, partial))
+    const dim3 g(nchunk, N);
+    switch (dtype) {
+        case DT_F32:
+            if (gram_fast<float>(qkv, dim, w)) k_attention_gram<float, true><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
+            else k_attention_gram<float, false><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
+            break;
+        case DT_F16:
+            if (gram_fast<_Float16>(qkv, dim, w)) k_attention_gram<_Float16, true><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
+            else k_attention_gram<_Float16, false><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
+            break;
+        case DT_BF16:
+            if (gram_fast<__bf16>(qkv, dim, w)) k_attention_gram<__bf16, true><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
+            else k_attention_gram<__bf16, false><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
+            break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
