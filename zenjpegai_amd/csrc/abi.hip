@@ -514,7 +514,7 @@ extern "C" int32_t zjai_channel_attention_noalloc(zjai_ctx* ctx, const void* qkv
         }
         const double n = (double)h * w, total = (double)heads * (c * c + 2 * c);
         {
-            LaunchScope sc(C, attention_gram_name(vq, precision, dim, w), 2.0 * total * n, es * 2.0 * dim * n + 4.0 * nchunk * total);
+            LaunchScope sc(C, attention_gram_name(vq, precision, dim, heads, w), 2.0 * total * n, es * 2.0 * dim * n + 4.0 * nchunk * total);
             ZJAI_HIP(launch_attention_gram(vq, precision, 1, dim, heads, h, w, partial, C.stream));
         }
         {

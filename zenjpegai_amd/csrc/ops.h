@@ -118,8 +118,9 @@ int attention_gram_chunks(int h, int w);
 // 160 KB of a CU for this dim: callers check it before their first launch.
 bool attention_gram_fits(int dtype, int dim);
 // Profile name of the Gram kernel launch_attention_gram runs for these operands, as the kernel
-// symbol reads (k_attention_gram<__bf16, true>: the fixed-offset staging form).
-std::string attention_gram_name(const View& qkv, int dtype, int dim, int w);
+// symbol reads (k_attention_gram<__bf16, true, 2>: the fixed-offset staging form, two 16-channel
+// blocks per head).
+std::string attention_gram_name(const View& qkv, int dtype, int dim, int heads, int w);
 hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads, int h, int w,
                                  float* partial, hipStream_t s);
 hipError_t launch_attention_softmax(const float* partial, int N, int nchunk, int dim, int heads,

@@ -385,13 +385,13 @@ static bool gram_fast(const View& qkv, int dim, int w) {
     return upp > 0 && GRAM_SUB<T> * upp <= GRAM_UNR * 256 && qkv.row == (long long)w * qkv.cs && 256 % upp == 0;
 }
 
-template <typename T, bool FAST>
+template <typename T, bool FAST, int NB>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 k_attention_gram(View qkv, int dim, int heads, int n, int w, float* partial) {
     extern __shared__ __align__(16) unsigned char s_raw[];
     T* s_qk = reinterpret_cast<T*>(s_raw);  // [GRAM_SUB][2 dim + GRAM_PAD]
     constexpr int VEC = 16 / (int)sizeof(T), SUB = GRAM_SUB<T>;
-    const int c = dim / heads, nb = (c + 15) / 16, E = c * c + 2 * c;
+    const int c = dim / heads, E = c * c + 2 * c;  // NB = (c + 15) / 16 head blocks
     const int ld = 2 * dim + GRAM_PAD, upp = 2 * dim / VEC;  // LDS row; 16-byte units per position
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m = lane & 15, kq = lane >> 4;
@@ -459,25 +459,27 @@ k_attention_gram(View qkv, int dim, int heads, int n, int w, float* partial) {
             if constexpr (FAST)
                 if (ps + SUB < p1) fetch(ps + SUB);
             if (hd >= heads) continue;  // uniform per wave
+            // Every LDS read is unconditional (row clamped into the sub-chunk; the element of a
+            // position past pe or a channel past the head is then replaced by 0), so a group's
+            // reads issue together instead of each waiting in its own branch.
             for (int p = ps; p < pe; p += 4) {
-                float aq[2], ak[2];
-                const T* r = s_qk + (p - ps + kq) * ld + hd * c + m;
+                float aq[NB], ak[NB];
+                const T* r = s_qk + min(p - ps + kq, SUB - 1) * ld + hd * c + m;
                 const bool ok = p + kq < pe;
 #pragma unroll
-                for (int bb = 0; bb < 2; ++bb) {
+                for (int bb = 0; bb < NB; ++bb) {
                     const bool in = ok && bb * 16 + m < c;
-                    aq[bb] = in ? (float)r[bb * 16] : 0.0f;
-                    ak[bb] = in ? (float)r[dim + bb * 16] : 0.0f;
+                    const float vq = (float)r[bb * 16], vk = (float)r[dim + bb * 16];
+                    aq[bb] = in ? vq : 0.0f;
+                    ak[bb] = in ? vk : 0.0f;
                     sq[bb] = fmaf(aq[bb], aq[bb], sq[bb]);
                     sk[bb] = fmaf(ak[bb], ak[bb], sk[bb]);
                 }
 #pragma unroll
-                for (int bi = 0; bi < 2; ++bi) {
-                    if (bi >= nb) continue;
+                for (int bi = 0; bi < NB; ++bi)
 #pragma unroll
-                    for (int bj = 0; bj < 2; ++bj)
-                        if (bj < nb) g[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[bi], ak[bj], g[bi][bj], 0, 0, 0);
-                }
+                    for (int bj = 0; bj < NB; ++bj)
+                        g[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[bi], ak[bj], g[bi][bj], 0, 0, 0);
             }
         }
         if (hd >= heads) continue;
@@ -492,14 +494,14 @@ k_attention_gram(View qkv, int dim, int heads, int n, int w, float* partial) {
         float* out = partial + (((long long)b * nchunk + blockIdx.x) * heads + hd) * E;
 #pragma unroll
         for (int bi = 0; bi < 2; ++bi) {
-            if (bi >= nb) continue;
+            if (bi >= NB) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = 4 * kq + i;
                 if (bi * 16 + r >= c) continue;
 #pragma unroll
                 for (int bj = 0; bj < 2; ++bj)
-                    if (bj < nb && bj * 16 + m < c) out[(bi * 16 + r) * c + bj * 16 + m] = g[bi][bj][i];
+                    if (bj < NB && bj * 16 + m < c) out[(bi * 16 + r) * c + bj * 16 + m] = g[bi][bj][i];
             }
             if (kq == 0 && bi * 16 + m < c) {
                 out[c * c + bi * 16 + m] = sq[bi];
@@ -743,12 +745,25 @@ bool attention_gram_fits(int dtype, int dim) {
     return lds <= 160 * 1024;
 }
 
-std::string attention_gram_name(const View& qkv, int dtype, int dim, int w) {
+template <typename T>
+static void gram_go(dim3 g, size_t lds, hipStream_t s, bool fast, int nb, View qkv, int dim, int heads, int n,
+                    int w, float* partial) {
+    if (fast) {
+        if (nb == 1) k_attention_gram<T, true, 1><<<g, 256, lds, s>>>(qkv, dim, heads, n, w, partial);
+        else k_attention_gram<T, true, 2><<<g, 256, lds, s>>>(qkv, dim, heads, n, w, partial);
+    } else {
+        if (nb == 1) k_attention_gram<T, false, 1><<<g, 256, lds, s>>>(qkv, dim, heads, n, w, partial);
+        else k_attention_gram<T, false, 2><<<g, 256, lds, s>>>(qkv, dim, heads, n, w, partial);
+    }
+}
+
+std::string attention_gram_name(const View& qkv, int dtype, int dim, int heads, int w) {
     static const char* ty[] = {"float", "_Float16", "__bf16"};
-    if (dtype < DT_F32 || dtype > DT_BF16) return "k_attention_gram";
+    if (dtype < DT_F32 || dtype > DT_BF16 || heads <= 0) return "k_attention_gram";
     const bool f = dtype == DT_F32 ? gram_fast<float>(qkv, dim, w)
                                    : dtype == DT_F16 ? gram_fast<_Float16>(qkv, dim, w) : gram_fast<__bf16>(qkv, dim, w);
-    return std::string("k_attention_gram<") + ty[dtype] + (f ? ", true>" : ", false>");
+    return std::string("k_attention_gram<") + ty[dtype] + (f ? ", true, " : ", false, ") +
+           (dim / heads > 16 ? "2>" : "1>");
 }
 
 hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads, int h, int w,
@@ -763,19 +778,11 @@ hipError_t launch_attention_gram(View qkv, int dtype, int N, int dim, int heads,
     if (!attention_gram_fits(dtype, dim)) return hipErrorInvalidValue;
     const size_t lds = (size_t)(dtype == DT_F32 ? 4 * GRAM_SUB<float> : 2 * GRAM_SUB<__bf16>) * (2 * dim + GRAM_PAD);
     const dim3 g(nchunk, N);
+    const int nb = (c + 15) / 16;
     switch (dtype) {
-        case DT_F32:
-            if (gram_fast<float>(qkv, dim, w)) k_attention_gram<float, true><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
-            else k_attention_gram<float, false><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
-            break;
-        case DT_F16:
-            if (gram_fast<_Float16>(qkv, dim, w)) k_attention_gram<_Float16, true><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
-            else k_attention_gram<_Float16, false><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
-            break;
-        case DT_BF16:
-            if (gram_fast<__bf16>(qkv, dim, w)) k_attention_gram<__bf16, true><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
-            else k_attention_gram<__bf16, false><<<g, 256, lds, s>>>(qkv, dim, heads, h * w, w, partial);
-            break;
+        case DT_F32: gram_go<float>(g, lds, s, gram_fast<float>(qkv, dim, w), nb, qkv, dim, heads, h * w, w, partial); break;
+        case DT_F16: gram_go<_Float16>(g, lds, s, gram_fast<_Float16>(qkv, dim, w), nb, qkv, dim, heads, h * w, w, partial); break;
+        case DT_BF16: gram_go<__bf16>(g, lds, s, gram_fast<__bf16>(qkv, dim, w), nb, qkv, dim, heads, h * w, w, partial); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

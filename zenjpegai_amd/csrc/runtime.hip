@@ -778,7 +778,7 @@ std::shared_ptr<void> attention_fold(Context& ctx, const TensorP& qkv, int heads
     if (proj.nblk_g * 16 != dim || proj.nchunks * CK != dim)  // padded rows / columns stay zero
         ZJAI_HIP(launch_zero(wfold, proj.wpk_bytes * N, ctx.stream));
     {
-        LaunchScope sc(ctx, attention_gram_name(qkv->v, qkv->dtype, dim, qkv->w), 2.0 * N * total * n, es * N * 2 * dim * n + 4.0 * N * nchunk * total);
+        LaunchScope sc(ctx, attention_gram_name(qkv->v, qkv->dtype, dim, heads, qkv->w), 2.0 * N * total * n, es * N * 2 * dim * n + 4.0 * N * nchunk * total);
         ZJAI_HIP(launch_attention_gram(qkv->v, qkv->dtype, N, dim, heads, qkv->h, qkv->w, partial, ctx.stream));
     }
     {
