@@ -530,13 +530,17 @@ __global__ void __launch_bounds__(256) k_attention_softmax(const float* partial,
     __shared__ float s_e[64];
     const int row = blockIdx.x, b = blockIdx.y, c = dim / heads, hd = row / c, i = row - hd * c;
     const int E = c * c + 2 * c, tid = threadIdx.x, sl = tid >> 5, j = tid & 31;
+    // Every lane of a row also sums |q_i|^2 (the same address across the row, so the loads of an
+    // iteration carry no branch and successive iterations' loads overlap); lane 0's sum is used.
     double sqk = 0.0, skk = 0.0, sqq = 0.0;
     if (j < c) {
+#pragma unroll 4
         for (int k = sl; k < nchunk; k += ATT_SL) {
             const float* pb = partial + (((long long)b * nchunk + k) * heads + hd) * E;
-            sqk += (double)pb[i * c + j];
-            skk += (double)pb[c * c + c + j];
-            if (j == 0) sqq += (double)pb[c * c + i];
+            const float vqk = pb[i * c + j], vkk = pb[c * c + c + j], vqq = pb[c * c + i];
+            sqk += (double)vqk;
+            skk += (double)vkk;
+            sqq += (double)vqq;
         }
     }
     s_red[sl][0][j] = sqk;
@@ -589,11 +593,22 @@ __global__ void k_attention_fold(const float* proj, const float* attn, int dim, 
     if (e >= dim * dim) return;
     const int c = dim / heads, o = e / dim, col = e - o * dim, hd = col / c, j = col - hd * c;
     const float* at_b = attn + (long long)b * dim * c;
-    double s = 0.0;
-    for (int i = 0; i < c; ++i) {
-        const float pw = proj ? proj[o * dim + hd * c + i] : (o == hd * c + i ? 1.0f : 0.0f);
-        s += (double)pw * (double)at_b[(hd * c + i) * c + j];
+    // All c (<= 32) operand pairs are loaded before the first product (indices clamped to the
+    // head), so the loads overlap instead of each waiting for the previous one's sum.
+    float pw[32], av[32];
+    if (proj) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) pw[i] = proj[o * dim + hd * c + min(i, c - 1)];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) pw[i] = o == hd * c + min(i, c - 1) ? 1.0f : 0.0f;
     }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) av[i] = at_b[(hd * c + min(i, c - 1)) * c + j];
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+        if (i < c) s += (double)pw[i] * (double)av[i];
     const int ch = col / CK, kk = col - ch * CK;
     wpk[(long long)b * w_bstride + (((long long)ch * nblk + o / 16) * 16 + o % 16) * CK + kk] = from_f32<T>((float)s);
 }
@@ -798,6 +813,7 @@ hipError_t launch_attention_softmax(const float* partial, int N, int nchunk, int
 hipError_t launch_attention_fold(const float* proj, const float* attn, int N, int dim, int heads,
                                  int dtype, int nblk, void* wpk, long long w_bstride,
                                  hipStream_t s) {
+    if (heads <= 0 || dim % heads || dim / heads > 32) return hipErrorInvalidValue;  // k_attention_fold's c <= 32
     const int CK = dtype == DT_F32 ? 16 : 32;
     const dim3 g((dim * dim + 255) / 256, N);
     switch (dtype) {
