@@ -38,8 +38,13 @@ template <typename T>
 __global__ void __launch_bounds__(256) k_planar_to_nhwc(const float* src, int C, int LH, int LW, Windows win,
                                                         int N, int h, int w, View dst) {
     __shared__ f32x4 s_t[PT_C / 4 * (PT_X + 1)];
-    const int ntx = (w + PT_X - 1) / PT_X;
-    const int bx = (int)blockIdx.x % ntx, by = ((int)blockIdx.x / ntx) % h, b = (int)blockIdx.x / (ntx * h);
+    // XCD-aware order: workgroup ids are dealt round-robin to the 8 XCDs (each with its own L2),
+    // so consecutive logical runs -- which share 128-byte lines of every plane row -- are given
+    // to one XCD (the grid is padded to a multiple of 8).
+    const int ntx = (w + PT_X - 1) / PT_X, nrun = ntx * h * N;
+    const int lid = ((int)blockIdx.x & 7) * ((int)gridDim.x >> 3) + ((int)blockIdx.x >> 3);
+    if (lid >= nrun) return;
+    const int bx = lid % ntx, by = (lid / ntx) % h, b = lid / (ntx * h);
     const int x0 = bx * PT_X, nx = min(PT_X, w - x0), tid = threadIdx.x;
     const float* row = src + (long long)(win.y0[b] + by) * LW + win.x0[b] + x0;
     const long long plane = (long long)LH * LW;
@@ -688,8 +693,9 @@ hipError_t launch_planar_to_nhwc(const float* src, int C, int LH, int LW, const 
         if (win.y0[b] < 0 || win.x0[b] < 0 || win.y0[b] + h > LH || win.x0[b] + w > LW) return hipErrorInvalidValue;
     const long long n = (long long)N * h * ((w + PT_X - 1) / PT_X);
     if (n == 0 || C == 0) return hipSuccess;
-    if (n > 0x7fffffffLL) return hipErrorInvalidValue;
-    ZJAI_DISPATCH(dtype, k_planar_to_nhwc, <<<dim3((unsigned)n), 256, 0, s>>>(src, C, LH, LW, win, N, h, w, dst))
+    if (n > 0x7ffffff0LL) return hipErrorInvalidValue;
+    const unsigned nb = (unsigned)((n + 7) / 8 * 8);
+    ZJAI_DISPATCH(dtype, k_planar_to_nhwc, <<<dim3(nb), 256, 0, s>>>(src, C, LH, LW, win, N, h, w, dst))
     return hipGetLastError();
 }
 
