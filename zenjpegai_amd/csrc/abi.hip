@@ -1037,7 +1037,10 @@ static void issue_picture(Context& root, zjai_picture* pic, int nl, hipEvent_t f
             py.dst_y0[b] = t.core_y;
             py.dst_x0[b] = t.core_x;
         }
-        TensorP by = c.alloc(N, 160, t0.latent_h, t0.latent_w, dt);
+        // With a chroma net both latents go into one 256-channel block (luma channels 0..159,
+        // chroma 160..255): the chroma net's input concatenation is then that block as it stands.
+        TensorP cat = pic->net_uv ? c.alloc(N, 256, t0.latent_h, t0.latent_w, dt) : nullptr;
+        TensorP by = cat ? channel_view(cat, 0, 160) : c.alloc(N, 160, t0.latent_h, t0.latent_w, dt);
         {
             LaunchScope sc(c, kname("k_planar_to_nhwc", dt), 0.0, (4.0 + dtype_size(dt)) * N * 160 * t0.latent_h * t0.latent_w);
             ZJAI_HIP(launch_planar_to_nhwc(pic->y_hat, 160, pic->lh, pic->lw, win, N, t0.latent_h, t0.latent_w,
@@ -1045,7 +1048,7 @@ static void issue_picture(Context& root, zjai_picture* pic, int nl, hipEvent_t f
         }
         primary_forward(c, *pic->net_y, by, t0.image_h, t0.image_w, py);
         if (pic->net_uv) {
-            TensorP buv = c.alloc(N, 96, t0.latent_h, t0.latent_w, dt);
+            TensorP buv = channel_view(cat, 160, 96);
             {
                 LaunchScope sc(c, kname("k_planar_to_nhwc", dt), 0.0, (4.0 + dtype_size(dt)) * N * 96 * t0.latent_h * t0.latent_w);
                 ZJAI_HIP(launch_planar_to_nhwc(pic->uv_hat, 96, pic->lh, pic->lw, win, N, t0.latent_h,

@@ -646,14 +646,27 @@ void secondary_forward(Context& ctx, const Net& net, const TensorP& y_luma, cons
     Fwd f{ctx, net};
     const int dt = net.dtype, N = y_luma->n;
     const double es = dtype_size(dt);
-    TensorP cat = ctx.alloc(N, 256, lh, lw, dt);
-    {
-        LaunchScope sc(ctx, kname("k_copy", dt), 0.0, 2.0 * es * N * 160 * lh * lw);
-        ZJAI_HIP(launch_copy(y_luma->v, cat->v, dt, N, 160, lh, lw, ctx.stream));
-    }
-    {
-        LaunchScope sc(ctx, kname("k_copy", dt), 0.0, 2.0 * es * N * 96 * lh * lw);
-        ZJAI_HIP(launch_copy(y_chroma->v, channel_view(cat, 160, 96)->v, dt, N, 96, lh, lw, ctx.stream));
+    // cat(luma, chroma): when the two latents already are channels 0..159 and 160..255 of one
+    // 256-channel block of this shape (as zjai_picture_run lays them out), that block is the
+    // concatenation and nothing is copied.
+    const bool joined = y_luma->base == y_chroma->base && y_luma->v.p == y_chroma->v.p &&
+                        y_luma->v.c_off == 0 && y_chroma->v.c_off == 160 && y_luma->v.cs == 256 &&
+                        y_chroma->v.cs == 256 && y_luma->v.row == y_chroma->v.row &&
+                        y_luma->v.bstride == y_chroma->v.bstride && y_luma->h == lh && y_luma->w == lw;
+    TensorP cat;
+    if (joined) {
+        cat = std::make_shared<Tensor>(*y_luma);
+        cat->c = 256;
+    } else {
+        cat = ctx.alloc(N, 256, lh, lw, dt);
+        {
+            LaunchScope sc(ctx, kname("k_copy", dt), 0.0, 2.0 * es * N * 160 * lh * lw);
+            ZJAI_HIP(launch_copy(y_luma->v, cat->v, dt, N, 160, lh, lw, ctx.stream));
+        }
+        {
+            LaunchScope sc(ctx, kname("k_copy", dt), 0.0, 2.0 * es * N * 96 * lh * lw);
+            ZJAI_HIP(launch_copy(y_chroma->v, channel_view(cat, 160, 96)->v, dt, N, 96, lh, lw, ctx.stream));
+        }
     }
     TensorP x = ctx.alloc(N, 144, lh, lw, dt);
     f.conv("first_stage.conv1", cat, Epilogue{}, channel_view(x, 0, 48));
